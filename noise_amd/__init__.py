@@ -1,0 +1,7 @@
+"""noise_amd: the MI355X (gfx950) population-forward hot path of pculaf/noise.
+
+Hand-written HIP kernels behind the C ABI of include/noise_amd.h (libnoise_amd.so), with Python
+mirrors of the reference's call sites: utils/model.py `attention`, train/val/eggroll.py `lowrank`,
+`lowrank_embed`, `population_loss` and `Eggroll` noise bookkeeping, train/val/run.py `head_loss`.
+"""
+from . import _lib  # noqa: F401

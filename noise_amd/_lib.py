@@ -1,0 +1,60 @@
+"""Loader of libnoise_amd.so, the C ABI declared in include/noise_amd.h.
+
+There is no fallback: if the library is missing or does not load, every op raises.
+"""
+import ctypes
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name('libnoise_amd.so')
+
+_p, _i64, _u64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
+
+# name -> argtypes (every entry point returns int status unless listed in _RESTYPES)
+SIGNATURES = {
+    'noise_abi_version': [],
+    'noise_last_error': [],
+    'noise_draw_layout': [_i32, _i64, _p, _p],
+    'noise_normal_fill': [_p, _i64, _i64, _u64, _u64, _i64, _f32, _f32, _p],
+    'noise_randint': [_p, _i64, _u64, _u64, _i64, _u64, _i64, _p],
+    'noise_gather_slices': [_p, _i64, _i64, _p, _p, _i64, _u64, _u64, _i64, _p],
+}
+_RESTYPES = {'noise_last_error': ctypes.c_char_p}
+
+_lib = None
+
+
+def lib():
+    """The loaded library (raises RuntimeError when it is not built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f'{LIB_PATH} is not built: run noise_amd.build.build() (hipcc, gfx950)')
+        handle = ctypes.CDLL(str(LIB_PATH))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = argtypes
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
+        _lib = handle
+    return _lib
+
+
+def call(name, *args):
+    """Call entry point `name`; raise RuntimeError with the library's message on a non-zero status."""
+    status = getattr(lib(), name)(*args)
+    if status != 0:
+        msg = lib().noise_last_error().decode(errors='replace')
+        kind = 'invalid argument' if status < 0 else f'HIP error {status}'
+        raise RuntimeError(f'{name}: {kind}: {msg}')
+    return status
+
+
+def stream_ptr(device=None):
+    """hipStream_t of torch's current stream on `device`, as an integer for ctypes."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t):
+    """Device address of a tensor (None -> NULL)."""
+    return None if t is None else t.data_ptr()

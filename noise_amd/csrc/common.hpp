@@ -1,0 +1,57 @@
+// Shared host/device helpers of libnoise_amd: status codes, the per-thread error message, bf16
+// conversions and launch checks. Every extern "C" entry point validates its arguments on the host and
+// returns a status (0 ok, <0 invalid argument, >0 hipError_t of a failed launch) instead of crashing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/noise_amd.h"
+
+namespace noise {
+
+// The message of the last failing call on this host thread (read back through noise_last_error()).
+void set_error(const char *fmt, ...);
+void clear_error();
+
+#define NOISE_CHECK_ARG(cond, ...)                 \
+    do {                                           \
+        if (!(cond)) {                             \
+            ::noise::set_error(__VA_ARGS__);       \
+            return NOISE_EINVAL;                   \
+        }                                          \
+    } while (0)
+
+// Status of the launch just issued (hipGetLastError also clears the sticky launch error).
+inline int launch_status(const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error("%s: launch failed: %s", what, hipGetErrorString(e));
+        return (int)e;
+    }
+    return NOISE_OK;
+}
+
+inline bool aligned(const void *p, size_t a) { return ((uintptr_t)p % a) == 0; }
+
+// bf16 <-> fp32 with round-to-nearest-even (the rounding torch's .bfloat16() uses). NaN stays NaN.
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float f) {
+    uint32_t u;
+    __builtin_memcpy(&u, &f, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+    uint32_t rounding = 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)((u + rounding) >> 16);
+}
+
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
+    uint32_t u = ((uint32_t)h) << 16;
+    float f;
+    __builtin_memcpy(&f, &u, 4);
+    return f;
+}
+
+__host__ __device__ inline float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
+
+}  // namespace noise

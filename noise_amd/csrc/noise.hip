@@ -1,0 +1,167 @@
+// Noise kernels: slices of torch-ROCm's seeded device draws, regenerated from the Philox counter.
+//
+// Replaces, bit for bit, the reference's noise producers:
+//   Eggroll.__init__  buffer = torch.randn(2**28, generator=cuda seed)           eggroll.py:114
+//   Eggroll.offsets   torch.randint(0, NOISE - sum(p.shape), (P,), generator=g)  eggroll.py:117-120
+//   Eggroll.noise     buffer[offsets[name][directions, None] + arange(width)]    eggroll.py:122-128
+//   DUST.noise / signs / orthogonal_noise offsets                                run.py:215-233
+// The draw layout is torch's grid-stride distribution kernel (torch: ATen/native/hip/
+// DistributionTemplates.h:52-89) and rocRAND's Philox4x32-10 + Box-Muller (rocrand_philox4x32_10.h,
+// rocrand_normal.h:53-68); philox.hpp states the closed form.
+#include "common.hpp"
+#include "philox.hpp"
+
+namespace noise {
+namespace {
+
+constexpr int kBlock = 256;
+
+// Element-wise: out[i] = element first+i. One Philox block per element.
+__global__ __launch_bounds__(kBlock) void normal_elementwise_kernel(float *__restrict__ out, int64_t n,
+                                                                    int64_t first, DrawLayout d, float mean,
+                                                                    float stdv) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        out[i] = draw_normal(d, (uint64_t)(first + i), mean, stdv);
+    }
+}
+
+// Block-wise, for ranges covering whole Philox planes: work item (k, t) computes block k of thread t
+// once and writes its four lanes L = 4Sk + qS + t that fall in [first, first + n). Writes are
+// coalesced along t. Covers k in [k0, k1].
+__global__ __launch_bounds__(kBlock) void normal_blockwise_kernel(float *__restrict__ out, int64_t n,
+                                                                  int64_t first, DrawLayout d, float mean,
+                                                                  float stdv, int64_t k0, int64_t items) {
+    const int64_t S = (int64_t)d.threads;
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t w = (int64_t)blockIdx.x * kBlock + threadIdx.x; w < items; w += stride) {
+        int64_t k = k0 + w / S;
+        int64_t t = w - (w / S) * S;
+        uint64_t c = d.offset / 4 + (uint64_t)k;
+        Philox4 b = philox4x32_10((uint32_t)c, (uint32_t)(c >> 32), (uint32_t)t, (uint32_t)((uint64_t)t >> 32),
+                                  (uint32_t)d.seed, (uint32_t)(d.seed >> 32));
+        int64_t base = 4 * S * k + t;
+        float v0 = box_muller_one(b.x, b.y, false) * stdv + mean;
+        float v1 = box_muller_one(b.x, b.y, true) * stdv + mean;
+        float v2 = box_muller_one(b.z, b.w, false) * stdv + mean;
+        float v3 = box_muller_one(b.z, b.w, true) * stdv + mean;
+        int64_t L0 = base - first;
+        if (L0 >= 0 && L0 < n) out[L0] = v0;
+        if (L0 + S >= 0 && L0 + S < n) out[L0 + S] = v1;
+        if (L0 + 2 * S >= 0 && L0 + 2 * S < n) out[L0 + 2 * S] = v2;
+        if (L0 + 3 * S >= 0 && L0 + 3 * S < n) out[L0 + 3 * S] = v3;
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void randint_kernel(int64_t *__restrict__ out, int64_t n, DrawLayout d,
+                                                         uint64_t range, int64_t base) {
+    int64_t stride = (int64_t)gridDim.x * kBlock;
+    for (int64_t i = (int64_t)blockIdx.x * kBlock + threadIdx.x; i < n; i += stride) {
+        uint32_t u = draw_u32(d, (uint64_t)i);
+        out[i] = (int64_t)(u % range) + base;
+    }
+}
+
+// grid = (ceil(width / 256), nrows)
+__global__ __launch_bounds__(kBlock) void gather_slices_kernel(float *__restrict__ out, int64_t width,
+                                                               const int64_t *__restrict__ offsets,
+                                                               const int64_t *__restrict__ rows, int64_t numel,
+                                                               DrawLayout d) {
+    int64_t r = blockIdx.y;
+    int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (j >= width) return;
+    int64_t src = rows ? rows[r] : r;
+    int64_t L = offsets[src] + j;
+    float v = (L >= 0 && L < numel) ? draw_normal(d, (uint64_t)L, 0.0f, 1.0f) : __builtin_nanf("");
+    out[r * width + j] = v;
+}
+
+int grid_for(int64_t work) {
+    int64_t g = (work + kBlock - 1) / kBlock;
+    if (g > 65536) g = 65536;
+    if (g < 1) g = 1;
+    return (int)g;
+}
+
+}  // namespace
+}  // namespace noise
+
+using namespace noise;
+
+extern "C" int noise_draw_layout(int device, int64_t numel, int64_t *threads_out, int64_t *offset_increment_out) {
+    clear_error();
+    NOISE_CHECK_ARG(numel > 0, "noise_draw_layout: numel must be positive, got %lld", (long long)numel);
+    NOISE_CHECK_ARG(threads_out != nullptr, "noise_draw_layout: threads_out is NULL");
+    hipDeviceProp_t prop;
+    hipError_t e = hipGetDeviceProperties(&prop, device);
+    if (e != hipSuccess) {
+        set_error("noise_draw_layout: hipGetDeviceProperties(%d): %s", device, hipGetErrorString(e));
+        return (int)e;
+    }
+    int64_t blocks = (numel + 255) / 256;
+    int64_t cap = (int64_t)prop.multiProcessorCount * (prop.maxThreadsPerMultiProcessor / 256);
+    if (blocks > cap) blocks = cap;
+    int64_t S = blocks * 256;
+    *threads_out = S;
+    if (offset_increment_out) *offset_increment_out = ((numel - 1) / (S * 4) + 1) * 4;
+    return NOISE_OK;
+}
+
+extern "C" int noise_normal_fill(float *out, int64_t n, int64_t first, uint64_t seed, uint64_t offset,
+                                 int64_t threads, float mean, float stdv, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(n >= 0 && first >= 0, "noise_normal_fill: n and first must be >= 0");
+    NOISE_CHECK_ARG(threads > 0 && threads % 256 == 0, "noise_normal_fill: threads must be a positive multiple of 256, got %lld",
+                    (long long)threads);
+    NOISE_CHECK_ARG(offset % 4 == 0, "noise_normal_fill: generator offset must be a multiple of 4");
+    if (n == 0) return NOISE_OK;
+    NOISE_CHECK_ARG(out != nullptr, "noise_normal_fill: out is NULL");
+    NOISE_CHECK_ARG(aligned(out, 4), "noise_normal_fill: out must be 4-byte aligned");
+    DrawLayout d{seed, offset, (uint64_t)threads};
+    hipStream_t s = (hipStream_t)stream;
+    if (n >= 4 * threads) {
+        int64_t k0 = first / (4 * threads);
+        int64_t k1 = (first + n - 1) / (4 * threads);
+        int64_t items = (k1 - k0 + 1) * threads;
+        hipLaunchKernelGGL(normal_blockwise_kernel, dim3(grid_for(items)), dim3(kBlock), 0, s, out, n, first, d,
+                           mean, stdv, k0, items);
+    } else {
+        hipLaunchKernelGGL(normal_elementwise_kernel, dim3(grid_for(n)), dim3(kBlock), 0, s, out, n, first, d,
+                           mean, stdv);
+    }
+    return launch_status("noise_normal_fill");
+}
+
+extern "C" int noise_randint(int64_t *out, int64_t n, uint64_t seed, uint64_t offset, int64_t threads,
+                             uint64_t range, int64_t base, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(n >= 0, "noise_randint: n must be >= 0");
+    NOISE_CHECK_ARG(threads > 0 && threads % 256 == 0, "noise_randint: threads must be a positive multiple of 256");
+    NOISE_CHECK_ARG(offset % 4 == 0, "noise_randint: generator offset must be a multiple of 4");
+    NOISE_CHECK_ARG(range >= 1 && range < (1ull << 28),
+                    "noise_randint: range must be in [1, 2^28) (torch's 32-bit path), got %llu",
+                    (unsigned long long)range);
+    if (n == 0) return NOISE_OK;
+    NOISE_CHECK_ARG(out != nullptr && aligned(out, 8), "noise_randint: out must be a non-NULL 8-byte aligned pointer");
+    DrawLayout d{seed, offset, (uint64_t)threads};
+    hipLaunchKernelGGL(randint_kernel, dim3(grid_for(n)), dim3(kBlock), 0, (hipStream_t)stream, out, n, d, range, base);
+    return launch_status("noise_randint");
+}
+
+extern "C" int noise_gather_slices(float *out, int64_t nrows, int64_t width, const int64_t *offsets,
+                                   const int64_t *rows, int64_t numel, uint64_t seed, uint64_t offset,
+                                   int64_t threads, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(nrows >= 0 && width >= 0, "noise_gather_slices: nrows and width must be >= 0");
+    NOISE_CHECK_ARG(nrows <= 65535, "noise_gather_slices: at most 65535 rows per call, got %lld", (long long)nrows);
+    NOISE_CHECK_ARG(threads > 0 && threads % 256 == 0, "noise_gather_slices: threads must be a positive multiple of 256");
+    NOISE_CHECK_ARG(offset % 4 == 0, "noise_gather_slices: generator offset must be a multiple of 4");
+    NOISE_CHECK_ARG(numel > 0, "noise_gather_slices: numel must be positive");
+    if (nrows == 0 || width == 0) return NOISE_OK;
+    NOISE_CHECK_ARG(out != nullptr && offsets != nullptr, "noise_gather_slices: out and offsets must be non-NULL");
+    DrawLayout d{seed, offset, (uint64_t)threads};
+    dim3 grid((unsigned)((width + kBlock - 1) / kBlock), (unsigned)nrows);
+    hipLaunchKernelGGL(gather_slices_kernel, grid, dim3(kBlock), 0, (hipStream_t)stream, out, width, offsets, rows,
+                       numel, d);
+    return launch_status("noise_gather_slices");
+}
