@@ -65,6 +65,27 @@ int noise_randint(int64_t *out, int64_t n, uint64_t seed, uint64_t offset, int64
 int noise_gather_slices(float *out, int64_t nrows, int64_t width, const int64_t *offsets, const int64_t *rows,
                         int64_t numel, uint64_t seed, uint64_t offset, int64_t threads, noise_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * Attention
+ * ---------------------------------------------------------------------------------------------- */
+
+/* Causal attention with a left window: query s attends to keys s - window .. s (window >= seq - 1 is
+ * plain causal), softmax(q k^T * scale) v, bf16 in and out, fp32 accumulation. Replaces utils/model.py:24-31
+ * `attention(q, k, v, window)` (flex_attention with the block mask q >= k & q - k <= window,
+ * model.py:17-21; scale 1/sqrt(head_dim), torch: nn/attention/flex_attention.py:1543-1544).
+ * q, k, o: element (b, t, h, d) at b*s_b + h*s_h + t*s_t + d (the reference's [B, T, H, D] and its
+ * transposes are all expressible). v: the same with vs_x = token stride when v_transposed == 0, or
+ * element (b, t, h, d) at b*vs_b + h*vs_h + d*vs_x + t when v_transposed == 1. head_dim must be 64.
+ * Optional fused output (dot_out != NULL): dot_out[(b*seq + t)*heads + h] = sum_d o[b,t,h,d] *
+ * dot_vec[(b / dot_div)*dot_vec_stride + h*64 + d], with o the bf16 output values; this is the
+ * per-head part of the next perturbed linear's x.b (eggroll.py:58), NULL to skip. */
+int noise_attention_fwd(const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
+                        int64_t seq, int64_t head_dim, int64_t qs_b, int64_t qs_h, int64_t qs_t, int64_t ks_b,
+                        int64_t ks_h, int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_x, int v_transposed,
+                        int64_t os_b, int64_t os_h, int64_t os_t, int64_t window, float scale,
+                        const float *dot_vec, int64_t dot_vec_stride, int64_t dot_div, float *dot_out,
+                        noise_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

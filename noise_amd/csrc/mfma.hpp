@@ -1,0 +1,54 @@
+// CDNA4 (gfx950) MFMA operand types and small device helpers shared by the kernels.
+//
+// v_mfma_f32_32x32x16_bf16 lane layout (64 lanes, l = lane, h = l / 32):
+//   A (32 x 16): lane l holds A[l % 32][8h .. 8h+7]
+//   B (16 x 32): lane l holds B[8h .. 8h+7][l % 32]
+//   D (32 x 32): lane l, register r holds D[8(r/4) + 4h + (r%4)][l % 32]
+// Any permutation of the contraction index applied to A and B alike leaves D unchanged, which the
+// attention kernel uses to feed softmax registers straight into the second product.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace noise {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 load_bf16x8(const __bf16 *p) { return *reinterpret_cast<const bf16x8 *>(p); }
+
+__device__ __forceinline__ bf16x4 load_bf16x4(const __bf16 *p) { return *reinterpret_cast<const bf16x4 *>(p); }
+
+__device__ __forceinline__ void store_bf16x8(__bf16 *p, bf16x8 v) { *reinterpret_cast<bf16x8 *>(p) = v; }
+
+__device__ __forceinline__ void store_bf16x4(__bf16 *p, bf16x4 v) { *reinterpret_cast<bf16x4 *>(p) = v; }
+
+__device__ __forceinline__ bf16x8 cat(bf16x4 lo, bf16x4 hi) {
+    return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value of lane (l ^ 32): the other half of a 32x32 MFMA column.
+__device__ __forceinline__ float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
+
+__device__ __forceinline__ bf16x8 zero_bf16x8() {
+    bf16x8 z;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) z[i] = (__bf16)0.0f;
+    return z;
+}
+
+}  // namespace noise

@@ -1,0 +1,191 @@
+"""ORACLE (test infrastructure only): fp32 CPU restatement of the reference's population forward.
+
+Follows, in plain fp32 torch CPU ops (no autocast, no flex_attention):
+  utils/model.py:17-31   attention with the window mask q >= k & q - k <= window (dense masked softmax)
+  utils/model.py:46-58   norm (rms_norm, eps = finfo(fp32).eps), has_ve, apply_rotary_emb
+  utils/model.py:177-191 rotary tables (fp32 freqs -> cos/sin rounded to bf16), window sizes
+  utils/model.py:193-209 GPT.forward (mix scalars, blocks, final norm, head, softcap 15, cross-entropy)
+  utils/model.py:81-120  CausalSelfAttention / MLP / Block forward
+  train/val/eggroll.py:56-103 lowrank, lowrank_embed, population_loss
+  train/val/run.py:89-94  head_loss (final norm, fp32 head, softcap, per-token CE)
+  train/val/run.py:143-152 hadamard
+Parameters are a dict name -> tensor using the reference's state-dict names.
+"""
+import math
+
+import torch
+import torch.nn.functional as F
+
+N_LAYER, N_HEAD, HEAD_DIM, N_EMBD, VOCAB, SEQ = 8, 8, 64, 512, 4096, 2048
+SOFTCAP = 15.0
+
+
+def has_ve(i, n_layer=N_LAYER):
+    return i % 2 == (n_layer - 1) % 2
+
+
+def window_sizes(n_layer=N_LAYER, seq=SEQ, pattern='SSSL'):
+    """model.py:185-191: S = seq // 2, L = seq, last block always L."""
+    sizes = [seq if pattern[i % len(pattern)] == 'L' else seq // 2 for i in range(n_layer)]
+    sizes[-1] = seq
+    return sizes
+
+
+def norm(x):
+    return F.rms_norm(x, (x.size(-1),))
+
+
+def rotary_tables(length, head_dim=HEAD_DIM, base=10000):
+    """cos, sin [length, head_dim/2] as fp32 holding the bf16-rounded values of model.py:177-183."""
+    inv_freq = 1.0 / base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim)
+    t = torch.arange(length, dtype=torch.float32)
+    freqs = torch.outer(t, inv_freq)
+    return freqs.cos().bfloat16().float(), freqs.sin().bfloat16().float()
+
+
+def apply_rotary_emb(x, cos, sin):
+    """x [B, T, H, D]; cos/sin [T, D/2]."""
+    d = x.shape[3] // 2
+    x1, x2 = x[..., :d], x[..., d:]
+    c, s = cos[None, :, None, :], sin[None, :, None, :]
+    return torch.cat([x1 * c + x2 * s, x1 * -s + x2 * c], 3)
+
+
+def attention(q, k, v, window, chunk=4):
+    """softmax(q k^T / sqrt(D) masked) v for [B, T, H, D] inputs, in fp32, batches in chunks."""
+    B, T, H, D = q.shape
+    i = torch.arange(T)[:, None]
+    j = torch.arange(T)[None, :]
+    visible = (i >= j) & (i - j <= window)
+    out = torch.empty(B, T, H, D, dtype=torch.float32)
+    for b0 in range(0, B, chunk):
+        qh = q[b0:b0 + chunk].float().transpose(1, 2)
+        kh = k[b0:b0 + chunk].float().transpose(1, 2)
+        vh = v[b0:b0 + chunk].float().transpose(1, 2)
+        s = (qh @ kh.transpose(-1, -2)) / math.sqrt(D)
+        s = s.masked_fill(~visible, float('-inf'))
+        out[b0:b0 + chunk] = (torch.softmax(s, -1) @ vh).transpose(1, 2)
+    return out
+
+
+def softcap_ce(logits, targets, reduction='mean'):
+    logits = SOFTCAP * torch.tanh(logits.float() / SOFTCAP)
+    return F.cross_entropy(logits.reshape(-1, logits.size(-1)), targets.reshape(-1), ignore_index=-1,
+                           reduction=reduction)
+
+
+def _block(P, i, x, ve, cos, sin, window):
+    """Block.forward (model.py:116-120) with CausalSelfAttention (81-97) and MLP (105-107)."""
+    B, T, C = x.shape
+    pre = f'transformer.h.{i}.'
+    h = norm(x)
+    q = (h @ P[pre + 'attn.c_q.weight'].t()).view(B, T, N_HEAD, HEAD_DIM)
+    k = (h @ P[pre + 'attn.c_k.weight'].t()).view(B, T, N_HEAD, HEAD_DIM)
+    v = (h @ P[pre + 'attn.c_v.weight'].t()).view(B, T, N_HEAD, HEAD_DIM)
+    if ve is not None:
+        gate = 2 * torch.sigmoid(h[..., :32] @ P[pre + 'attn.ve_gate.weight'].t())
+        v = v + gate.unsqueeze(-1) * ve.view(B, T, N_HEAD, HEAD_DIM)
+    q, k = norm(apply_rotary_emb(q, cos, sin)), norm(apply_rotary_emb(k, cos, sin))
+    y = attention(q, k, v, window).reshape(B, T, C)
+    x = x + y @ P[pre + 'attn.c_proj.weight'].t()
+    x = x + F.relu(norm(x) @ P[pre + 'mlp.c_fc.weight'].t()).square() @ P[pre + 'mlp.c_proj.weight'].t()
+    return x
+
+
+def gpt_forward(P, idx, targets=None, reduction='mean'):
+    """GPT.forward (model.py:193-209) in fp32: logits, or the softcapped cross-entropy."""
+    B, T = idx.shape
+    cos, sin = rotary_tables(T)
+    windows = window_sizes()
+    x = x0 = norm(P['transformer.wte.weight'][idx].float())
+    for i in range(N_LAYER):
+        x = P['resid_lambdas'][i] * x + P['x0_lambdas'][i] * x0
+        ve = P[f'value_embeds.{i}.weight'][idx].float() if has_ve(i) else None
+        x = _block(P, i, x, ve, cos, sin, windows[i])
+    x = norm(x)
+    logits = (x @ P['lm_head.weight'].t())[..., :VOCAB].float()
+    if targets is None:
+        return SOFTCAP * torch.tanh(logits / SOFTCAP)
+    return softcap_ce(logits, targets, reduction)
+
+
+def lowrank(x, weight, a, b, sign):
+    """eggroll.py:56-58 in fp32: x [m, T, in] through W [out, in] + sign * a b^T per member."""
+    return x @ weight.t() + sign[:, None, None] * (x @ b.unsqueeze(-1)) * a[:, None, :]
+
+
+def lowrank_embed(weight, a, b, idx, sign):
+    """eggroll.py:61-63: embedding rows of W + sign * a b^T for token ids idx [T]."""
+    return weight[idx].unsqueeze(0) + sign[:, None, None] * a[:, idx].unsqueeze(-1) * b[:, None, :]
+
+
+def population_loss(P, noise, sign, idx, targets, members_per_chunk=None):
+    """eggroll.py:66-103 in fp32: mean CE [m] of m perturbed models on one sequence.
+
+    noise: name -> (a [m, out], b [m, in]) for perturbed matrices/embeddings, or eps [m, L] for the mixing
+    scalars; names absent from `noise` are unperturbed. members_per_chunk splits m to bound memory."""
+    m = sign.shape[0]
+    if members_per_chunk and m > members_per_chunk:
+        parts = []
+        for c in range(0, m, members_per_chunk):
+            sl = slice(c, c + members_per_chunk)
+            sub = {n: (tuple(t[sl] for t in v) if isinstance(v, tuple) else v[sl]) for n, v in noise.items()}
+            parts.append(population_loss(P, sub, sign[sl], idx, targets))
+        return torch.cat(parts)
+    length = idx.shape[0]
+    cos, sin = rotary_tables(length)
+    windows = window_sizes()
+    s = sign[:, None, None]
+
+    def lin(name, inp):
+        if name in noise:
+            return lowrank(inp, P[name], *noise[name], sign)
+        return inp @ P[name].t()
+
+    def emb(name):
+        if name in noise:
+            return lowrank_embed(P[name].float(), *noise[name], idx, sign)
+        return P[name][idx].float().unsqueeze(0).expand(m, length, -1)
+
+    def scalar(name, i):
+        base = P[name][i]
+        if name in noise:
+            return base + s * noise[name][:, i, None, None]
+        return base
+
+    x = x0 = norm(emb('transformer.wte.weight'))
+    for i in range(N_LAYER):
+        pre = f'transformer.h.{i}.'
+        x = scalar('resid_lambdas', i) * x + scalar('x0_lambdas', i) * x0
+        h = norm(x)
+        q = lin(pre + 'attn.c_q.weight', h).view(m, length, N_HEAD, HEAD_DIM)
+        k = lin(pre + 'attn.c_k.weight', h).view(m, length, N_HEAD, HEAD_DIM)
+        v = lin(pre + 'attn.c_v.weight', h).view(m, length, N_HEAD, HEAD_DIM)
+        if has_ve(i):
+            ve = emb(f'value_embeds.{i}.weight').reshape(m, length, N_HEAD, HEAD_DIM)
+            gate = 2 * torch.sigmoid(lin(pre + 'attn.ve_gate.weight', h[..., :32]))
+            v = v + gate.unsqueeze(-1) * ve
+        q, k = norm(apply_rotary_emb(q, cos, sin)), norm(apply_rotary_emb(k, cos, sin))
+        y = attention(q, k, v, windows[i]).reshape(m, length, -1)
+        x = x + lin(pre + 'attn.c_proj.weight', y)
+        x = x + lin(pre + 'mlp.c_proj.weight', F.relu(lin(pre + 'mlp.c_fc.weight', norm(x))).square())
+    h = norm(x)
+    logits = lin('lm_head.weight', h)[..., :VOCAB]
+    ce = softcap_ce(logits, targets.repeat(m), reduction='none')
+    return ce.view(m, length).mean(-1)
+
+
+def head_loss(x, weight, targets, vocab=VOCAB):
+    """run.py:89-94 in fp32: final norm, head, softcap, per-token CE (ignore_index -1), reduction none."""
+    logits = (norm(x.float()) @ weight.float().t())[..., :vocab]
+    return softcap_ce(logits, targets, reduction='none')
+
+
+def hadamard(d):
+    """run.py:143-152: Sylvester Hadamard matrix of order d (power of two), entries +-1."""
+    if d & (d - 1):
+        raise ValueError(f'Orthogonal draws need a power-of-two width, not {d}.')
+    H = torch.ones(1, 1)
+    while H.shape[0] < d:
+        H = torch.cat([torch.cat([H, H], 1), torch.cat([H, -H], 1)], 0)
+    return H

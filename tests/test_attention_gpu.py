@@ -1,0 +1,107 @@
+"""HIP attention vs fp32 references (utils/model.py:24-31 semantics).
+
+Tolerance (bf16 inputs, fp32 reference): relative Frobenius error ||out - ref|| / ||ref|| <= 2e-2 and
+max |out - ref| <= 2e-2 * max |ref|.
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device('cuda', 0)
+
+
+def rel_ok(out, ref, tol=2e-2):
+    out, ref = out.float(), ref.float()
+    fro = ((out - ref).norm() / ref.norm()).item()
+    mx = ((out - ref).abs().max() / ref.abs().max()).item()
+    assert fro <= tol and mx <= tol, f'rel fro {fro:.3e}, rel max {mx:.3e}'
+    return fro, mx
+
+
+def fp32_reference_gpu(q, k, v, window):
+    """Dense masked softmax in fp32 on the GPU, one batch at a time (no bf16 batched products)."""
+    B, T, H, D = q.shape
+    i = torch.arange(T, device=q.device)[:, None]
+    j = torch.arange(T, device=q.device)[None, :]
+    visible = (i >= j) & (i - j <= window)
+    out = torch.empty(B, T, H, D, device=q.device, dtype=torch.float32)
+    for b in range(B):
+        qh, kh, vh = (t[b].float().transpose(0, 1).contiguous() for t in (q, k, v))
+        s = torch.matmul(qh, kh.transpose(-1, -2).contiguous()) / math.sqrt(D)
+        s = s.masked_fill(~visible, float('-inf'))
+        out[b] = torch.matmul(torch.softmax(s, -1), vh).transpose(0, 1)
+    return out
+
+
+def test_config_attention_causal():
+    """bf16 q, k, v [B=16, H=8, T=2048, D=64] ~ N(0,1) from one CPU generator seed 0 (q, k, v in order),
+    causal, passed as the [B, T, H, D] views the reference's attention() takes."""
+    from noise_amd.model import attention
+    g = torch.Generator().manual_seed(0)
+    q, k, v = (torch.randn(16, 8, 2048, 64, generator=g).bfloat16().to(DEV).transpose(1, 2) for _ in range(3))
+    out = attention(q, k, v, 2048)
+    assert out.dtype == torch.bfloat16 and out.shape == q.shape
+    rel_ok(out, fp32_reference_gpu(q, k, v, 2048))
+
+
+@pytest.mark.parametrize('B,T,H,window', [(2, 2048, 8, 1024), (1, 1000, 3, 300), (3, 64, 8, 0), (1, 130, 2, 5000),
+                                          (2, 513, 8, 64)])
+def test_windows_and_ragged_lengths_vs_oracle(B, T, H, window):
+    """Against the CPU oracle (dense masked fp32): window edges, lengths not multiple of 64,
+    heads not a multiple of 8, window 0 (each query sees only itself)."""
+    from noise_amd.model import attention
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn(B, T, H, 64, generator=g).bfloat16() for _ in range(3))
+    out = attention(q.to(DEV), k.to(DEV), v.to(DEV), window).cpu()
+    ref = om.attention(q.float(), k.float(), v.float(), window)
+    rel_ok(out, ref)
+    if window == 0:
+        assert torch.equal(out, v), 'window 0: each query returns its own value row'
+
+
+def test_strided_views_and_fp32_inputs():
+    """[B, H, T, D] storage passed as transposed views (the reference's flex call layout), fp32 in -> fp32 out."""
+    from noise_amd.model import attention
+    g = torch.Generator().manual_seed(2)
+    qh, kh, vh = (torch.randn(2, 8, 512, 64, generator=g).to(DEV) for _ in range(3))
+    q, k, v = (t.transpose(1, 2) for t in (qh, kh, vh))
+    out = attention(q, k, v, 200)
+    assert out.dtype == torch.float32
+    rel_ok(out, fp32_reference_gpu(q.bfloat16(), k.bfloat16(), v.bfloat16(), 200))
+
+
+def test_transposed_v_and_fused_dot():
+    """Population layout: q, k [B, H, T, D], v^T [B, H, D, T], fused x.b dot per head."""
+    from noise_amd.model import attention, attention_raw
+    g = torch.Generator().manual_seed(3)
+    B, H, T = 4, 8, 256
+    q, k, v = (torch.randn(B, T, H, 64, generator=g).bfloat16().to(DEV) for _ in range(3))
+    ref = attention(q, k, v, 100)
+    qh, kh = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
+    vt = v.permute(0, 2, 3, 1).contiguous()  # [B, H, D, T]
+    out = torch.empty(B, T, H, 64, dtype=torch.bfloat16, device=DEV)
+    dvec = torch.randn(B // 2, H * 64, generator=g).to(DEV)
+    dot = torch.empty(B, T, H, device=DEV)
+    attention_raw(qh.transpose(1, 2), kh.transpose(1, 2), vt, out, 100, v_transposed=True, dot_vec=dvec,
+                  dot_div=2, dot_out=dot)
+    assert torch.equal(out, ref)
+    expect = (out.float().view(B, T, H, 64) * dvec.repeat_interleave(2, 0).view(B, 1, H, 64)).sum(-1)
+    assert torch.allclose(dot, expect, rtol=1e-4, atol=1e-4)
+
+
+def test_deterministic():
+    from noise_amd.model import attention
+    g = torch.Generator().manual_seed(4)
+    q, k, v = (torch.randn(2, 1024, 8, 64, generator=g).bfloat16().to(DEV) for _ in range(3))
+    assert torch.equal(attention(q, k, v, 1024), attention(q, k, v, 1024))
+
+
+def test_invalid_head_dim_raises():
+    from noise_amd.model import attention
+    q = torch.zeros(1, 64, 2, 32, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises(RuntimeError, match='head_dim must be 64'):
+        attention(q, q, q, 10)
