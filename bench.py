@@ -1,0 +1,178 @@
+"""Population-forward throughput on one MI355X: member-tokens/s at 1024 members x 2048 tokens.
+
+Workload (the reference's EGGROLL population evaluation, train/val/eggroll.py:130-146, on one GPU):
+  model     the fixed 37.7M GPT (utils/model.py), make_model init seed 0 on the CPU (eggroll.py:38-53)
+  tokens    one 2049-token sequence ~ Zipf(s=1.1) over [0, 4096) (torch.multinomial, CPU generator seed 0),
+            shared by every member (eggroll.py:143); x = seq[:-1], y = seq[1:]
+  members   512 antithetic pairs = 1024 members, sigma 0.002 (eggroll.py:31), rank-1 noise on the 48 block
+            matrices, sliced from the seed-0 noise buffer at the step-0 offsets (eggroll.py:114-128)
+A step = offsets draw + noise regeneration + weight prep + the fused population forward -> 1024 losses.
+The CPU baseline is the fp32 oracle restatement of the same forward on a bounded member sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+TOKENS = 2048
+PAIRS = 512
+SIGMA = 0.002
+BF16_PEAK = 2.5e15           # MI355X dense bf16 MFMA, FLOP/s
+HBM_PEAK = 8.0e12            # MI355X HBM3E, B/s
+WINDOWS = None
+
+
+def zipf_tokens(n, s=1.1, vocab=4096, seed=0):
+    import torch
+    p = (torch.arange(vocab, dtype=torch.float64) + 1) ** -s
+    return torch.multinomial(p / p.sum(), n, replacement=True, generator=torch.Generator().manual_seed(seed))
+
+
+def visible_pairs(T, window):
+    """Sum over queries of keys visible under q >= k, q - k <= window."""
+    return sum(min(q, window) + 1 for q in range(T))
+
+
+def kernel_flops_per_launch(name, label, members, T):
+    """Algorithmic FLOPs one launch performs (dense products; rank-1 terms not counted)."""
+    rows = members * T
+    if name == 'noise_pop_qkv':
+        return 2 * 512 * 1536 * rows
+    if name == 'noise_pop_fc':
+        return 2 * 512 * 2048 * rows
+    if name == 'noise_pop_residual':
+        return 2 * (2048 if label == 'mlp.c_proj' else 512) * 512 * rows
+    if name == 'noise_pop_head_ce':
+        return 2 * 512 * 4096 * rows
+    if name == 'noise_attention_fwd':
+        window = int(label.split()[-1])
+        return 4 * 64 * 8 * members * visible_pairs(T, window)
+    return None
+
+
+def block_matrix_names():
+    return [f'transformer.h.{i}.{s}.weight' for i in range(8)
+            for s in ('attn.c_q', 'attn.c_k', 'attn.c_v', 'attn.c_proj', 'mlp.c_fc', 'mlp.c_proj')]
+
+
+def cpu_baseline(P, tables, x, y, members):
+    """The oracle forward (fp32, torch CPU) on `members` members of the same workload."""
+    import torch
+    from oracle import model as om
+    threads = torch.get_num_threads()
+    noise = {}
+    for n, (a, b) in tables.items():
+        noise[n] = (a[:members // 2].cpu().repeat_interleave(2, 0), b[:members // 2].cpu().repeat_interleave(2, 0))
+    sign = torch.tensor([SIGMA, -SIGMA]).repeat(members // 2)
+    Pc = {k: v.cpu().float() for k, v in P.items()}
+    om.population_loss(Pc, {n: (a[:2], b[:2]) for n, (a, b) in noise.items()}, sign[:2], x.cpu()[:256], y.cpu()[:256])
+    t0 = time.perf_counter()
+    losses = om.population_loss(Pc, noise, sign, x.cpu(), y.cpu(), members_per_chunk=2)
+    dt = time.perf_counter() - t0
+    return dict(value=members * x.numel() / dt, unit='member-tokens/s', cores=threads, kind='port',
+                sample=f'{members} members x {x.numel()} tokens, fp32 oracle forward (oracle/model.py), '
+                       f'{dt:.1f} s on {threads} threads'), losses
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=5)
+    ap.add_argument('--warmup', type=int, default=2)
+    ap.add_argument('--members', type=int, default=2 * PAIRS)
+    ap.add_argument('--cpu-members', type=int, default=4, help='members of the CPU-baseline sample (0: skip)')
+    ap.add_argument('--profile-steps', type=int, default=1, help='extra timed steps with per-kernel events')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py measures one GPU: this build has no multi-GPU path (members shard across GPUs with one '
+              'all_gather of the losses; see DESIGN.md). Run with --gpus 1.', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from noise_amd import eggroll as eg
+    from noise_amd.model import make_model, window_sizes
+
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    model = make_model('cpu', 0)
+    P = {k: v.to(dev) for k, v in model.state_dict().items()}
+    model = model.to(dev)
+    seq = zipf_tokens(TOKENS + 1)
+    x, y = seq[:-1].to(dev), seq[1:].to(dev)
+    names = block_matrix_names()
+    members = args.members
+    pairs = members // 2
+    es = eg.Eggroll(model, pairs)
+    rope = None
+    sign = torch.tensor([SIGMA, -SIGMA], device=dev).repeat(pairs)
+    directions = torch.arange(0, members, 2, device=dev) % (2 * pairs) // 2
+
+    def step():
+        offsets = es.offsets(0)
+        tables = {}
+        for n in names:
+            p = es.params[n]
+            rows = es.buffer.gather(offsets[n], sum(p.shape), rows=directions)
+            tables[n] = tuple(rows.split(list(p.shape), dim=1))
+        W = eg.Weights(P)
+        return eg.population_forward(W, tables, sign, x, y, dir_div=2, rope=rope), tables
+
+    for _ in range(args.warmup):
+        losses, tables = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        losses, tables = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    value = members * TOKENS / dt
+
+    # per-kernel HIP events (torch's current stream = the launch stream) over extra timed steps
+    timer = eg.KernelTimer()
+    eg.set_timer(timer)
+    for _ in range(args.profile_steps):
+        step()
+    torch.cuda.synchronize()
+    eg.set_timer(None)
+    kernels = {}
+    for (name, label), (n, ms) in timer.totals().items():
+        key = name if label is None else f'{name}[{label}]'
+        flops = kernel_flops_per_launch(name, label, members, TOKENS)
+        entry = dict(launches=n // args.profile_steps, ms_per_step=round(ms / args.profile_steps, 4))
+        if flops is not None:
+            tf = flops * n / (ms * 1e-3)
+            entry.update(tflops=round(tf / 1e12, 1), mfma_frac=round(tf / BF16_PEAK, 4))
+        kernels[key] = entry
+    dominant = max((k for k in kernels if 'tflops' in kernels[k]), key=lambda k: kernels[k]['ms_per_step'])
+    dk = kernels[dominant]
+    roofline = dict(bound='mfma', kernel=dominant, achieved=round(dk['tflops'], 1), peak=BF16_PEAK / 1e12,
+                    unit='TFLOP/s', frac=dk['mfma_frac'], traffic=None)
+
+    algo_flops = 68_318_208 * members * TOKENS
+    line = dict(
+        metric='member-tokens/sec forward at P=1024,T=2048 on 1 GPU; attn/GEMM % MFMA peak',
+        value=round(value, 1), unit='member-tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(dt * 1e3, 3), higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
+        data='synthetic',
+        config=dict(workload='population fitness: fixed 37.7M GPT (seed-0 init), 1024 members (512 antithetic '
+                             'pairs, sigma 0.002, rank-1 noise on the 48 block matrices) x 2048 Zipf(1.1) tokens, '
+                             'fused per-member CE', members=members, tokens=TOKENS, pairs=pairs),
+        roofline=roofline,
+        whole_forward=dict(algorithmic_tflops=round(algo_flops / dt / 1e12, 1),
+                           mfma_frac=round(algo_flops / dt / BF16_PEAK, 4)),
+        kernels=kernels,
+        losses=dict(mean=round(losses.mean().item(), 6), first=round(losses[0].item(), 6),
+                    finite=bool(torch.isfinite(losses).all().item())),
+    )
+    if args.cpu_members:
+        cb, cpu_losses = cpu_baseline(P, {n: t for n, t in tables.items()}, x, y, args.cpu_members)
+        line['cpu_baseline'] = cb
+        line['cpu_parity_max_abs'] = float((cpu_losses - losses[:args.cpu_members].cpu()).abs().max())
+    else:
+        line['cpu_baseline'] = None
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -86,6 +86,118 @@ int noise_attention_fwd(const void *q, const void *k, const void *v, void *o, in
                         const float *dot_vec, int64_t dot_vec_stride, int64_t dot_div, float *dot_out,
                         noise_stream_t stream);
 
+/* ------------------------------------------------------------------------------------------------
+ * Perturbed linears of the population forward (eggroll.py:56-58 `lowrank`, fused with what the
+ * reference runs around each one in population_loss, eggroll.py:66-103).
+ *
+ * Rows are (member, token) pairs. A member m uses noise row m / dir_div of each [directions, width]
+ * noise table (dir_div = 2 for antithetic pairs, eggroll.py:141) and scale sign[m] (+-sigma,
+ * eggroll.py:138). The rank-1 term sign[m] * (x . b) * a^T is split: the x . b dots of a layer's input
+ * are produced by the kernel that writes that input (its epilogue), and the consumer adds
+ * sign[m] * dot * a[n]. Matrices are bf16 [out, in] row-major (torch Linear layout). Activations are
+ * bf16 unless stated; the residual stream is fp32. tokens must be a multiple of the tile (256).
+ * ---------------------------------------------------------------------------------------------- */
+
+/* Strided 3-D view: element (m, t, j) at ptr + m*sm + t*st + j. sm = 0 broadcasts one row-set to all
+ * members. Strides are in elements. */
+typedef struct {
+    const void *ptr;
+    int64_t sm, st;
+} noise_view_t;
+
+/* Per-member rank-1 noise of one matrix: a [dirs, out], b [dirs, in] fp32 rows (a_stride, b_stride
+ * elements apart); NULL a means the matrix is unperturbed. */
+typedef struct {
+    const float *a;
+    const float *b;
+    int64_t a_stride, b_stride;
+} noise_rank1_t;
+
+/* Shared member bookkeeping of one population call. */
+typedef struct {
+    int64_t members, tokens;
+    const float *sign;   /* [members] +-sigma (or any per-member scale) */
+    int64_t dir_div;     /* member m uses noise row m / dir_div */
+} noise_population_t;
+
+/* Block entry (eggroll.py:74-79 for block 0; model.py:196-199): e = wte[idx[t]] (+ sign * a[idx[t]] * b,
+ * lowrank_embed eggroll.py:61-63), x0 = norm(e), x = rl*x0 + ml*x0 (rl/ml = resid/x0 lambda of block 0,
+ * + sign * eps when eps_* != NULL, eggroll.py:77-78), h = bf16(norm(x)). per_member = 0 writes one shared
+ * [tokens][512] set (no embedding or lambda noise); per_member = 1 writes [members][tokens][512]. wte is
+ * fp32 [V][512] (eggroll.py:50). x0, xin fp32, h bf16. */
+int noise_pop_embed(const noise_population_t *pop, int per_member, const float *wte, const int64_t *idx,
+                    const noise_rank1_t *emb_noise, float lam_r, float lam_x, const float *eps_r, const float *eps_x,
+                    int64_t eps_stride, float *x0, float *xin, void *h, noise_stream_t stream);
+
+/* out[(m*tokens + t)*nk + k] = sum_n x[m, t, n] * vecs[k].b[(m / dir_div)*b_stride + n], n < width:
+ * the x . b factor of eggroll.py:58's rank-1 term for up to 3 matrices sharing input x. */
+int noise_member_dots(const noise_population_t *pop, noise_view_t x, int64_t width, const noise_rank1_t *vecs,
+                      int64_t nk, float *out, noise_stream_t stream);
+
+/* Q, K, V of one block for every member (eggroll.py:81-90): x (= norm of the block input, bf16) times
+ * c_q, c_k, c_v (w[0..2], bf16 [512][512]) + sign * dots[row*3 + i] * a_i, value-embedding gate on V
+ * (ve fp32 [V][512] or NULL; gate_w fp32 [8][32] = attn.ve_gate.weight; gate_noise: rank-1 noise of
+ * ve_gate, a [dirs][8], b [dirs][32]; ve_noise: lowrank_embed noise of the value table, a [dirs][V],
+ * b [dirs][512]; either NULL), rotary (rope_cos/rope_sin fp32 [tokens][32] holding model.py:177-183's
+ * bf16 tables) then per-head RMSNorm on Q and K. Outputs bf16 [members][8][tokens][64]. */
+int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3], const noise_rank1_t r1[3],
+                  const float *dots, const float *rope_cos, const float *rope_sin, const float *ve,
+                  const int64_t *idx, const float *gate_w, const noise_rank1_t *gate_noise,
+                  const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream);
+
+/* Residual writer (eggroll.py:92 attn.c_proj and :93 mlp.c_proj): y = xres + x w^T + sign * (sum of
+ * dots_count dots at dots[row*dots_stride]) * a; if mix: y = rl*y + ml*x0 (the next block's mixing,
+ * eggroll.py:79, lambdas + sign * eps); xout = y (fp32, may be NULL); hout = bf16(norm(y)) [m][T][512]
+ * or, with split3, its [hi | lo | hi] bf16 split [m][T][1536] for the fp32 head; next_dots[row*nnext+k]
+ * = norm(y) . next[k].b (0 <= nnext <= 3). w bf16 [512][K]. */
+int noise_pop_residual(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K,
+                       const noise_rank1_t *r1, const float *dots, int64_t dots_stride, int64_t dots_count,
+                       noise_view_t xres, float *xout, int mix, float lam_r, float lam_x, const float *eps_r,
+                       const float *eps_x, int64_t eps_stride, noise_view_t x0, void *hout, int split3,
+                       const noise_rank1_t *next, int64_t nnext, float *next_dots, noise_stream_t stream);
+
+/* MLP hidden (eggroll.py:93): act = relu(x w^T + sign * dots[row] * a)^2 as bf16 [m][T][2048];
+ * partial_dots[row*16 + n/128] = sum over that 128-feature slice of act * next->b (for mlp.c_proj's
+ * rank-1 term; NULL next skips). w bf16 [2048][512]. */
+int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const void *w, const noise_rank1_t *r1,
+                 const float *dots, void *act, const noise_rank1_t *next, float *partial_dots,
+                 noise_stream_t stream);
+
+/* Perturbed linear (eggroll.py:56-58 `lowrank`): y[m, t, :] = x[m, t, :] w^T + sign[m] * dots[m*T+t] *
+ * a[m / dir_div] (dots = x . b from noise_member_dots; r1 NULL or r1->a NULL: plain linear). bf16 x and
+ * w [N][K]; y bf16 or fp32 (y_fp32) with strides ys_m, ys_t. N multiple of 256, K of 64. */
+int noise_pop_linear(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K, int64_t N,
+                     const noise_rank1_t *r1, const float *dots, void *y, int y_fp32, int64_t ys_m, int64_t ys_t,
+                     noise_stream_t stream);
+
+/* Head, soft cap 15 and per-token cross-entropy (eggroll.py:94-101, model.py:202-209, run.py:89-94):
+ * logits = x w^T (+ sign * dots * a), z = 15 tanh(logits / 15), token_loss[m*T + t] = logsumexp(z) -
+ * z[target] (0 where target < 0). w bf16 [vocab][K]; K = 512, or 1536 for the split-bf16x3 fp32 head
+ * (x = [hi|lo|hi], w = [hi|hi|lo], noise_split3). targets int64 [T] shared (targets_sm = 0) or per member. */
+int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K, int64_t vocab,
+                      const noise_rank1_t *r1, const float *dots, const int64_t *targets, int64_t targets_sm,
+                      float *token_loss, noise_stream_t stream);
+
+/* out[m] = mean over tokens of token_loss[m][:] (eggroll.py:102), deterministic order. */
+int noise_member_mean(const float *token_loss, int64_t members, int64_t tokens, float *out, noise_stream_t stream);
+
+/* bf16x3 split of fp32 rows of width 512: out[r] = [hi | lo | hi] of (normalize ? norm(x[r]) : x[r]), or
+ * [hi | hi | lo] when weight_order (hi = bf16(v), lo = bf16(v - hi)). Feeds the fp32 head of run.py:273-278
+ * (TF32 on the reference's H100; split-bf16x3 on gfx950, which has no xf32 MFMA). */
+int noise_split3(const float *x, int64_t rows, int64_t width, int normalize, int weight_order, void *out,
+                 noise_stream_t stream);
+
+/* lowrank_embed (eggroll.py:61-63): out[m, t, :] = w[idx[t], :] + sign[m] * a[m/dir_div, idx[t]] *
+ * b[m/dir_div, :] (r1 NULL or r1->a NULL: plain gather), fp32 [members][tokens][width]. */
+int noise_lowrank_embed(float *out, const float *w, int64_t vocab, int64_t width, const int64_t *idx,
+                        const noise_population_t *pop, const noise_rank1_t *r1, noise_stream_t stream);
+
+/* Rank-1 expansion of a product shared by all members (eggroll.py:58 with x broadcast over members):
+ * y[m, t, n] = base[t, n] + sign[m] * dots[m*T + t] * a[m/dir_div, n], y bf16 or fp32 [m][T][width],
+ * base fp32 [T][width]. An HBM-write stream: the shared x W^T is computed once (noise_pop_linear). */
+int noise_rank1_expand(const noise_population_t *pop, const float *base, int64_t width, const float *dots,
+                       const noise_rank1_t *r1, void *y, int y_fp32, noise_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

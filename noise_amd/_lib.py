@@ -21,8 +21,37 @@ SIGNATURES = {
     'noise_gather_slices': [_p, _i64, _i64, _p, _p, _i64, _u64, _u64, _i64, _p],
     'noise_attention_fwd': [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _p, _p],
+    'noise_pop_embed': [_p, _i32, _p, _p, _p, _f32, _f32, _p, _p, _i64, _p, _p, _p, _p],
+    'noise_member_dots': [_p, 'View', _i64, _p, _i64, _p, _p],
+    'noise_pop_qkv': [_p, 'View', _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    'noise_pop_residual': [_p, 'View', _p, _i64, _p, _p, _i64, _i64, 'View', _p, _i32, _f32, _f32, _p, _p,
+                           _i64, 'View', _p, _i32, _p, _i64, _p, _p],
+    'noise_pop_fc': [_p, 'View', _p, _p, _p, _p, _p, _p, _p],
+    'noise_pop_linear': [_p, 'View', _p, _i64, _i64, _p, _p, _p, _i32, _i64, _i64, _p],
+    'noise_pop_head_ce': [_p, 'View', _p, _i64, _i64, _p, _p, _p, _i64, _p, _p],
+    'noise_member_mean': [_p, _i64, _i64, _p, _p],
+    'noise_split3': [_p, _i64, _i64, _i32, _i32, _p, _p],
+    'noise_lowrank_embed': [_p, _p, _i64, _i64, _p, _p, _p, _p],
+    'noise_rank1_expand': [_p, _p, _i64, _p, _p, _p, _i32, _p],
 }
 _RESTYPES = {'noise_last_error': ctypes.c_char_p}
+
+
+class View(ctypes.Structure):
+    """noise_view_t: element (m, t, j) at ptr + m*sm + t*st + j."""
+    _fields_ = [('ptr', ctypes.c_void_p), ('sm', ctypes.c_int64), ('st', ctypes.c_int64)]
+
+
+class Rank1(ctypes.Structure):
+    """noise_rank1_t: per-direction a [dirs, out], b [dirs, in] rows (NULL a: unperturbed)."""
+    _fields_ = [('a', ctypes.c_void_p), ('b', ctypes.c_void_p), ('a_stride', ctypes.c_int64),
+                ('b_stride', ctypes.c_int64)]
+
+
+class Population(ctypes.Structure):
+    """noise_population_t."""
+    _fields_ = [('members', ctypes.c_int64), ('tokens', ctypes.c_int64), ('sign', ctypes.c_void_p),
+                ('dir_div', ctypes.c_int64)]
 
 _lib = None
 
@@ -36,7 +65,7 @@ def lib():
         handle = ctypes.CDLL(str(LIB_PATH))
         for name, argtypes in SIGNATURES.items():
             fn = getattr(handle, name)
-            fn.argtypes = argtypes
+            fn.argtypes = [View if a == 'View' else a for a in argtypes]
             fn.restype = _RESTYPES.get(name, ctypes.c_int)
         _lib = handle
     return _lib

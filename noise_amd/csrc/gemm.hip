@@ -1,0 +1,830 @@
+// Perturbed linears of the population forward and the fused head + soft-capped cross-entropy.
+//
+// Replaces eggroll.py:56-58 `lowrank` (x W^T + sign (x b) a^T, the rank-1 term never materialised) at
+// every call site of population_loss (eggroll.py:80-93, 99), together with the elementwise work the
+// reference runs between them (rotary + per-head norm, eggroll.py:90 / model.py:55-58, 46-47; value
+// embedding gate, eggroll.py:85-89; residual adds and mixing scalars, eggroll.py:77-79, 92-93; ReLU^2,
+// eggroll.py:93; RMSNorm, model.py:46-47) and the head's softcap + cross-entropy + per-member mean
+// (eggroll.py:94-103; run.py:89-94 for the fp32 head).
+//
+// Shape of every product: out[(m,t), n] = sum_k W[n, k] x[(m,t), k], computed transposed (W rows are the
+// MFMA A operand, token rows the B operand) so that each lane of a v_mfma_f32_32x32x16_bf16 result holds
+// 16 output features of ONE token: per-token / per-head epilogue reductions stay in the lane plus one
+// exchange with lane ^ 32. A workgroup (4 waves) computes a BN x BM (features x tokens) tile, each wave
+// 128 x 128 (4 x 4 MFMA blocks, 256 fp32 accumulators); tiles are streamed through one padded LDS buffer
+// (144 B rows: conflict-free 16 B fragment reads) with the next k-step's global loads in flight.
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace noise {
+namespace {
+
+constexpr int kBK = 64;
+constexpr int kLdsRow = 72;
+constexpr float kEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps, F.rms_norm's default
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+__device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+__device__ __forceinline__ float f4get(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
+
+// ------------------------------------------------------------------------------------------------
+// K loop: acc[fb][tb] += W[n0 + wn0 + 32fb + .., :] . X[t + wm0 + 32tb + .., :]
+// ------------------------------------------------------------------------------------------------
+template <int BN, int BM>
+struct Mma {
+    static constexpr int WN = BN / 128;
+    static constexpr int WM = BM / 128;
+    static_assert(WN * WM == 4, "4 waves of 128 x 128");
+    static constexpr int CW = BN / 32;  // 16 B chunks per thread
+    static constexpr int CX = BM / 32;
+
+    __device__ static void run(const __bf16 *W, int64_t ldw, const __bf16 *X, int64_t ldx, int K,
+                               __bf16 (*sW)[kLdsRow], __bf16 (*sX)[kLdsRow], f32x16 (&acc)[4][4], int tid,
+                               int wn0, int wm0) {
+        const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
+#pragma unroll
+        for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) acc[fb][tb] = f32x16{};
+        bf16x8 rw[CW], rx[CX];
+        auto load = [&](int k0) {
+#pragma unroll
+            for (int i = 0; i < CW; ++i) {
+                int c = tid + 256 * i;
+                rw[i] = load_bf16x8(W + (int64_t)(c >> 3) * ldw + k0 + (c & 7) * 8);
+            }
+#pragma unroll
+            for (int i = 0; i < CX; ++i) {
+                int c = tid + 256 * i;
+                rx[i] = load_bf16x8(X + (int64_t)(c >> 3) * ldx + k0 + (c & 7) * 8);
+            }
+        };
+        auto store = [&]() {
+#pragma unroll
+            for (int i = 0; i < CW; ++i) {
+                int c = tid + 256 * i;
+                store_bf16x8(&sW[c >> 3][(c & 7) * 8], rw[i]);
+            }
+#pragma unroll
+            for (int i = 0; i < CX; ++i) {
+                int c = tid + 256 * i;
+                store_bf16x8(&sX[c >> 3][(c & 7) * 8], rx[i]);
+            }
+        };
+        load(0);
+        store();
+        __syncthreads();
+        for (int k0 = 0; k0 < K; k0 += kBK) {
+            const bool more = k0 + kBK < K;
+            if (more) load(k0 + kBK);
+            // the 4 sub-steps stay a loop: unrolling them hoists all fragment loads and spills
+#pragma unroll 1
+            for (int s = 0; s < 4; ++s) {
+                bf16x8 af[4], bf[4];
+#pragma unroll
+                for (int fb = 0; fb < 4; ++fb) af[fb] = load_bf16x8(&sW[wn0 + 32 * fb + j][16 * s + 8 * hf]);
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb) bf[tb] = load_bf16x8(&sX[wm0 + 32 * tb + j][16 * s + 8 * hf]);
+#pragma unroll
+                for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+                    for (int tb = 0; tb < 4; ++tb) acc[fb][tb] = mfma32x32x16(af[fb], bf[tb], acc[fb][tb]);
+            }
+            __syncthreads();
+            if (more) {
+                store();
+                __syncthreads();
+            }
+        }
+    }
+};
+
+// feature offset (within a wave's 128) of accumulator register r of block fb for lane half hf
+__device__ __forceinline__ int feat(int fb, int r, int hf) { return 32 * fb + 8 * (r >> 2) + 4 * hf + (r & 3); }
+
+struct Pop {
+    int members, tokens;
+    const float *sign;
+    int dir_div;
+};
+
+struct Rank1 {
+    const float *a, *b;
+    int64_t a_stride, b_stride;
+};
+
+// ------------------------------------------------------------------------------------------------
+// Q, K, V: rank-1 correction, value-embedding gate (V), rotary + per-head RMSNorm (Q, K),
+// written bf16 [m][H][T][64].
+// ------------------------------------------------------------------------------------------------
+struct QkvArgs {
+    Pop pop;
+    const __bf16 *x;
+    int64_t xs_m, xs_t;
+    const __bf16 *w[3];
+    Rank1 r1[3];
+    const float *dots;        // [rows][3]: x . b_q, x . b_k, x . b_v
+    const float *cos_t, *sin_t;  // [T][32]
+    const float *ve;          // [V][512] fp32 or NULL
+    const int64_t *idx;       // [T]
+    const float *gate_w;      // [8][32] fp32
+    Rank1 gate_r1;            // ve_gate noise (a [dirs][8], b [dirs][32]) or a == NULL
+    Rank1 ve_r1;              // value-embedding noise (a [dirs][V], b [dirs][512]) or a == NULL
+    __bf16 *out[3];           // [m][8][T][64]
+};
+
+__global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
+    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    const int T = p.pop.tokens;
+    const int tiles_t = T / 256;
+    // blockIdx.x -> (feature tile, token tile); the 6 feature tiles of a token tile are adjacent, so
+    // its x rows are re-read from L2 while hot.
+    const int nt = blockIdx.x % 6, tt = blockIdx.x / 6;
+    const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
+    const int n0 = nt * 256, mat = n0 / 512, nl0 = n0 % 512;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+
+    f32x16 acc[4][4];
+    Mma<256, 256>::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512,
+                       sW, sX, acc, tid, wn0, wm0);
+
+    const int dir = m / p.pop.dir_div;
+    const float sgn = p.pop.sign[m];
+    const Rank1 r1 = p.r1[mat];
+    const int head0 = (nl0 + wn0) / 64;
+    const float *arow = r1.a ? r1.a + dir * r1.a_stride + nl0 + wn0 : nullptr;
+    __bf16 *outm = p.out[mat];
+
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int t = t0 + wm0 + 32 * tb + j;
+        const int64_t row = (int64_t)m * T + t;
+        if (arow) {
+            const float corr = sgn * p.dots[row * 3 + mat];
+#pragma unroll
+            for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float4 a4 = ld4(arow + 32 * fb + 8 * g + 4 * hf);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc[fb][tb][4 * g + e] += corr * f4get(a4, e);
+                }
+        }
+        if (mat == 2 && p.ve) {
+            // v += 2 sigmoid(x[:32] . Wg[head]) * ve[idx[t], head*64 + d]   (eggroll.py:85-89)
+            const __bf16 *xr = p.x + m * p.xs_m + (int64_t)t * p.xs_t;
+            float z[2] = {0.f, 0.f};
+#pragma unroll
+            for (int c8 = 0; c8 < 4; ++c8) {
+                bf16x8 xv = load_bf16x8(xr + 8 * c8);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float xf = (float)xv[e];
+                    z[0] += xf * p.gate_w[head0 * 32 + 8 * c8 + e];
+                    z[1] += xf * p.gate_w[(head0 + 1) * 32 + 8 * c8 + e];
+                }
+            }
+            if (p.gate_r1.a) {
+                // lowrank ve_gate: + sign * (x[:32] . b_g) * a_g[head]
+                const float *gb = p.gate_r1.b + dir * p.gate_r1.b_stride;
+                float dg = 0.f;
+#pragma unroll
+                for (int c8 = 0; c8 < 4; ++c8) {
+                    bf16x8 xv = load_bf16x8(xr + 8 * c8);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) dg += (float)xv[e] * gb[8 * c8 + e];
+                }
+                const float *ga = p.gate_r1.a + dir * p.gate_r1.a_stride;
+                z[0] += sgn * dg * ga[head0];
+                z[1] += sgn * dg * ga[head0 + 1];
+            }
+            const int64_t tok = p.idx[t];
+            const float *ver = p.ve + tok * 512;
+            // lowrank_embed of the value table (eggroll.py:61-63): + sign * a_ve[tok] * b_ve[:]
+            const float ves = p.ve_r1.a ? sgn * p.ve_r1.a[dir * p.ve_r1.a_stride + tok] : 0.f;
+            const float *veb = p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride : nullptr;
+#pragma unroll
+            for (int hd = 0; hd < 2; ++hd) {
+                const float gate = 2.0f / (1.0f + __expf(-z[hd]));
+#pragma unroll
+                for (int half = 0; half < 2; ++half)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int d0 = (head0 + hd) * 64 + 32 * half + 8 * g + 4 * hf;
+                        float4 e4 = ld4(ver + d0);
+                        float4 b4 = veb ? ld4(veb + d0) : float4{0, 0, 0, 0};
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[2 * hd + half][tb][4 * g + e] += gate * (f4get(e4, e) + ves * f4get(b4, e));
+                    }
+            }
+        }
+        if (mat < 2) {
+            // rotary (model.py:55-58) then RMSNorm over the head (model.py:46-47)
+            const float *cr = p.cos_t + (int64_t)t * 32, *sr = p.sin_t + (int64_t)t * 32;
+#pragma unroll
+            for (int hd = 0; hd < 2; ++hd) {
+                float ss = 0.f;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float4 c4 = ld4(cr + 8 * g + 4 * hf), s4 = ld4(sr + 8 * g + 4 * hf);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * g + e;
+                        const float c = f4get(c4, e), s = f4get(s4, e);
+                        const float x1 = acc[2 * hd][tb][r], x2 = acc[2 * hd + 1][tb][r];
+                        const float o1 = x1 * c + x2 * s;
+                        const float o2 = x1 * -s + x2 * c;
+                        acc[2 * hd][tb][r] = o1;
+                        acc[2 * hd + 1][tb][r] = o2;
+                        ss += o1 * o1 + o2 * o2;
+                    }
+                }
+                ss += swap_halves(ss);
+                const float rstd = rsqrtf(ss * (1.0f / 64.0f) + kEps);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    acc[2 * hd][tb][r] *= rstd;
+                    acc[2 * hd + 1][tb][r] *= rstd;
+                }
+            }
+        }
+#pragma unroll
+        for (int hd = 0; hd < 2; ++hd) {
+            __bf16 *orow = outm + (((int64_t)m * 8 + head0 + hd) * T + t) * 64;
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    bf16x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) o[e] = (__bf16)acc[2 * hd + half][tb][4 * g + e];
+                    store_bf16x4(orow + 32 * half + 8 * g + 4 * hf, o);
+                }
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Residual writers (attn.c_proj, mlp.c_proj; N = 512, whole rows per workgroup):
+//   y = xres + (x W^T + sign * dot * a)        [+ mix: y = rl * y + ml * x0 for the next block]
+//   write y (fp32) if xout; h = RMSNorm(y) as bf16 (or its [hi | lo | hi] bf16 split for the fp32 head);
+//   next_dots[row][k] = h . b_k for the next perturbed linear(s).
+// ------------------------------------------------------------------------------------------------
+struct ResidArgs {
+    Pop pop;
+    const __bf16 *x;
+    int64_t xs_m, xs_t;
+    const __bf16 *w;
+    int K;
+    Rank1 r1;
+    const float *dots;
+    int64_t dots_stride;
+    int dots_count;
+    const float *xres;
+    int64_t xr_m, xr_t;
+    float *xout;              // [m][T][512] or NULL
+    int mix;
+    float lam_r, lam_x;
+    const float *eps_r, *eps_x;  // per-direction lambda noise (eps[dir * eps_stride]) or NULL
+    int64_t eps_stride;
+    const float *x0;
+    int64_t x0_m, x0_t;
+    __bf16 *hout;             // [m][T][512] or [m][T][1536] (split3)
+    int split3;
+    const float *nb[3];
+    int64_t nb_stride[3];
+    int nnext;
+    float *ndots;             // [rows][nnext]
+};
+
+__global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sW[512][kLdsRow];
+    __shared__ __attribute__((aligned(16))) __bf16 sX[128][kLdsRow];
+    const int T = p.pop.tokens;
+    const int tiles_t = T / 128;
+    const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * 128;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int wn0 = 128 * wave;
+
+    f32x16 acc[4][4];
+    Mma<512, 128>::run(p.w, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, sW, sX, acc, tid, wn0, 0);
+
+    const int dir = m / p.pop.dir_div;
+    const float sgn = p.pop.sign[m];
+    float rl = p.lam_r, ml = p.lam_x;
+    if (p.mix) {
+        if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
+        if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
+    }
+    // per-token partial statistics: [0] sum y^2, [1..3] y . b_k, reduced over lanes and waves in LDS
+    float *red = reinterpret_cast<float *>(&sX[0][0]);  // [128 tokens][4 waves][4]
+
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int t = t0 + 32 * tb + j;
+        const int64_t row = (int64_t)m * T + t;
+        float corr = 0.f;
+        if (p.r1.a) {
+            float c = 0.f;
+            for (int i = 0; i < p.dots_count; ++i) c += p.dots[row * p.dots_stride + i];
+            corr = sgn * c;
+        }
+        const float *xr = p.xres + m * p.xr_m + (int64_t)t * p.xr_t + wn0;
+        const float *x0r = p.mix ? p.x0 + m * p.x0_m + (int64_t)t * p.x0_t + wn0 : nullptr;
+        const float *ar = p.r1.a ? p.r1.a + dir * p.r1.a_stride + wn0 : nullptr;
+        float st[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int f0 = 32 * fb + 8 * g + 4 * hf;
+                float4 xv = ld4(xr + f0);
+                float4 a4 = ar ? ld4(ar + f0) : float4{0, 0, 0, 0};
+                float4 z4 = x0r ? ld4(x0r + f0) : float4{0, 0, 0, 0};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float y = f4get(xv, e) + (acc[fb][tb][4 * g + e] + corr * f4get(a4, e));
+                    if (p.mix) y = rl * y + ml * f4get(z4, e);
+                    acc[fb][tb][4 * g + e] = y;
+                    st[0] += y * y;
+                }
+#pragma unroll
+                for (int k = 0; k < 3; ++k) {
+                    if (k < p.nnext) {
+                        float4 b4 = ld4(p.nb[k] + dir * p.nb_stride[k] + wn0 + f0);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) st[1 + k] += acc[fb][tb][4 * g + e] * f4get(b4, e);
+                    }
+                }
+            }
+        if (p.xout) {
+            float *xo = p.xout + row * 512 + wn0;
+#pragma unroll
+            for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    st4(xo + 32 * fb + 8 * g + 4 * hf, float4{acc[fb][tb][4 * g], acc[fb][tb][4 * g + 1],
+                                                              acc[fb][tb][4 * g + 2], acc[fb][tb][4 * g + 3]});
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) st[k] += swap_halves(st[k]);
+        if (hf == 0) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) red[((32 * tb + j) * 4 + wave) * 4 + k] = st[k];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int tl = 32 * tb + j;
+        const int t = t0 + tl;
+        const int64_t row = (int64_t)m * T + t;
+        float tot[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) tot[k] += red[(tl * 4 + w) * 4 + k];
+        const float rstd = rsqrtf(tot[0] * (1.0f / 512.0f) + kEps);
+        if (p.split3) {
+            __bf16 *ho = p.hout + row * 1536 + wn0;
+#pragma unroll
+            for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    bf16x4 hi, lo;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        float h = acc[fb][tb][4 * g + e] * rstd;
+                        hi[e] = (__bf16)h;
+                        lo[e] = (__bf16)(h - (float)hi[e]);
+                    }
+                    const int f0 = 32 * fb + 8 * g + 4 * hf;
+                    store_bf16x4(ho + f0, hi);
+                    store_bf16x4(ho + 512 + f0, lo);
+                    store_bf16x4(ho + 1024 + f0, hi);
+                }
+        } else {
+            __bf16 *ho = p.hout + row * 512 + wn0;
+#pragma unroll
+            for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    bf16x4 hv;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) hv[e] = (__bf16)(acc[fb][tb][4 * g + e] * rstd);
+                    store_bf16x4(ho + 32 * fb + 8 * g + 4 * hf, hv);
+                }
+        }
+        if (wave == 0 && hf == 0) {
+            for (int k = 0; k < p.nnext; ++k) p.ndots[row * p.nnext + k] = rstd * tot[1 + k];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// MLP hidden (mlp.c_fc, N = 2048): act = relu(x W^T + sign * dot * a)^2 as bf16, and the partial dots
+// act . b of the following mlp.c_proj over this wave's 128 features: pdots[row][n / 128].
+// ------------------------------------------------------------------------------------------------
+struct FcArgs {
+    Pop pop;
+    const __bf16 *x;
+    int64_t xs_m, xs_t;
+    const __bf16 *w;
+    Rank1 r1;
+    const float *dots;        // [rows]
+    __bf16 *act;              // [m][T][2048]
+    const float *nb;          // next b rows [dirs][2048] or NULL
+    int64_t nb_stride;
+    float *pdots;             // [rows][16]
+};
+
+__global__ __launch_bounds__(256, 1) void fc_kernel(FcArgs p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
+    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    const int T = p.pop.tokens;
+    const int tiles_t = T / 256;
+    const int nt = blockIdx.x % 8, tt = blockIdx.x / 8;
+    const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
+    const int n0 = nt * 256;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+
+    f32x16 acc[4][4];
+    Mma<256, 256>::run(p.w + (int64_t)n0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, sW, sX,
+                       acc, tid, wn0, wm0);
+
+    const int dir = m / p.pop.dir_div;
+    const float sgn = p.pop.sign[m];
+    const int nf0 = n0 + wn0;
+    const float *arow = p.r1.a ? p.r1.a + dir * p.r1.a_stride + nf0 : nullptr;
+    const float *brow = p.nb ? p.nb + dir * p.nb_stride + nf0 : nullptr;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int t = t0 + wm0 + 32 * tb + j;
+        const int64_t row = (int64_t)m * T + t;
+        const float corr = arow ? sgn * p.dots[row] : 0.f;
+        float pd = 0.f;
+        __bf16 *ar = p.act + row * 2048 + nf0;
+#pragma unroll
+        for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int f = 32 * fb + 8 * g + 4 * hf;
+                float4 a4 = arow ? ld4(arow + f) : float4{0, 0, 0, 0};
+                float4 b4 = brow ? ld4(brow + f) : float4{0, 0, 0, 0};
+                bf16x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    float y = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
+                    y = y > 0.f ? y * y : 0.f;
+                    o[e] = (__bf16)y;
+                    pd += (float)o[e] * f4get(b4, e);
+                }
+                store_bf16x4(ar + f, o);
+            }
+        if (p.pdots) {
+            pd += swap_halves(pd);
+            if (hf == 0) p.pdots[row * 16 + nf0 / 128] = pd;
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Generic perturbed linear (eggroll.py:56-58): y = x W^T + sign * dot * a, bf16 or fp32 out.
+// grid: (N / 256) * (T / 256) * members; N, T multiples of 256, K multiple of 64.
+// ------------------------------------------------------------------------------------------------
+struct LowrankArgs {
+    Pop pop;
+    const __bf16 *x;
+    int64_t xs_m, xs_t;
+    const __bf16 *w;
+    int K, N;
+    Rank1 r1;
+    const float *dots;        // [rows] (x . b per row) or NULL when unperturbed
+    void *y;
+    int y_fp32;
+    int64_t ys_m, ys_t;
+};
+
+__global__ __launch_bounds__(256, 1) void lowrank_kernel(LowrankArgs p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
+    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    const int T = p.pop.tokens, ntiles = p.N / 256, tiles_t = T / 256;
+    const int nt = blockIdx.x % ntiles, tt = blockIdx.x / ntiles;
+    const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
+    const int n0 = nt * 256;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+
+    f32x16 acc[4][4];
+    Mma<256, 256>::run(p.w + (int64_t)n0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, sW, sX,
+                       acc, tid, wn0, wm0);
+    const int dir = m / p.pop.dir_div;
+    const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;
+    const int nf0 = n0 + wn0;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int t = t0 + wm0 + 32 * tb + j;
+        const int64_t row = (int64_t)m * T + t;
+        const float corr = p.r1.a ? sgn * p.dots[row] : 0.f;
+#pragma unroll
+        for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int f = nf0 + 32 * fb + 8 * g + 4 * hf;
+                float4 a4 = p.r1.a ? ld4(p.r1.a + dir * p.r1.a_stride + f) : float4{0, 0, 0, 0};
+                float o[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
+                if (p.y_fp32) {
+                    st4((float *)p.y + m * p.ys_m + (int64_t)t * p.ys_t + f, float4{o[0], o[1], o[2], o[3]});
+                } else {
+                    bf16x4 ob;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) ob[e] = (__bf16)o[e];
+                    store_bf16x4((__bf16 *)p.y + m * p.ys_m + (int64_t)t * p.ys_t + f, ob);
+                }
+            }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// Head + softcap 15 + cross-entropy per token (eggroll.py:94-103, model.py:202-209, run.py:89-94).
+// A workgroup owns 256 tokens of one member and sweeps the vocabulary in 256-wide chunks. With
+// z = 15 tanh(l / 15) <= 15 the log-sum-exp needs no running max: lse = 15 + log sum exp(z - 15), and
+// exp(z - 15) = exp(-30 / (e^(2l/15) + 1)). K = 1536 with [hi|hi|lo] weights and [hi|lo|hi] inputs gives
+// the split-bf16x3 fp32 head.
+// ------------------------------------------------------------------------------------------------
+struct HeadArgs {
+    Pop pop;
+    const __bf16 *x;
+    int64_t xs_m, xs_t;
+    const __bf16 *w;
+    int K, vocab;
+    Rank1 r1;
+    const float *dots;
+    const int64_t *targets;   // [T] shared by all members, or [m][T] when targets_sm != 0
+    int64_t targets_sm;
+    float *loss;              // [m][T] per-token CE (0 where target < 0)
+};
+
+__global__ __launch_bounds__(256, 1) void head_ce_kernel(HeadArgs p) {
+    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
+    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    const int T = p.pop.tokens, tiles_t = T / 256;
+    const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * 256;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+    const int dir = m / p.pop.dir_div;
+    const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;
+
+    float corr[4];
+    int64_t tgt[4];
+    float sum[4] = {0.f, 0.f, 0.f, 0.f}, zt[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int t = t0 + wm0 + 32 * tb + j;
+        const int64_t row = (int64_t)m * T + t;
+        corr[tb] = p.r1.a ? sgn * p.dots[row] : 0.f;
+        tgt[tb] = p.targets[m * p.targets_sm + t];
+    }
+    const float k1 = (2.0f / 15.0f) * kLog2e, k2 = -30.0f * kLog2e;
+    f32x16 acc[4][4];
+    for (int v0 = 0; v0 < p.vocab; v0 += 256) {
+        Mma<256, 256>::run(p.w + (int64_t)v0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, sW,
+                           sX, acc, tid, wn0, wm0);
+        const int nf0 = v0 + wn0;
+#pragma unroll
+        for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int f = nf0 + 32 * fb + 8 * g + 4 * hf;
+                float4 a4 = p.r1.a ? ld4(p.r1.a + dir * p.r1.a_stride + f) : float4{0, 0, 0, 0};
+#pragma unroll
+                for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float l = acc[fb][tb][4 * g + e] + corr[tb] * f4get(a4, e);
+                        const float u = exp2_fast(l * k1) + 1.0f;
+                        const float ru = __builtin_amdgcn_rcpf(u);
+                        sum[tb] += exp2_fast(k2 * ru);
+                        if (f + e == tgt[tb]) zt[tb] = 15.0f - 30.0f * ru;
+                    }
+            }
+    }
+    // combine the two lane halves and the two feature waves
+    float *red = reinterpret_cast<float *>(&sX[0][0]);  // [256 tokens][2 waves][2]
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        sum[tb] += swap_halves(sum[tb]);
+        zt[tb] += swap_halves(zt[tb]);
+        if (hf == 0) {
+            const int tl = wm0 + 32 * tb + j;
+            red[(tl * 2 + (wave & 1)) * 2 + 0] = sum[tb];
+            red[(tl * 2 + (wave & 1)) * 2 + 1] = zt[tb];
+        }
+    }
+    __syncthreads();
+    if ((wave & 1) == 0 && hf == 0) {
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) {
+            const int tl = wm0 + 32 * tb + j;
+            const float s = red[(tl * 2) * 2] + red[(tl * 2 + 1) * 2];
+            const float z = red[(tl * 2) * 2 + 1] + red[(tl * 2 + 1) * 2 + 1];
+            const float ce = 15.0f + __logf(s) - z;
+            p.loss[(int64_t)m * T + t0 + tl] = tgt[tb] < 0 ? 0.f : ce;
+        }
+    }
+}
+
+Pop make_pop(const noise_population_t *pp) {
+    Pop p;
+    p.members = (int)pp->members;
+    p.tokens = (int)pp->tokens;
+    p.sign = pp->sign;
+    p.dir_div = (int)pp->dir_div;
+    return p;
+}
+
+Rank1 make_r1(const noise_rank1_t *r) {
+    Rank1 o{nullptr, nullptr, 0, 0};
+    if (r && r->a) {
+        o.a = r->a;
+        o.b = r->b;
+        o.a_stride = r->a_stride;
+        o.b_stride = r->b_stride;
+    }
+    return o;
+}
+
+int check_pop(const noise_population_t *pp, int tile, const char *fn) {
+    NOISE_CHECK_ARG(pp != nullptr, "%s: population is NULL", fn);
+    NOISE_CHECK_ARG(pp->members > 0 && pp->tokens > 0, "%s: members and tokens must be positive", fn);
+    NOISE_CHECK_ARG(pp->tokens % tile == 0, "%s: tokens (%lld) must be a multiple of %d", fn, (long long)pp->tokens, tile);
+    NOISE_CHECK_ARG(pp->dir_div >= 1, "%s: dir_div must be >= 1", fn);
+    NOISE_CHECK_ARG(pp->members * pp->tokens < (1ll << 31), "%s: members * tokens must stay below 2^31", fn);
+    return NOISE_OK;
+}
+
+int check_view(const noise_view_t &v, const char *fn, const char *name) {
+    NOISE_CHECK_ARG(v.ptr != nullptr, "%s: %s is NULL", fn, name);
+    NOISE_CHECK_ARG(aligned(v.ptr, 16) && v.sm % 8 == 0 && v.st % 8 == 0,
+                    "%s: %s must be 16 B aligned with strides multiple of 8 elements", fn, name);
+    return NOISE_OK;
+}
+
+#define NOISE_TRY(x)                 \
+    do {                             \
+        int _s = (x);                \
+        if (_s != NOISE_OK) return _s; \
+    } while (0)
+
+}  // namespace
+}  // namespace noise
+
+using namespace noise;
+
+extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3],
+                             const noise_rank1_t r1[3], const float *dots, const float *rope_cos, const float *rope_sin,
+                             const float *ve, const int64_t *idx, const float *gate_w, const noise_rank1_t *gate_noise,
+                             const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_qkv";
+    NOISE_TRY(check_pop(pop, 256, fn));
+    NOISE_TRY(check_view(x, fn, "x"));
+    NOISE_CHECK_ARG(w && out && rope_cos && rope_sin, "%s: NULL weight/output/rotary pointer", fn);
+    for (int i = 0; i < 3; ++i) {
+        NOISE_CHECK_ARG(w[i] && out[i] && aligned(w[i], 16) && aligned(out[i], 8), "%s: weight/output %d NULL or misaligned", fn, i);
+        NOISE_CHECK_ARG(!r1 || !r1[i].a || (dots && aligned(r1[i].a, 16) && r1[i].a_stride % 4 == 0),
+                        "%s: perturbed matrix %d needs dots and 16 B aligned a rows", fn, i);
+    }
+    NOISE_CHECK_ARG(!ve || (idx && gate_w), "%s: value embeddings need idx and gate weights", fn);
+    QkvArgs a;
+    a.pop = make_pop(pop);
+    a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
+    for (int i = 0; i < 3; ++i) {
+        a.w[i] = (const __bf16 *)w[i];
+        a.r1[i] = make_r1(r1 ? &r1[i] : nullptr);
+        a.out[i] = (__bf16 *)out[i];
+    }
+    a.dots = dots; a.cos_t = rope_cos; a.sin_t = rope_sin; a.ve = ve; a.idx = idx; a.gate_w = gate_w;
+    a.gate_r1 = make_r1(ve ? gate_noise : nullptr);
+    a.ve_r1 = make_r1(ve ? ve_noise : nullptr);
+    NOISE_CHECK_ARG(!a.ve_r1.a || (aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
+                    "%s: value-embedding noise b rows must be 16 B aligned", fn);
+    dim3 grid((unsigned)(6 * pop->members * (pop->tokens / 256)));
+    hipLaunchKernelGGL(qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}
+
+extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K,
+                                  const noise_rank1_t *r1, const float *dots, int64_t dots_stride, int64_t dots_count,
+                                  noise_view_t xres, float *xout, int mix, float lam_r, float lam_x,
+                                  const float *eps_r, const float *eps_x, int64_t eps_stride, noise_view_t x0,
+                                  void *hout, int split3, const noise_rank1_t *next, int64_t nnext, float *next_dots,
+                                  noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_residual";
+    NOISE_TRY(check_pop(pop, 128, fn));
+    NOISE_TRY(check_view(x, fn, "x"));
+    NOISE_CHECK_ARG(w && aligned(w, 16) && K % 64 == 0 && K > 0, "%s: w must be 16 B aligned, K a positive multiple of 64", fn);
+    NOISE_CHECK_ARG(xres.ptr && aligned(xres.ptr, 16) && xres.sm % 4 == 0 && xres.st % 4 == 0, "%s: bad xres", fn);
+    NOISE_CHECK_ARG(!xout || aligned(xout, 16), "%s: xout must be 16 B aligned", fn);
+    NOISE_CHECK_ARG(!mix || (x0.ptr && aligned(x0.ptr, 16) && x0.sm % 4 == 0 && x0.st % 4 == 0), "%s: mix needs x0", fn);
+    NOISE_CHECK_ARG(hout && aligned(hout, 8), "%s: hout NULL or misaligned", fn);
+    NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || (next && next_dots)), "%s: bad next-dot request", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && dots_count >= 1 && aligned(r1->a, 16)), "%s: perturbation needs dots", fn);
+    ResidArgs a;
+    a.pop = make_pop(pop);
+    a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
+    a.w = (const __bf16 *)w; a.K = (int)K;
+    a.r1 = make_r1(r1);
+    a.dots = dots; a.dots_stride = dots_stride; a.dots_count = (int)dots_count;
+    a.xres = (const float *)xres.ptr; a.xr_m = xres.sm; a.xr_t = xres.st;
+    a.xout = xout;
+    a.mix = mix; a.lam_r = lam_r; a.lam_x = lam_x; a.eps_r = eps_r; a.eps_x = eps_x; a.eps_stride = eps_stride;
+    a.x0 = (const float *)x0.ptr; a.x0_m = x0.sm; a.x0_t = x0.st;
+    a.hout = (__bf16 *)hout; a.split3 = split3;
+    a.nnext = (int)nnext; a.ndots = next_dots;
+    for (int k = 0; k < 3; ++k) {
+        a.nb[k] = (k < nnext) ? next[k].b : nullptr;
+        a.nb_stride[k] = (k < nnext) ? next[k].b_stride : 0;
+        if (k < nnext) NOISE_CHECK_ARG(next[k].b && aligned(next[k].b, 16), "%s: next b %d NULL or misaligned", fn, k);
+    }
+    dim3 grid((unsigned)(pop->members * (pop->tokens / 128)));
+    hipLaunchKernelGGL(resid_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}
+
+extern "C" int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const void *w, const noise_rank1_t *r1,
+                            const float *dots, void *act, const noise_rank1_t *next, float *partial_dots,
+                            noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_fc";
+    NOISE_TRY(check_pop(pop, 256, fn));
+    NOISE_TRY(check_view(x, fn, "x"));
+    NOISE_CHECK_ARG(w && aligned(w, 16) && act && aligned(act, 8), "%s: w/act NULL or misaligned", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || dots, "%s: perturbation needs dots", fn);
+    NOISE_CHECK_ARG(!next || !next->b || partial_dots, "%s: next b needs partial_dots", fn);
+    FcArgs a;
+    a.pop = make_pop(pop);
+    a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
+    a.w = (const __bf16 *)w;
+    a.r1 = make_r1(r1);
+    a.dots = dots;
+    a.act = (__bf16 *)act;
+    a.nb = (next && next->b) ? next->b : nullptr;
+    a.nb_stride = (next && next->b) ? next->b_stride : 0;
+    a.pdots = a.nb ? partial_dots : nullptr;
+    dim3 grid((unsigned)(8 * pop->members * (pop->tokens / 256)));
+    hipLaunchKernelGGL(fc_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}
+
+extern "C" int noise_pop_linear(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K, int64_t N,
+                                const noise_rank1_t *r1, const float *dots, void *y, int y_fp32, int64_t ys_m,
+                                int64_t ys_t, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_linear";
+    NOISE_TRY(check_pop(pop, 256, fn));
+    NOISE_TRY(check_view(x, fn, "x"));
+    NOISE_CHECK_ARG(K > 0 && K % 64 == 0 && N > 0 && N % 256 == 0, "%s: K must be a multiple of 64 and N of 256", fn);
+    NOISE_CHECK_ARG(w && aligned(w, 16) && y && aligned(y, 16) && ys_m % 4 == 0 && ys_t % 4 == 0,
+                    "%s: w/y NULL or misaligned", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && pop->sign), "%s: perturbation needs dots and sign", fn);
+    LowrankArgs a;
+    a.pop = make_pop(pop);
+    a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
+    a.w = (const __bf16 *)w; a.K = (int)K; a.N = (int)N;
+    a.r1 = make_r1(r1);
+    a.dots = dots; a.y = y; a.y_fp32 = y_fp32; a.ys_m = ys_m; a.ys_t = ys_t;
+    int64_t grid = (N / 256) * pop->members * (pop->tokens / 256);
+    NOISE_CHECK_ARG(grid < (1ll << 31), "%s: too many tiles", fn);
+    hipLaunchKernelGGL(lowrank_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}
+
+extern "C" int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K,
+                                 int64_t vocab, const noise_rank1_t *r1, const float *dots, const int64_t *targets,
+                                 int64_t targets_sm, float *token_loss, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_head_ce";
+    NOISE_TRY(check_pop(pop, 256, fn));
+    NOISE_TRY(check_view(x, fn, "x"));
+    NOISE_CHECK_ARG(K > 0 && K % 64 == 0 && vocab > 0 && vocab % 256 == 0, "%s: K multiple of 64, vocab of 256", fn);
+    NOISE_CHECK_ARG(w && aligned(w, 16) && targets && token_loss, "%s: NULL w/targets/loss", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && pop->sign), "%s: perturbation needs dots and sign", fn);
+    HeadArgs a;
+    a.pop = make_pop(pop);
+    a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
+    a.w = (const __bf16 *)w; a.K = (int)K; a.vocab = (int)vocab;
+    a.r1 = make_r1(r1);
+    a.dots = dots; a.targets = targets; a.targets_sm = targets_sm; a.loss = token_loss;
+    dim3 grid((unsigned)(pop->members * (pop->tokens / 256)));
+    hipLaunchKernelGGL(head_ce_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}

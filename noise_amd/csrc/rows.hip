@@ -1,0 +1,335 @@
+// Row-wise kernels of the population forward: embedding entry, member dot products, loss reduction and
+// the split-bf16x3 operands of the fp32 head. One 64-lane wave per 512-wide row, 8 elements per lane.
+#include "common.hpp"
+#include "mfma.hpp"
+
+namespace noise {
+namespace {
+
+constexpr float kEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ __forceinline__ void ld8(const float *p, float (&v)[8]) {
+    float4 a = *reinterpret_cast<const float4 *>(p), b = *reinterpret_cast<const float4 *>(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+__device__ __forceinline__ void st8(float *p, const float (&v)[8]) {
+    *reinterpret_cast<float4 *>(p) = float4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<float4 *>(p + 4) = float4{v[4], v[5], v[6], v[7]};
+}
+
+// Embedding entry of population_loss (eggroll.py:74-79 for block 0, model.py:196-199):
+//   e = W[idx[t]] (+ sign * a[dir, idx[t]] * b[dir, :])      lowrank_embed, eggroll.py:61-63
+//   x0 = norm(e); x = rl * x0 + ml * x0 (block 0's mix); h = bf16(norm(x))
+// rows = (member or shared, token); grid = rows / 4 workgroups of 4 waves.
+struct EmbedArgs {
+    int rows, tokens, per_member, dir_div;
+    const float *wte;
+    const int64_t *idx;
+    const float *sign;
+    const float *ea, *eb;     // embedding noise rows or NULL
+    int64_t ea_stride, eb_stride;
+    float lam_r, lam_x;
+    const float *eps_r, *eps_x;
+    int64_t eps_stride;
+    float *x0, *xin;
+    __bf16 *h;
+};
+
+__global__ __launch_bounds__(256) void embed_kernel(EmbedArgs p) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= p.rows) return;
+    const int m = p.per_member ? row / p.tokens : 0;
+    const int t = row - (p.per_member ? m * p.tokens : 0);
+    const int dir = m / p.dir_div;
+    const float sgn = p.per_member && p.sign ? p.sign[m] : 0.f;
+    const int64_t tok = p.idx[t];
+    float e[8];
+    ld8(p.wte + tok * 512 + lane * 8, e);
+    if (p.ea) {
+        const float s = sgn * p.ea[dir * p.ea_stride + tok];
+        float b[8];
+        ld8(p.eb + dir * p.eb_stride + lane * 8, b);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] += s * b[i];
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += e[i] * e[i];
+    float r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
+    float rl = p.lam_r, ml = p.lam_x;
+    if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
+    if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
+    float x0[8], x[8];
+    ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        x0[i] = e[i] * r;
+        x[i] = rl * x0[i] + ml * x0[i];
+        ss += x[i] * x[i];
+    }
+    r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
+    const int64_t o = (int64_t)row * 512 + lane * 8;
+    st8(p.x0 + o, x0);
+    st8(p.xin + o, x);
+    bf16x8 hv;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hv[i] = (__bf16)(x[i] * r);
+    store_bf16x8(p.h + o, hv);
+}
+
+// out[(m*T + t)*nk + k] = sum_n x[m, t, n] * b_k[m / dir_div, n], x bf16 with strides, n < width.
+struct DotsArgs {
+    int members, tokens, width, nk, dir_div;
+    const __bf16 *x;
+    int64_t xs_m, xs_t;
+    const float *b[3];
+    int64_t b_stride[3];
+    float *out;
+};
+
+__global__ __launch_bounds__(256) void dots_kernel(DotsArgs p) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= (int64_t)p.members * p.tokens) return;
+    const int m = (int)(row / p.tokens), t = (int)(row - (int64_t)m * p.tokens);
+    const int dir = m / p.dir_div;
+    const __bf16 *xr = p.x + m * p.xs_m + (int64_t)t * p.xs_t;
+    float acc[3] = {0.f, 0.f, 0.f};
+    for (int n0 = lane * 8; n0 < p.width; n0 += 512) {
+        bf16x8 xv = load_bf16x8(xr + n0);
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            if (k < p.nk) {
+                float b[8];
+                ld8(p.b[k] + dir * p.b_stride[k] + n0, b);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) acc[k] += (float)xv[i] * b[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+        if (k < p.nk) {
+            float v = wave_sum(acc[k]);
+            if (lane == 0) p.out[row * p.nk + k] = v;
+        }
+    }
+}
+
+// out[m] = mean_t loss[m, t] (eggroll.py:102 `.mean(-1)`), fixed-order tree: deterministic.
+__global__ __launch_bounds__(256) void member_mean_kernel(const float *loss, int tokens, float *out) {
+    __shared__ float part[256];
+    const int m = blockIdx.x;
+    const float *l = loss + (int64_t)m * tokens;
+    float s = 0.f;
+    for (int t = threadIdx.x; t < tokens; t += 256) s += l[t];
+    part[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w >= 1; w >>= 1) {
+        if ((int)threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[m] = part[0] / (float)tokens;
+}
+
+// fp32 head operands split into bf16 pairs (hi = bf16(v), lo = bf16(v - hi)):
+//   rows:   out[r] = [hi | lo | hi] of norm(x[r]) (norm optional)   -- the activations
+//   weight: out[r] = [hi | hi | lo] of w[r]                           -- the head matrix
+__global__ __launch_bounds__(256) void split3_kernel(const float *x, int64_t rows, int do_norm, int weight_order,
+                                                     __bf16 *out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float v[8];
+    ld8(x + row * 512 + lane * 8, v);
+    if (do_norm) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+        const float r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] *= r;
+    }
+    bf16x8 hi, lo;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        hi[i] = (__bf16)v[i];
+        lo[i] = (__bf16)(v[i] - (float)hi[i]);
+    }
+    __bf16 *o = out + row * 1536 + lane * 8;
+    store_bf16x8(o, hi);
+    store_bf16x8(o + 512, weight_order ? hi : lo);
+    store_bf16x8(o + 1024, weight_order ? lo : hi);
+}
+
+unsigned rows_grid(int64_t rows) { return (unsigned)((rows + 3) / 4); }
+
+}  // namespace
+}  // namespace noise
+
+using namespace noise;
+
+extern "C" int noise_pop_embed(const noise_population_t *pop, int per_member, const float *wte, const int64_t *idx,
+                               const noise_rank1_t *emb_noise, float lam_r, float lam_x, const float *eps_r,
+                               const float *eps_x, int64_t eps_stride, float *x0, float *xin, void *h,
+                               noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_embed";
+    NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
+    NOISE_CHECK_ARG(wte && idx && x0 && xin && h, "%s: NULL pointer", fn);
+    NOISE_CHECK_ARG(aligned(wte, 16) && aligned(x0, 16) && aligned(xin, 16) && aligned(h, 16), "%s: 16 B alignment", fn);
+    const bool noisy = (emb_noise && emb_noise->a) || eps_r || eps_x;
+    NOISE_CHECK_ARG(!noisy || (per_member && pop->sign), "%s: per-member noise needs per_member = 1 and sign", fn);
+    EmbedArgs a;
+    a.tokens = (int)pop->tokens;
+    a.per_member = per_member;
+    a.rows = (int)(per_member ? pop->members * pop->tokens : pop->tokens);
+    a.dir_div = (int)pop->dir_div;
+    a.wte = wte; a.idx = idx; a.sign = pop->sign;
+    a.ea = emb_noise && emb_noise->a ? emb_noise->a : nullptr;
+    a.eb = a.ea ? emb_noise->b : nullptr;
+    a.ea_stride = a.ea ? emb_noise->a_stride : 0;
+    a.eb_stride = a.ea ? emb_noise->b_stride : 0;
+    a.lam_r = lam_r; a.lam_x = lam_x; a.eps_r = eps_r; a.eps_x = eps_x; a.eps_stride = eps_stride;
+    a.x0 = x0; a.xin = xin; a.h = (__bf16 *)h;
+    hipLaunchKernelGGL(embed_kernel, dim3(rows_grid(a.rows)), dim3(256), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}
+
+extern "C" int noise_member_dots(const noise_population_t *pop, noise_view_t x, int64_t width,
+                                 const noise_rank1_t *vecs, int64_t nk, float *out, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_member_dots";
+    NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
+    NOISE_CHECK_ARG(nk >= 1 && nk <= 3 && vecs && out, "%s: need 1..3 vectors and an output", fn);
+    NOISE_CHECK_ARG(width > 0 && width % 512 == 0, "%s: width must be a multiple of 512", fn);
+    NOISE_CHECK_ARG(x.ptr && aligned(x.ptr, 16) && x.sm % 8 == 0 && x.st % 8 == 0, "%s: x misaligned", fn);
+    DotsArgs a;
+    a.members = (int)pop->members; a.tokens = (int)pop->tokens; a.width = (int)width; a.nk = (int)nk;
+    a.dir_div = (int)pop->dir_div;
+    a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
+    for (int k = 0; k < 3; ++k) {
+        a.b[k] = k < nk ? vecs[k].b : nullptr;
+        a.b_stride[k] = k < nk ? vecs[k].b_stride : 0;
+        if (k < nk) NOISE_CHECK_ARG(vecs[k].b && aligned(vecs[k].b, 16), "%s: b %d NULL or misaligned", fn, k);
+    }
+    a.out = out;
+    hipLaunchKernelGGL(dots_kernel, dim3(rows_grid(pop->members * pop->tokens)), dim3(256), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}
+
+extern "C" int noise_member_mean(const float *token_loss, int64_t members, int64_t tokens, float *out,
+                                 noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(token_loss && out && members > 0 && tokens > 0, "noise_member_mean: bad arguments");
+    hipLaunchKernelGGL(member_mean_kernel, dim3((unsigned)members), dim3(256), 0, (hipStream_t)stream, token_loss,
+                       (int)tokens, out);
+    return launch_status("noise_member_mean");
+}
+
+extern "C" int noise_split3(const float *x, int64_t rows, int64_t width, int normalize, int weight_order, void *out,
+                            noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(x && out && rows > 0 && width == 512, "noise_split3: x/out NULL or width != 512");
+    NOISE_CHECK_ARG(aligned(x, 16) && aligned(out, 16), "noise_split3: 16 B alignment");
+    hipLaunchKernelGGL(split3_kernel, dim3(rows_grid(rows)), dim3(256), 0, (hipStream_t)stream, x, rows, normalize,
+                       weight_order, (__bf16 *)out);
+    return launch_status("noise_split3");
+}
+
+namespace noise {
+namespace {
+
+// lowrank_embed (eggroll.py:61-63): out[m, t, :] = W[idx[t], :] + sign[m] * a[dir, idx[t]] * b[dir, :]
+__global__ __launch_bounds__(256) void lowrank_embed_kernel(float *out, const float *w, const int64_t *idx, int tokens,
+                                                            int width, const float *a, const float *b,
+                                                            int64_t a_stride, int64_t b_stride, const float *sign,
+                                                            int dir_div, int64_t total) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= total) return;
+    const int64_t row = i / width;
+    const int n = (int)(i - row * width);
+    const int m = (int)(row / tokens), t = (int)(row - (int64_t)m * tokens);
+    const int dir = m / dir_div;
+    const int64_t tok = idx[t];
+    float4 v = *reinterpret_cast<const float4 *>(w + tok * width + n);
+    if (a) {
+        const float s = sign[m] * a[dir * a_stride + tok];
+        float4 bv = *reinterpret_cast<const float4 *>(b + dir * b_stride + n);
+        v.x += s * bv.x; v.y += s * bv.y; v.z += s * bv.z; v.w += s * bv.w;
+    }
+    *reinterpret_cast<float4 *>(out + i) = v;
+}
+
+// Rank-1 expansion of a shared product (lowrank with x broadcast over members, eggroll.py:58):
+// y[m, t, n] = base[t, n] + sign[m] * dots[m*T + t] * a[dir, n]; 8 outputs per thread, bf16 or fp32.
+__global__ __launch_bounds__(256) void rank1_expand_kernel(void *y, int y_fp32, const float *base, const float *dots,
+                                                           const float *a, int64_t a_stride, const float *sign,
+                                                           int dir_div, int tokens, int width, int64_t total) {
+    const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+    if (i >= total) return;
+    const int64_t row = i / width;
+    const int n = (int)(i - row * width);
+    const int m = (int)(row / tokens), t = (int)(row - (int64_t)m * tokens);
+    const float c = sign[m] * dots[row];
+    const float *ar = a + (int64_t)(m / dir_div) * a_stride + n;
+    const float *br = base + (int64_t)t * width + n;
+    float o[8];
+    ld8(br, o);
+    float av[8];
+    ld8(ar, av);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] += c * av[e];
+    if (y_fp32) {
+        st8((float *)y + i, o);
+    } else {
+        bf16x8 ob;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ob[e] = (__bf16)o[e];
+        store_bf16x8((__bf16 *)y + i, ob);
+    }
+}
+
+}  // namespace
+}  // namespace noise
+
+extern "C" int noise_lowrank_embed(float *out, const float *w, int64_t vocab, int64_t width, const int64_t *idx,
+                                   const noise_population_t *pop, const noise_rank1_t *r1, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_lowrank_embed";
+    NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
+    NOISE_CHECK_ARG(out && w && idx && vocab > 0 && width > 0 && width % 4 == 0, "%s: bad arguments", fn);
+    NOISE_CHECK_ARG(aligned(out, 16) && aligned(w, 16), "%s: 16 B alignment", fn);
+    const bool noisy = r1 && r1->a;
+    NOISE_CHECK_ARG(!noisy || (pop->sign && r1->b && aligned(r1->b, 16) && r1->b_stride % 4 == 0),
+                    "%s: noise needs sign and 16 B aligned b rows", fn);
+    const int64_t total = pop->members * pop->tokens * width;
+    hipLaunchKernelGGL(lowrank_embed_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, out, w, idx, (int)pop->tokens, (int)width, noisy ? r1->a : nullptr,
+                       noisy ? r1->b : nullptr, noisy ? r1->a_stride : 0, noisy ? r1->b_stride : 0, pop->sign,
+                       (int)pop->dir_div, total);
+    return launch_status(fn);
+}
+
+extern "C" int noise_rank1_expand(const noise_population_t *pop, const float *base, int64_t width, const float *dots,
+                                  const noise_rank1_t *r1, void *y, int y_fp32, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_rank1_expand";
+    NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1 && pop->sign, "%s: bad population", fn);
+    NOISE_CHECK_ARG(base && dots && r1 && r1->a && y && width > 0 && width % 8 == 0, "%s: bad arguments", fn);
+    NOISE_CHECK_ARG(aligned(base, 16) && aligned(r1->a, 16) && r1->a_stride % 4 == 0 && aligned(y, 16),
+                    "%s: 16 B alignment", fn);
+    const int64_t total = pop->members * pop->tokens * width;
+    hipLaunchKernelGGL(rank1_expand_kernel, dim3((unsigned)((total / 8 + 255) / 256)), dim3(256), 0,
+                       (hipStream_t)stream, y, y_fp32, base, dots, r1->a, r1->a_stride, pop->sign, (int)pop->dir_div,
+                       (int)pop->tokens, (int)width, total);
+    return launch_status(fn);
+}

@@ -1,0 +1,416 @@
+"""EGGROLL's population forward on libnoise_amd (train/val/eggroll.py:56-168 call sites).
+
+  lowrank(x, weight, a, b, sign)            eggroll.py:56-58
+  lowrank_embed(weight, a, b, idx, sign)    eggroll.py:61-63
+  population_loss(model, p, noise, sign, idx, targets)   eggroll.py:66-103
+  Eggroll(model, pairs).offsets(step) / .noise(offsets, directions)   eggroll.py:106-128
+
+The forward runs as one chain of fused HIP kernels per block (noise_pop_* in include/noise_amd.h):
+  qkv (+rank-1, ve gate, rotary, q/k norm) -> attention (+ x.b dots of c_proj) ->
+  residual (c_proj, + norm, + c_fc dot) -> fc (ReLU^2, + mlp.c_proj partial dots) ->
+  residual (mlp.c_proj, + next block's mix, norm and q/k/v dots) ... -> head + softcap + CE -> mean.
+Noise enters as per-direction rows: member m uses row m // dir_div (2 for antithetic pairs) of every
+[dirs, out + in] table, never repeated per member.
+"""
+import ctypes
+import math
+
+import torch
+
+from . import _lib
+from .model import rotary_tables, window_sizes, has_ve, N_EMBD, N_HEAD, HEAD_DIM, VOCAB
+from .noise import DeviceGenerator
+
+BF16 = torch.bfloat16
+F32 = torch.float32
+
+BUFFER_NUMEL = 2 ** 28   # eggroll.py:35 NOISE
+SEED = 0                 # eggroll.py:29
+
+
+def _view(t, sm, st):
+    return _lib.View(t.data_ptr(), sm, st)
+
+
+class KernelTimer:
+    """Records HIP events around every library launch of the forward on torch's current stream (the
+    stream the kernels run on): name -> list of (start, end) event pairs, tagged with a caller label."""
+
+    def __init__(self):
+        self.events = []
+        self.label = None
+
+    def call(self, name, *args):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        _lib.call(name, *args)
+        e.record()
+        self.events.append((name, self.label, s, e))
+
+    def totals(self):
+        """(name, label) -> (launches, total ms), after a synchronize."""
+        out = {}
+        for name, label, s, e in self.events:
+            n, t = out.get((name, label), (0, 0.0))
+            out[(name, label)] = (n + 1, t + s.elapsed_time(e))
+        return out
+
+
+_TIMER = None
+
+
+def set_timer(timer):
+    """Install (or clear, with None) a KernelTimer for subsequent population_forward calls."""
+    global _TIMER
+    _TIMER = timer
+
+
+def _call(name, *args, label=None):
+    if _TIMER is None:
+        return _lib.call(name, *args)
+    _TIMER.label = label
+    return _TIMER.call(name, *args)
+
+
+def _rank1(pair):
+    """noise_rank1_t of an (a, b) pair of [dirs, out] / [dirs, in] fp32 row views (None: unperturbed)."""
+    if pair is None:
+        return _lib.Rank1(None, None, 0, 0)
+    a, b = pair
+    for t in (a, b):
+        if t.dtype != F32 or t.stride(-1) != 1 or t.data_ptr() % 16 or t.stride(0) % 4:
+            raise ValueError('noise rows must be fp32, 16 B aligned, unit inner stride')
+    return _lib.Rank1(a.data_ptr(), b.data_ptr(), a.stride(0), b.stride(0))
+
+
+def _rank1_array(pairs):
+    arr = (_lib.Rank1 * len(pairs))()
+    for i, pr in enumerate(pairs):
+        arr[i] = _rank1(pr)
+    return arr
+
+
+class Weights:
+    """Device copies of a parameter dict in the layouts the kernels read (bf16 matrices, fp32 tables),
+    built once per parameter update. Names are the reference's state-dict names (utils/model.py)."""
+
+    def __init__(self, p, device=None, n_layer=8, fp32_head=False):
+        dev = torch.device(device) if device is not None else p['lm_head.weight'].device
+        if dev.type != 'cuda':
+            raise ValueError('population_loss runs on the GPU')
+        self.device, self.n_layer = dev, n_layer
+        g = lambda n: p[n].detach().to(dev)
+        bf = lambda n: g(n).to(BF16).contiguous()
+        self.wte = g('transformer.wte.weight').to(F32).contiguous()
+        self.lm_head = bf('lm_head.weight')
+        self.fp32_head = fp32_head
+        if fp32_head:
+            w = g('lm_head.weight').to(F32).contiguous()
+            self.lm_head3 = torch.empty(w.shape[0], 3 * w.shape[1], dtype=BF16, device=dev)
+            _lib.call('noise_split3', w.data_ptr(), w.shape[0], w.shape[1], 0, 1, self.lm_head3.data_ptr(),
+                      _lib.stream_ptr(dev))
+        lam = torch.stack([p['resid_lambdas'].detach().float().cpu(), p['x0_lambdas'].detach().float().cpu()])
+        self.resid_lambdas, self.x0_lambdas = lam[0].tolist(), lam[1].tolist()
+        self.blocks = []
+        for i in range(n_layer):
+            pre = f'transformer.h.{i}.'
+            blk = dict(q=bf(pre + 'attn.c_q.weight'), k=bf(pre + 'attn.c_k.weight'), v=bf(pre + 'attn.c_v.weight'),
+                       o=bf(pre + 'attn.c_proj.weight'), fc=bf(pre + 'mlp.c_fc.weight'),
+                       mp=bf(pre + 'mlp.c_proj.weight'))
+            if has_ve(i, n_layer):
+                blk['gate'] = g(pre + 'attn.ve_gate.weight').to(F32).contiguous()
+                blk['ve'] = g(f'value_embeds.{i}.weight').to(F32).contiguous()
+            self.blocks.append(blk)
+        self.windows = window_sizes(n_layer)
+
+
+class _Buffers:
+    def __init__(self, m, T, dev, fp32_head, per_member):
+        rows = m * T
+        e = m if per_member else 1
+        self.x0 = torch.empty(e, T, N_EMBD, dtype=F32, device=dev)
+        self.xin0 = torch.empty(e, T, N_EMBD, dtype=F32, device=dev)
+        self.h0 = torch.empty(e, T, N_EMBD, dtype=BF16, device=dev)
+        self.resid = torch.empty(m, T, N_EMBD, dtype=F32, device=dev)
+        self.h = torch.empty(m, T, N_EMBD, dtype=BF16, device=dev)
+        self.qkv = torch.empty(3, m, N_HEAD, T, HEAD_DIM, dtype=BF16, device=dev)
+        self.y = torch.empty(m, T, N_EMBD, dtype=BF16, device=dev)
+        self.act = torch.empty(m, T, 4 * N_EMBD, dtype=BF16, device=dev)
+        self.h3 = torch.empty(m, T, 3 * N_EMBD, dtype=BF16, device=dev) if fp32_head else None
+        self.d_qkv = torch.empty(rows, 3, dtype=F32, device=dev)
+        self.d_attn = torch.empty(rows, N_HEAD, dtype=F32, device=dev)
+        self.d_fc = torch.empty(rows, dtype=F32, device=dev)
+        self.d_mp = torch.empty(rows, 16, dtype=F32, device=dev)
+        self.d_head = torch.empty(rows, 1, dtype=F32, device=dev)
+        self.loss_tok = torch.empty(rows, dtype=F32, device=dev)
+
+
+_ZERO_ROWS = {}
+
+
+def _zero_b(dev, width):
+    """A single zero row with stride 0: the b of an unperturbed matrix whose dot slot must still exist."""
+    key = (dev, width)
+    if key not in _ZERO_ROWS:
+        _ZERO_ROWS[key] = torch.zeros(width, dtype=F32, device=dev)
+    z = _ZERO_ROWS[key]
+    return _lib.Rank1(None, z.data_ptr(), 0, 0)
+
+
+def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffers=None):
+    """Per-member mean cross-entropy [m] of the perturbed models (eggroll.py:66-103 semantics).
+
+    W: Weights. noise: name -> (a [dirs, out], b [dirs, in]) fp32 row views for matrices and embeddings,
+    or eps [dirs, L] for 'resid_lambdas' / 'x0_lambdas'; absent names are unperturbed. sign: [m] fp32
+    (+-sigma). Member m uses noise row m // dir_div. idx, targets: [T] int64 token ids shared by all
+    members."""
+    dev = W.device
+    m, T = sign.shape[0], idx.shape[0]
+    if T % 256:
+        raise ValueError(f'sequence length must be a multiple of 256, got {T}')
+    sign = sign.to(device=dev, dtype=F32).contiguous()
+    idx = idx.to(device=dev, dtype=torch.int64).contiguous()
+    targets = targets.to(device=dev, dtype=torch.int64).contiguous()
+    stream = _lib.stream_ptr(dev)
+    pop = _lib.Population(m, T, sign.data_ptr(), dir_div)
+    popp = ctypes.byref(pop)
+    if rope is None:
+        cos, sin = rotary_tables(T)
+        rope = (cos.to(dev).contiguous(), sin.to(dev).contiguous())
+    cos_t, sin_t = rope
+    L = W.n_layer
+    E = N_EMBD
+
+    def nz(name):
+        v = noise.get(name)
+        return v
+
+    eps_r, eps_x = nz('resid_lambdas'), nz('x0_lambdas')
+    emb = nz('transformer.wte.weight')
+    per_member = emb is not None or eps_r is not None or eps_x is not None
+    B = buffers if buffers is not None else _Buffers(m, T, dev, W.fp32_head, per_member)
+    # block 0 entry: embedding, norm, mix, norm (shared by every member when nothing there is perturbed)
+    emb_r1 = _rank1(emb)
+    _call('noise_pop_embed', popp, 1 if per_member else 0, W.wte.data_ptr(), idx.data_ptr(),
+              ctypes.byref(emb_r1), W.resid_lambdas[0], W.x0_lambdas[0],
+              None if eps_r is None else eps_r.data_ptr(), None if eps_x is None else eps_x.data_ptr(),
+              0 if eps_r is None and eps_x is None else (eps_r if eps_r is not None else eps_x).stride(0),
+              B.x0.data_ptr(), B.xin0.data_ptr(), B.h0.data_ptr(), stream)
+    sm_e = T * E if per_member else 0
+    eps_ptr = lambda e, i: None if e is None else e[:, i].data_ptr()
+    eps_stride = (eps_r if eps_r is not None else eps_x).stride(0) if (eps_r is not None or eps_x is not None) else 0
+
+    def qkv_noise(i):
+        pre = f'transformer.h.{i}.'
+        return [nz(pre + 'attn.c_q.weight'), nz(pre + 'attn.c_k.weight'), nz(pre + 'attn.c_v.weight')]
+
+    def dot_vecs(pairs, width):
+        arr = (_lib.Rank1 * len(pairs))()
+        for k, pr in enumerate(pairs):
+            arr[k] = _rank1(pr) if pr is not None else _zero_b(dev, width)
+        return arr
+
+    # q/k/v dots of block 0
+    n0 = qkv_noise(0)
+    if any(v is not None for v in n0):
+        _call('noise_member_dots', popp, _view(B.h0, sm_e, E), E, dot_vecs(n0, E), 3, B.d_qkv.data_ptr(), stream)
+
+    qkv_out = (ctypes.c_void_p * 3)(*(B.qkv[i].data_ptr() for i in range(3)))
+    for i in range(L):
+        pre = f'transformer.h.{i}.'
+        blk = W.blocks[i]
+        nq = qkv_noise(i)
+        x_in = _view(B.h0, sm_e, E) if i == 0 else _view(B.h, T * E, E)
+        ws = (ctypes.c_void_p * 3)(blk['q'].data_ptr(), blk['k'].data_ptr(), blk['v'].data_ptr())
+        gate_r1 = _rank1(nz(pre + 'attn.ve_gate.weight'))
+        ve_r1 = _rank1(nz(f'value_embeds.{i}.weight'))
+        _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
+                  sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(),
+                  blk['gate'].data_ptr() if 'gate' in blk else None, ctypes.byref(gate_r1), ctypes.byref(ve_r1),
+                  qkv_out, stream)
+        # attention; its epilogue also forms y . b_o per head for c_proj's rank-1 term
+        no = nz(pre + 'attn.c_proj.weight')
+        q4, k4, v4 = (B.qkv[j].transpose(1, 2) for j in range(3))  # [m, T, H, D] views of [m, H, T, D]
+        yv = B.y.view(m, T, N_HEAD, HEAD_DIM)
+        _call('noise_attention_fwd', q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), yv.data_ptr(), m, N_HEAD, T,
+                  HEAD_DIM, q4.stride(0), q4.stride(2), q4.stride(1), k4.stride(0), k4.stride(2), k4.stride(1),
+                  v4.stride(0), v4.stride(2), v4.stride(1), 0, yv.stride(0), yv.stride(2), yv.stride(1),
+                  W.windows[i], 1.0 / math.sqrt(HEAD_DIM), None if no is None else no[1].data_ptr(),
+                  0 if no is None else no[1].stride(0), dir_div, None if no is None else B.d_attn.data_ptr(),
+                  stream, label=f'window {W.windows[i]}')
+        # attn.c_proj + residual; h = norm(x_mid); c_fc dot
+        nfc, nmp = nz(pre + 'mlp.c_fc.weight'), nz(pre + 'mlp.c_proj.weight')
+        o_r1 = _rank1(no)
+        xres = _view(B.xin0, sm_e, E) if i == 0 else _view(B.resid, T * E, E)
+        nxt = dot_vecs([nfc], E) if nfc is not None else None
+        _call('noise_pop_residual', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), E, ctypes.byref(o_r1),
+                  B.d_attn.data_ptr(), N_HEAD, N_HEAD, xres, B.resid.data_ptr(), 0, 0.0, 0.0, None, None, 0,
+                  _view(B.x0, sm_e, E), B.h.data_ptr(), 0, nxt, 1 if nfc is not None else 0,
+                  B.d_fc.data_ptr(), stream, label='attn.c_proj')
+        # mlp.c_fc, ReLU^2; partial dots for mlp.c_proj
+        fc_r1 = _rank1(nfc)
+        mp_next = _rank1(nmp)
+        _call('noise_pop_fc', popp, _view(B.h, T * E, E), blk['fc'].data_ptr(), ctypes.byref(fc_r1),
+                  B.d_fc.data_ptr(), B.act.data_ptr(), ctypes.byref(mp_next) if nmp is not None else None,
+                  B.d_mp.data_ptr(), stream)
+        # mlp.c_proj + residual; next block's mix, norm and q/k/v dots (or the head input)
+        mp_r1 = _rank1(nmp)
+        last = i == L - 1
+        if not last:
+            nn = qkv_noise(i + 1)
+            want = any(v is not None for v in nn)
+            nxt, nnext, ndots = (dot_vecs(nn, E), 3, B.d_qkv.data_ptr()) if want else (None, 0, None)
+            _call('noise_pop_residual', popp, _view(B.act, T * 4 * E, 4 * E), blk['mp'].data_ptr(), 4 * E,
+                  ctypes.byref(mp_r1), B.d_mp.data_ptr(), 16, 16, _view(B.resid, T * E, E), B.resid.data_ptr(),
+                  1, W.resid_lambdas[i + 1], W.x0_lambdas[i + 1], eps_ptr(eps_r, i + 1), eps_ptr(eps_x, i + 1),
+                  eps_stride, _view(B.x0, sm_e, E), B.h.data_ptr(), 0, nxt, nnext, ndots, stream, label='mlp.c_proj')
+        else:
+            nh = nz('lm_head.weight')
+            nxt, nnext, ndots = (dot_vecs([nh], E), 1, B.d_head.data_ptr()) if nh is not None else (None, 0, None)
+            hout = B.h3 if W.fp32_head else B.h
+            _call('noise_pop_residual', popp, _view(B.act, T * 4 * E, 4 * E), blk['mp'].data_ptr(), 4 * E,
+                  ctypes.byref(mp_r1), B.d_mp.data_ptr(), 16, 16, _view(B.resid, T * E, E), None, 0, 0.0, 0.0,
+                  None, None, 0, _view(B.x0, sm_e, E), hout.data_ptr(), 1 if W.fp32_head else 0, nxt, nnext,
+                  ndots, stream, label='mlp.c_proj')
+    nh = nz('lm_head.weight')
+    head_r1 = _rank1(nh)
+    if W.fp32_head:
+        hx, hw, K = _view(B.h3, T * 3 * E, 3 * E), W.lm_head3, 3 * E
+    else:
+        hx, hw, K = _view(B.h, T * E, E), W.lm_head, E
+    _call('noise_pop_head_ce', popp, hx, hw.data_ptr(), K, VOCAB, ctypes.byref(head_r1), B.d_head.data_ptr(),
+              targets.data_ptr(), 0, B.loss_tok.data_ptr(), stream)
+    out = torch.empty(m, dtype=F32, device=dev)
+    _call('noise_member_mean', B.loss_tok.data_ptr(), m, T, out.data_ptr(), stream)
+    return out
+
+
+def population_loss(model, p, noise, sign, idx, targets, dir_div=1, fp32_head=False):
+    """eggroll.py:66-103 `population_loss(model, p, noise, sign, idx, targets)` on the GPU.
+
+    noise values may be per member (dir_div = 1, as the reference passes them after repeat_interleave)
+    or per direction with dir_div = 2 (member m uses row m // 2)."""
+    W = Weights(p, fp32_head=fp32_head, n_layer=model.config.n_layer if model is not None else 8)
+    return population_forward(W, noise, sign, idx, targets, dir_div=dir_div)
+
+
+def _pop(m, T, sign, dir_div):
+    return _lib.Population(m, T, None if sign is None else sign.data_ptr(), dir_div)
+
+
+def lowrank(x, weight, a, b, sign, dir_div=1):
+    """eggroll.py:56-58: x [m, T, in] through W [out, in] + sign * a b^T per member, never materialised.
+
+    a [dirs, out], b [dirs, in] fp32 rows, member m uses row m // dir_div; sign [m]. x may broadcast over
+    members (stride 0 in dim 0): then x W^T is computed once and the rank-1 terms are streamed out.
+    Returns fp32 [m, T, out] (the reference's autocast promotion of the bf16 product plus the fp32
+    correction). in must be a multiple of 512, out of 256, T of 256."""
+    m, T, n_in = x.shape
+    n_out = weight.shape[0]
+    dev = x.device
+    if n_in % 512 or n_out % 256 or T % 256:
+        raise ValueError(f'lowrank: need in % 512 == 0, out % 256 == 0, T % 256 == 0; got {tuple(x.shape)} x {tuple(weight.shape)}')
+    sign = sign.to(device=dev, dtype=F32).contiguous()
+    a = a if (a.dtype == F32 and a.stride(-1) == 1 and a.data_ptr() % 16 == 0 and a.stride(0) % 4 == 0) else a.float().contiguous()
+    b = b if (b.dtype == F32 and b.stride(-1) == 1 and b.data_ptr() % 16 == 0 and b.stride(0) % 4 == 0) else b.float().contiguous()
+    r1 = _rank1((a, b))
+    stream = _lib.stream_ptr(dev)
+    shared = x.stride(0) == 0
+    xb = x[:1] if shared else x
+    xb = xb.to(BF16)
+    if xb.stride(-1) != 1 or xb.stride(1) % 8 or xb.data_ptr() % 16 or (not shared and xb.stride(0) % 8):
+        xb = xb.contiguous()
+    xs_m = 0 if shared else xb.stride(0)
+    w = weight.to(device=dev, dtype=BF16).contiguous()
+    pop = _pop(m, T, sign, dir_div)
+    dots = torch.empty(m * T, dtype=F32, device=dev)
+    _lib.call('noise_member_dots', ctypes.byref(pop), _lib.View(xb.data_ptr(), xs_m, xb.stride(1)), n_in,
+              ctypes.byref(r1), 1, dots.data_ptr(), stream)
+    y = torch.empty(m, T, n_out, dtype=F32, device=dev)
+    if shared:
+        base = torch.empty(1, T, n_out, dtype=F32, device=dev)
+        one = _pop(1, T, None, 1)
+        _lib.call('noise_pop_linear', ctypes.byref(one), _lib.View(xb.data_ptr(), 0, xb.stride(1)), w.data_ptr(),
+                  n_in, n_out, None, None, base.data_ptr(), 1, T * n_out, n_out, stream)
+        _lib.call('noise_rank1_expand', ctypes.byref(pop), base.data_ptr(), n_out, dots.data_ptr(), ctypes.byref(r1),
+                  y.data_ptr(), 1, stream)
+    else:
+        _lib.call('noise_pop_linear', ctypes.byref(pop), _lib.View(xb.data_ptr(), xs_m, xb.stride(1)), w.data_ptr(),
+                  n_in, n_out, ctypes.byref(r1), dots.data_ptr(), y.data_ptr(), 1, T * n_out, n_out, stream)
+    return y
+
+
+def lowrank_embed(weight, a, b, idx, sign, dir_div=1):
+    """eggroll.py:61-63: embedding rows of W [V, d] + sign * a b^T for token ids idx [T] -> fp32 [m, T, d]."""
+    dev = weight.device
+    V, d = weight.shape
+    m, T = sign.shape[0], idx.shape[0]
+    w = weight.to(F32).contiguous()
+    sign = sign.to(device=dev, dtype=F32).contiguous()
+    idx = idx.to(device=dev, dtype=torch.int64).contiguous()
+    a = a.float().contiguous()
+    b = b.float().contiguous()
+    out = torch.empty(m, T, d, dtype=F32, device=dev)
+    r1 = _rank1((a, b))
+    _lib.call('noise_lowrank_embed', out.data_ptr(), w.data_ptr(), V, d, idx.data_ptr(),
+              ctypes.byref(_pop(m, T, sign, dir_div)), ctypes.byref(r1), _lib.stream_ptr(dev))
+    return out
+
+
+class Eggroll:
+    """EGGROLL's perturbation bookkeeping (eggroll.py:106-128) over the virtual noise buffer.
+
+    The reference draws buffer = torch.randn(2**28) once (1 GiB of HBM) and slices each direction's a, b
+    at per-step offsets. Here the buffer is a Draw: every slice is regenerated from the Philox counter,
+    bit-identical to the reference's buffer on the same GPU, and nothing is materialised beyond the
+    requested rows."""
+
+    def __init__(self, model, pairs, rank=0, world=1, seed=SEED, noise_numel=BUFFER_NUMEL):
+        self.model, self.pairs, self.rank, self.world = model, pairs, rank, world
+        self.params = dict(model.named_parameters())
+        self.device = next(iter(self.params.values())).device
+        self.seed, self.noise_numel = seed, noise_numel
+        self.buffer = DeviceGenerator(seed, self.device).take(noise_numel)
+
+    def offsets(self, step):
+        """eggroll.py:117-120: one randint draw of [pairs] per parameter, in named_parameters order."""
+        g = DeviceGenerator(1_000_003 * self.seed + step, self.device)
+        return {name: g.randint(0, self.noise_numel - sum(p.shape), (self.pairs,)) for name, p in self.params.items()}
+
+    def noise(self, offsets, directions):
+        """eggroll.py:122-128: name -> (a [n, out], b [n, in]) for matrices and embeddings, eps [n, L]."""
+        out = {}
+        for name, p in self.params.items():
+            rows = self.buffer.gather(offsets[name], sum(p.shape), rows=directions)
+            out[name] = tuple(rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
+        return out
+
+    def population(self, step, x, y, weights=None, chunk=512, names=None, fp32_head=False):
+        """This rank's population losses for one update (the hot loop of eggroll.py:133-146): members
+        [rank * per_rank, (rank + 1) * per_rank), member g on direction (g mod 2P) // 2 with sign
+        +sigma for even g and -sigma for odd g, sequence g // per_seq. names restricts which parameters
+        are perturbed (None: all, as the reference)."""
+        pairs = self.pairs
+        members = max(2 * pairs, 2 * len(x))
+        per_seq, per_rank = members // len(x), members // self.world
+        offsets = self.offsets(step)
+        if names is not None:
+            offsets = {n: o for n, o in offsets.items() if n in names}
+        W = weights if weights is not None else Weights(self.params, fp32_head=fp32_head)
+        losses = torch.empty(per_rank, device=self.device)
+        for start in range(self.rank * per_rank, (self.rank + 1) * per_rank, chunk):
+            n = min(chunk, (self.rank + 1) * per_rank - start)
+            directions = torch.arange(start, start + n, 2, device=self.device) % (2 * pairs) // 2
+            noise = {}
+            for name, o in offsets.items():
+                p = self.params[name]
+                rows = self.buffer.gather(o, sum(p.shape), rows=directions)
+                noise[name] = tuple(rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
+            sign = torch.tensor([SIGMA, -SIGMA], device=self.device).repeat(n // 2)
+            seq = start // per_seq
+            losses[start - self.rank * per_rank:start - self.rank * per_rank + n] = population_forward(
+                W, noise, sign, x[seq], y[seq], dir_div=2)
+        return losses
+
+
+SIGMA = 0.002   # eggroll.py:31

@@ -1,14 +1,135 @@
-"""The fixed model's ops on libnoise_amd, with utils/model.py's call signatures.
+"""The fixed model on libnoise_amd, with utils/model.py's names and call signatures.
 
 attention(q, k, v, window)  replaces utils/model.py:24-31 (flex_attention over the window block mask).
+GPTConfig / GPT / make_model hold the same parameters under the same state-dict names as
+utils/model.py:34-175 and train/val/eggroll.py:38-53, so weights load strictly either way.
 """
 import math
+from dataclasses import dataclass
 
 import torch
+from torch import nn
 
 from . import _lib
 
 BF16 = torch.bfloat16
+N_LAYER, N_HEAD, HEAD_DIM, N_EMBD, VOCAB, SEQ = 8, 8, 64, 512, 4096, 2048
+
+
+@dataclass
+class GPTConfig:
+    """utils/model.py:34-43."""
+    sequence_len: int = 2048
+    vocab_size: int = 4096
+    n_layer: int = 8
+    n_head: int = 8
+    n_kv_head: int = 8
+    n_embd: int = 512
+    window_pattern: str = 'SSSL'
+
+
+def has_ve(layer_idx, n_layer=N_LAYER):
+    """Value embeddings on every other block, counting back from the last (model.py:50-52)."""
+    return layer_idx % 2 == (n_layer - 1) % 2
+
+
+def window_sizes(n_layer=N_LAYER, sequence_len=SEQ, pattern='SSSL'):
+    """Left window per block (model.py:185-191): 'S' = half the sequence, 'L' = all of it; last is L."""
+    pattern = pattern.upper()
+    sizes = [sequence_len if pattern[i % len(pattern)] == 'L' else sequence_len // 2 for i in range(n_layer)]
+    sizes[-1] = sequence_len
+    return sizes
+
+
+def rotary_tables(length, head_dim=HEAD_DIM, base=10000):
+    """cos, sin [length, head_dim/2] fp32 holding the bf16 tables of model.py:177-183 (fp32 angles
+    t * base^(-2i/d), cos/sin rounded to bf16)."""
+    inv_freq = 1.0 / base ** (torch.arange(0, head_dim, 2, dtype=torch.float32) / head_dim)
+    angles = torch.outer(torch.arange(length, dtype=torch.float32), inv_freq)
+    return angles.cos().bfloat16().float(), angles.sin().bfloat16().float()
+
+
+class _Attn(nn.Module):
+    def __init__(self, cfg, layer_idx):
+        super().__init__()
+        d, kv = cfg.n_embd, cfg.n_kv_head * (cfg.n_embd // cfg.n_head)
+        self.c_q = nn.Linear(d, d, bias=False)
+        self.c_k = nn.Linear(d, kv, bias=False)
+        self.c_v = nn.Linear(d, kv, bias=False)
+        self.c_proj = nn.Linear(d, d, bias=False)
+        self.ve_gate = nn.Linear(32, cfg.n_kv_head, bias=False) if has_ve(layer_idx, cfg.n_layer) else None
+
+
+class _MLP(nn.Module):
+    def __init__(self, cfg):
+        super().__init__()
+        self.c_fc = nn.Linear(cfg.n_embd, 4 * cfg.n_embd, bias=False)
+        self.c_proj = nn.Linear(4 * cfg.n_embd, cfg.n_embd, bias=False)
+
+
+class _Block(nn.Module):
+    def __init__(self, cfg, layer_idx):
+        super().__init__()
+        self.attn = _Attn(cfg, layer_idx)
+        self.mlp = _MLP(cfg)
+
+
+class GPT(nn.Module):
+    """Parameter container of the fixed model (model.py:122-147), same names and shapes. The forward
+    lives in population_loss / gpt_loss (noise_amd.eggroll)."""
+
+    def __init__(self, config, pad_vocab_size_to=64):
+        super().__init__()
+        self.config = config
+        self.window_sizes = [(w, 0) for w in window_sizes(config.n_layer, config.sequence_len, config.window_pattern)]
+        vocab = -(-config.vocab_size // pad_vocab_size_to) * pad_vocab_size_to
+        self.transformer = nn.ModuleDict({
+            'wte': nn.Embedding(vocab, config.n_embd),
+            'h': nn.ModuleList([_Block(config, i) for i in range(config.n_layer)]),
+        })
+        self.lm_head = nn.Linear(config.n_embd, vocab, bias=False)
+        self.resid_lambdas = nn.Parameter(torch.ones(config.n_layer))
+        self.x0_lambdas = nn.Parameter(torch.zeros(config.n_layer))
+        kv = config.n_kv_head * (config.n_embd // config.n_head)
+        self.value_embeds = nn.ModuleDict({str(i): nn.Embedding(vocab, kv)
+                                           for i in range(config.n_layer) if has_ve(i, config.n_layer)})
+
+    @torch.no_grad()
+    def init_weights(self):
+        """model.py:149-175's draws, in its order, on this module's device generator."""
+        s = 3 ** 0.5 * self.config.n_embd ** -0.5
+        nn.init.normal_(self.transformer.wte.weight, mean=0.0, std=1.0)
+        nn.init.normal_(self.lm_head.weight, mean=0.0, std=0.001)
+        for blk in self.transformer.h:
+            for lin in (blk.attn.c_q, blk.attn.c_k, blk.attn.c_v):
+                nn.init.uniform_(lin.weight, -s, s)
+            nn.init.zeros_(blk.attn.c_proj.weight)
+            nn.init.uniform_(blk.mlp.c_fc.weight, -s, s)
+            nn.init.zeros_(blk.mlp.c_proj.weight)
+        self.resid_lambdas.fill_(1.0)
+        self.x0_lambdas.fill_(0.1)
+        for emb in self.value_embeds.values():
+            nn.init.uniform_(emb.weight, -s, s)
+        for blk in self.transformer.h:
+            if blk.attn.ve_gate is not None:
+                nn.init.zeros_(blk.attn.ve_gate.weight)
+
+
+def make_model(device='cpu', seed=0):
+    """The training scripts' model (eggroll.py:38-53, run.py:545-557): seeded init_weights, then the
+    output projections (every '*c_proj' Linear, in module order) re-drawn U(+-1.5 sqrt(3 / fan_in));
+    embeddings kept in fp32. Built on `device` (CPU: torch's CPU generator)."""
+    torch.manual_seed(seed)
+    with torch.device('meta'):
+        model = GPT(GPTConfig())
+    model.to_empty(device=device)
+    model.init_weights()
+    with torch.no_grad():
+        for name, module in model.named_modules():
+            if 'c_proj' in name and isinstance(module, nn.Linear):
+                bound = 1.5 * (3 / module.weight.shape[1]) ** 0.5
+                nn.init.uniform_(module.weight, -bound, bound)
+    return model.requires_grad_(False)
 
 
 def _operand(t):

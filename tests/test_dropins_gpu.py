@@ -1,0 +1,110 @@
+"""The reference's call-site functions on the GPU vs the oracle / torch's own generators.
+
+lowrank (eggroll.py:56-58), lowrank_embed (61-63), head_loss (run.py:89-94), Eggroll.offsets / noise
+(eggroll.py:117-128).
+"""
+import pytest
+import torch
+
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device('cuda', 0)
+
+
+def bits(t):
+    return t.contiguous().view(torch.int32)
+
+
+@pytest.mark.parametrize('shared', [False, True])
+def test_lowrank_vs_oracle(shared):
+    """y = x W^T + sign (x b) a^T; bf16 operands, fp32 output. Tolerance: 1e-2 of the output's max
+    magnitude (bf16 inputs), and the rank-1 term itself to 2e-2 of its scale."""
+    from noise_amd.eggroll import lowrank
+    g = torch.Generator().manual_seed(0)
+    m, T, n_in, n_out = 4, 512, 512, 2048
+    # per-member x, equal within each antithetic pair (as members of a pair see one sequence)
+    x = torch.randn(1 if shared else m // 2, T, n_in, generator=g)
+    x = x.expand(m, T, n_in) if shared else x.repeat_interleave(2, 0)
+    w = torch.randn(n_out, n_in, generator=g) * 0.02
+    a, b = torch.randn(m // 2, n_out, generator=g), torch.randn(m // 2, n_in, generator=g)
+    sign = torch.tensor([1e-2, -1e-2] * (m // 2))
+    xd = x.to(DEV) if not shared else x[:1].to(DEV).expand(m, T, n_in)
+    y = lowrank(xd, w.to(DEV), a.to(DEV), b.to(DEV), sign.to(DEV), dir_div=2).cpu()
+    xr = x.bfloat16().float()
+    ref = om.lowrank(xr, w.bfloat16().float(), a.repeat_interleave(2, 0), b.repeat_interleave(2, 0), sign)
+    scale = ref.abs().max()
+    assert (y - ref).abs().max() <= 1e-2 * scale
+    # antithetic: y+ + y- = 2 x W^T (the rank-1 terms cancel) and y+ - y- = 2 sigma (x b) a^T
+    d = (y[0] - y[1]) / 2
+    rank1 = 1e-2 * (xr[0] @ b[0])[:, None] * a[0][None, :]
+    assert (d - rank1).abs().max() <= 2e-2 * rank1.abs().max()
+
+
+def test_lowrank_embed_exact():
+    from noise_amd.eggroll import lowrank_embed
+    g = torch.Generator().manual_seed(1)
+    W = torch.randn(4096, 512, generator=g)
+    a, b = torch.randn(3, 4096, generator=g), torch.randn(3, 512, generator=g)
+    idx = torch.randint(0, 4096, (300,), generator=g)
+    sign = torch.tensor([0.1, -0.2, 0.3])
+    out = lowrank_embed(W.to(DEV), a.to(DEV), b.to(DEV), idx.to(DEV), sign.to(DEV)).cpu()
+    ref = om.lowrank_embed(W, a, b, idx, sign)
+    assert torch.allclose(out, ref, rtol=1e-6, atol=1e-6)
+
+
+def test_head_loss_fp32_precision():
+    """Large logits (|z| up to the cap): split-bf16x3 matches the fp32 oracle to 2e-4 per token, where a
+    plain bf16 head is off by far more (checked) -- the test discriminates the two."""
+    from noise_amd.dust import head_loss
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(3, 512, 512, generator=g)
+    w = torch.randn(4096, 512, generator=g) * 0.3
+    y = torch.randint(0, 4096, (3, 512), generator=g)
+    y[0, :7] = -1
+    got = head_loss(x.to(DEV), w.to(DEV), y.to(DEV), 4096).cpu()
+    ref = om.head_loss(x, w, y)
+    assert got.shape == ref.shape == (3 * 512,)
+    assert (got - ref).abs().max() <= 2e-4
+    assert (got.view(3, 512)[0, :7] == 0).all()
+    bf16_ref = om.softcap_ce((om.norm(x).bfloat16().float() @ w.bfloat16().float().t()), y, 'none')
+    assert (bf16_ref - ref).abs().max() > 10 * 2e-4
+
+
+def test_head_loss_ragged_rows():
+    from noise_amd.dust import head_loss
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(1, 100, 512, generator=g)
+    w = torch.randn(4096, 512, generator=g) * 0.05
+    y = torch.randint(0, 4096, (1, 100), generator=g)
+    got = head_loss(x.to(DEV), w.to(DEV), y.to(DEV), 4096).cpu()
+    assert (got - om.head_loss(x, w, y)).abs().max() <= 2e-4
+
+
+def test_eggroll_offsets_and_noise_bit_exact():
+    """Offsets = torch.randint on a cuda generator seeded 1_000_003*SEED + step, one draw per parameter in
+    named_parameters order; noise rows = the reference buffer's slices. Checked against torch's own device
+    draws (the buffer materialised here only as the reference)."""
+    from noise_amd.eggroll import Eggroll
+    from noise_amd.model import make_model
+    model = make_model('cpu', 0).to(DEV)
+    pairs = 512
+    es = Eggroll(model, pairs)
+    offs = es.offsets(3)
+    g = torch.Generator(DEV).manual_seed(1_000_003 * 0 + 3)
+    params = dict(model.named_parameters())
+    NOISE = 2 ** 28
+    for name, p in params.items():
+        ref = torch.randint(0, NOISE - sum(p.shape), (pairs,), device=DEV, generator=g)
+        assert torch.equal(offs[name], ref), name
+    buffer = torch.randn(NOISE, device=DEV, generator=torch.Generator(DEV).manual_seed(0))
+    directions = torch.arange(256, 256 + 64, 2, device=DEV) % (2 * pairs) // 2
+    noise = es.noise(offs, directions)
+    for name in ('resid_lambdas', 'transformer.wte.weight', 'transformer.h.3.mlp.c_fc.weight', 'lm_head.weight',
+                 'value_embeds.7.weight', 'transformer.h.7.attn.ve_gate.weight'):
+        p = params[name]
+        rows = buffer[offs[name][directions, None] + torch.arange(sum(p.shape), device=DEV)]
+        ref = rows.split(list(p.shape), dim=1) if p.dim() == 2 else (rows,)
+        got = noise[name] if p.dim() == 2 else (noise[name],)
+        for r, o in zip(ref, got):
+            assert torch.equal(bits(o), bits(r)), name

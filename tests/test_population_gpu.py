@@ -1,0 +1,153 @@
+"""Population forward (eggroll.py:66-103) on the GPU vs the fp32 CPU oracle (oracle/model.py).
+
+Bar: per-member mean CE within 1e-3 absolute (BASELINE: per-member losses within 1e-3 of fp32), and the
+antithetic fitness L[2i+1] - L[2i] within 1e-3. At the seed-0 init the head is tiny (std 0.001) and
+every loss sits at ln 4096 whatever the blocks compute, so most cases also scale the head (x30: logits of
+order 1, the loss ~0.3 off ln 4096) to make the loss depend on the hidden state; a wrong block then moves
+the loss by far more than the tolerance. (With x300, bf16 rounding of the head's inputs alone moves the
+loss by ~2e-3, as it does in the reference's autocast head; that case runs on the fp32 head.)
+"""
+import math
+
+import pytest
+import torch
+
+from oracle import model as om
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device('cuda', 0)
+TOL = 1e-3
+
+
+@pytest.fixture(scope='module')
+def params():
+    from noise_amd.model import make_model
+    return {k: v.float() for k, v in make_model('cpu', 0).state_dict().items()}
+
+
+def scaled_head(P, factor):
+    Q = dict(P)
+    Q['lm_head.weight'] = P['lm_head.weight'] * factor
+    return Q
+
+
+def make_noise(P, names, dirs, seed):
+    """Per-direction (a, b) tables as [dirs, out + in] rows (the layout Eggroll.noise slices), CPU."""
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for n in names:
+        shape = P[n].shape
+        if len(shape) == 2:
+            rows = torch.randn(dirs, shape[0] + shape[1], generator=g)
+            out[n] = rows
+        else:
+            out[n] = torch.randn(dirs, shape[0], generator=g)
+    return out
+
+
+def split(P, tables, device):
+    res = {}
+    for n, rows in tables.items():
+        rows = rows.to(device).contiguous()
+        if P[n].dim() == 2:
+            o = P[n].shape[0]
+            res[n] = (rows[:, :o], rows[:, o:])
+        else:
+            res[n] = rows
+    return res
+
+
+def per_member(noise, rep):
+    return {n: (tuple(t.repeat_interleave(rep, 0) for t in v) if isinstance(v, tuple) else v.repeat_interleave(rep, 0))
+            for n, v in noise.items()}
+
+
+BLOCK_MATRICES = [f'transformer.h.{i}.{s}.weight' for i in range(8)
+                  for s in ('attn.c_q', 'attn.c_k', 'attn.c_v', 'attn.c_proj', 'mlp.c_fc', 'mlp.c_proj')]
+
+
+def run_both(P, names, m, T, sigma, seed=0, fp32_head=False, oracle_chunk=2):
+    from noise_amd.eggroll import Weights, population_forward
+    g = torch.Generator().manual_seed(100 + seed)
+    idx = torch.randint(0, 4096, (T + 1,), generator=g)
+    x, y = idx[:-1], idx[1:]
+    dirs = m // 2
+    tables = make_noise(P, names, dirs, seed)
+    sign = torch.tensor([sigma, -sigma]).repeat(dirs)
+    W = Weights({k: v.to(DEV) for k, v in P.items()}, fp32_head=fp32_head)
+    got = population_forward(W, split(P, tables, DEV), sign.to(DEV), x.to(DEV), y.to(DEV), dir_div=2).cpu()
+    ref = om.population_loss(P, per_member(split(P, tables, 'cpu'), 2), sign, x, y, members_per_chunk=oracle_chunk)
+    return got, ref
+
+
+def check(got, ref, tol=TOL):
+    assert torch.isfinite(got).all()
+    err = (got - ref).abs().max().item()
+    fit_err = ((got[1::2] - got[0::2]) - (ref[1::2] - ref[0::2])).abs().max().item()
+    print(f'max |loss - oracle| = {err:.3e}, fitness err {fit_err:.3e}, loss {ref.mean().item():.4f}')
+    assert err <= tol, f'max |loss - oracle| = {err:.3e}; got {got.tolist()} ref {ref.tolist()}'
+    assert fit_err <= tol, f'max fitness error {fit_err:.3e}'
+    return err, fit_err
+
+
+def test_unperturbed_scaled_head(params):
+    """sigma = 0: every member is GPT.forward's loss (model.py:193-209); head x30 so blocks matter."""
+    P = scaled_head(params, 30.0)
+    got, ref = run_both(P, [], 2, 512, 0.0)
+    check(got, ref)
+    assert abs(got[0] - got[1]) == 0
+    assert abs(ref[0].item() - math.log(4096)) > 0.05, 'scaled head must move the loss off ln V'
+
+
+def test_block_matrices_seed0_init(params):
+    """Config: rank-1 noise on the 48 block matrices, seed-0 init, antithetic pairs, sigma 0.002."""
+    got, ref = run_both(params, BLOCK_MATRICES, 4, 512, 0.002)
+    check(got, ref)
+    # init invariant: loss ~ ln 4096 (logits ~ 0 at init)
+    assert (got - math.log(4096)).abs().max() < 0.01
+
+
+def test_block_matrices_scaled_head_large_sigma(params):
+    """Large sigma and a scaled head: perturbation effects are many times the tolerance."""
+    P = scaled_head(params, 30.0)
+    got, ref = run_both(P, BLOCK_MATRICES, 4, 512, 0.02, seed=1)
+    check(got, ref)
+    assert (ref[1::2] - ref[0::2]).abs().max() > 5 * TOL, 'perturbations must be visible'
+
+
+def test_windows_full_length(params):
+    """T = 2048: the S blocks' 1024-token window is active; head scaled."""
+    P = scaled_head(params, 30.0)
+    got, ref = run_both(P, BLOCK_MATRICES, 2, 2048, 0.02, seed=2, oracle_chunk=1)
+    check(got, ref)
+
+
+def test_every_parameter_perturbed(params):
+    """EGGROLL perturbs all 60 parameters (eggroll.py:4-6): embeddings, lambdas, ve gates, value
+    embeddings and the head too."""
+    P = scaled_head(params, 30.0)
+    P = dict(P)
+    # non-zero gates so the gate path is exercised
+    for i in (1, 3, 5, 7):
+        P[f'transformer.h.{i}.attn.ve_gate.weight'] = torch.randn(8, 32, generator=torch.Generator().manual_seed(i)) * 0.3
+    got, ref = run_both(P, list(P.keys()), 4, 512, 0.01, seed=3)
+    check(got, ref)
+
+
+def test_fp32_head_split_bf16x3(params):
+    """run.py:273-278's fp32 head, as split-bf16x3 on MFMA, in the population path; x100 head."""
+    P = scaled_head(params, 100.0)
+    got, ref = run_both(P, BLOCK_MATRICES, 4, 512, 0.02, seed=4, fp32_head=True)
+    check(got, ref)
+
+
+def test_repeatable(params):
+    from noise_amd.eggroll import Weights, population_forward
+    P = scaled_head(params, 30.0)
+    tables = split(P, make_noise(P, BLOCK_MATRICES, 2, 5), DEV)
+    W = Weights({k: v.to(DEV) for k, v in P.items()})
+    idx = torch.randint(0, 4096, (257,), generator=torch.Generator().manual_seed(6)).to(DEV)
+    sign = torch.tensor([0.01, -0.01, 0.01, -0.01], device=DEV)
+    a = population_forward(W, tables, sign, idx[:-1], idx[1:], dir_div=2)
+    b = population_forward(W, tables, sign, idx[:-1], idx[1:], dir_div=2)
+    assert torch.equal(a, b)
