@@ -144,10 +144,13 @@ def main():
             tf = flops * n / (ms * 1e-3)
             entry.update(tflops=round(tf / 1e12, 1), mfma_frac=round(tf / BF16_PEAK, 4))
         kernels[key] = entry
-    dominant = max((k for k in kernels if 'tflops' in kernels[k]), key=lambda k: kernels[k]['ms_per_step'])
-    dk = kernels[dominant]
-    roofline = dict(bound='mfma', kernel=dominant, achieved=round(dk['tflops'], 1), peak=BF16_PEAK / 1e12,
-                    unit='TFLOP/s', frac=dk['mfma_frac'], traffic=None)
+    timed = [k for k in kernels if 'tflops' in kernels[k]]
+    roofline = None
+    if timed:
+        dominant = max(timed, key=lambda k: kernels[k]['ms_per_step'])
+        dk = kernels[dominant]
+        roofline = dict(bound='mfma', kernel=dominant, achieved=round(dk['tflops'], 1), peak=BF16_PEAK / 1e12,
+                        unit='TFLOP/s', frac=dk['mfma_frac'], traffic=None)
 
     algo_flops = 68_318_208 * members * TOKENS
     line = dict(

@@ -3,11 +3,13 @@
 There is no fallback: if the library is missing or does not load, every op raises.
 """
 import ctypes
+import os
 from pathlib import Path
 
 import torch
 
-LIB_PATH = Path(__file__).resolve().with_name('libnoise_amd.so')
+# NOISE_AMD_LIB: path of another build of the library (A/B timing of kernel variants)
+LIB_PATH = Path(os.environ.get('NOISE_AMD_LIB') or Path(__file__).resolve().with_name('libnoise_amd.so'))
 
 _p, _i64, _u64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
 

@@ -19,8 +19,6 @@
 namespace noise {
 namespace {
 
-constexpr int kBK = 64;
-constexpr int kLdsRow = 72;
 constexpr float kEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps, F.rms_norm's default
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -30,18 +28,24 @@ __device__ __forceinline__ float f4get(const float4 &v, int e) { return e == 0 ?
 
 // ------------------------------------------------------------------------------------------------
 // K loop: acc[fb][tb] += W[n0 + wn0 + 32fb + .., :] . X[t + wm0 + 32tb + .., :]
+// Two LDS stages of BN + BM rows x BK (rows padded by 8 bf16: conflict-free 16 B fragment reads). The
+// next k-step's tile is fetched into registers while the current stage feeds the MFMAs, then written to
+// the other stage; one barrier per k-step.
 // ------------------------------------------------------------------------------------------------
-template <int BN, int BM>
+template <int BN, int BM, int BK>
 struct Mma {
     static constexpr int WN = BN / 128;
     static constexpr int WM = BM / 128;
     static_assert(WN * WM == 4, "4 waves of 128 x 128");
-    static constexpr int CW = BN / 32;  // 16 B chunks per thread
-    static constexpr int CX = BM / 32;
+    static constexpr int LD = BK + 8;           // padded LDS row (bf16)
+    static constexpr int CPR = BK / 8;          // 16 B chunks per row
+    static constexpr int CW = BN * CPR / 256;   // chunks per thread
+    static constexpr int CX = BM * CPR / 256;
+    static constexpr int STAGE = (BN + BM) * LD;  // bf16 per stage
+    static constexpr int LDS_BYTES = 2 * STAGE * 2;
 
-    __device__ static void run(const __bf16 *W, int64_t ldw, const __bf16 *X, int64_t ldx, int K,
-                               __bf16 (*sW)[kLdsRow], __bf16 (*sX)[kLdsRow], f32x16 (&acc)[4][4], int tid,
-                               int wn0, int wm0) {
+    __device__ static void run(const __bf16 *W, int64_t ldw, const __bf16 *X, int64_t ldx, int K, __bf16 *lds,
+                               f32x16 (&acc)[4][4], int tid, int wn0, int wm0) {
         const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
@@ -52,56 +56,77 @@ struct Mma {
 #pragma unroll
             for (int i = 0; i < CW; ++i) {
                 int c = tid + 256 * i;
-                rw[i] = load_bf16x8(W + (int64_t)(c >> 3) * ldw + k0 + (c & 7) * 8);
+                rw[i] = load_bf16x8(W + (int64_t)(c / CPR) * ldw + k0 + (c % CPR) * 8);
             }
 #pragma unroll
             for (int i = 0; i < CX; ++i) {
                 int c = tid + 256 * i;
-                rx[i] = load_bf16x8(X + (int64_t)(c >> 3) * ldx + k0 + (c & 7) * 8);
+                rx[i] = load_bf16x8(X + (int64_t)(c / CPR) * ldx + k0 + (c % CPR) * 8);
             }
         };
-        auto store = [&]() {
+        auto store = [&](__bf16 *st) {
 #pragma unroll
             for (int i = 0; i < CW; ++i) {
                 int c = tid + 256 * i;
-                store_bf16x8(&sW[c >> 3][(c & 7) * 8], rw[i]);
+                store_bf16x8(st + (c / CPR) * LD + (c % CPR) * 8, rw[i]);
             }
 #pragma unroll
             for (int i = 0; i < CX; ++i) {
                 int c = tid + 256 * i;
-                store_bf16x8(&sX[c >> 3][(c & 7) * 8], rx[i]);
+                store_bf16x8(st + (BN + c / CPR) * LD + (c % CPR) * 8, rx[i]);
             }
         };
         load(0);
-        store();
+        store(lds);
         __syncthreads();
-        for (int k0 = 0; k0 < K; k0 += kBK) {
-            const bool more = k0 + kBK < K;
-            if (more) load(k0 + kBK);
-            // the 4 sub-steps stay a loop: unrolling them hoists all fragment loads and spills
+        int cur = 0;
+        for (int k0 = 0; k0 < K; k0 += BK) {
+            const bool more = k0 + BK < K;
+            if (more) load(k0 + BK);
+            const __bf16 *sw = lds + cur * STAGE;
+            const __bf16 *sx = sw + BN * LD;
+            // the sub-steps stay a loop: unrolling them hoists all fragment loads and spills
 #pragma unroll 1
-            for (int s = 0; s < 4; ++s) {
+            for (int s = 0; s < BK / 16; ++s) {
                 bf16x8 af[4], bf[4];
 #pragma unroll
-                for (int fb = 0; fb < 4; ++fb) af[fb] = load_bf16x8(&sW[wn0 + 32 * fb + j][16 * s + 8 * hf]);
+                for (int fb = 0; fb < 4; ++fb) af[fb] = load_bf16x8(sw + (wn0 + 32 * fb + j) * LD + 16 * s + 8 * hf);
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb) bf[tb] = load_bf16x8(&sX[wm0 + 32 * tb + j][16 * s + 8 * hf]);
+                for (int tb = 0; tb < 4; ++tb) bf[tb] = load_bf16x8(sx + (wm0 + 32 * tb + j) * LD + 16 * s + 8 * hf);
 #pragma unroll
                 for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
                     for (int tb = 0; tb < 4; ++tb) acc[fb][tb] = mfma32x32x16(af[fb], bf[tb], acc[fb][tb]);
             }
+            if (more) store(lds + (cur ^ 1) * STAGE);
             __syncthreads();
-            if (more) {
-                store();
-                __syncthreads();
-            }
+            cur ^= 1;
         }
     }
 };
 
 // feature offset (within a wave's 128) of accumulator register r of block fb for lane half hf
 __device__ __forceinline__ int feat(int fb, int r, int hf) { return 32 * fb + 8 * (r >> 2) + 4 * hf + (r & 3); }
+
+// Workgroup -> (token tile, feature tile). Workgroups are dispatched round-robin over the 8 XCDs, so the
+// feature tiles of one token tile are given consecutive slots of one XCD: its x rows are fetched into that
+// XCD's L2 once and re-read from there. Falls back to row-major order when token tiles are not a
+// multiple of 8.
+__device__ __forceinline__ void tile_order(int wg, int ntiles_n, int ntiles_t, int &tt, int &nt) {
+    if ((ntiles_t & 7) == 0) {
+        const int slot = wg >> 3;
+        nt = slot % ntiles_n;
+        tt = (slot / ntiles_n) * 8 + (wg & 7);
+    } else {
+        nt = wg % ntiles_n;
+        tt = wg / ntiles_n;
+    }
+}
+
+// Epilogue staging: each wave writes its finished 128 x 128 tile into a private LDS region (rows padded
+// to kStg) and re-reads it as 16 B row chunks, so global stores are whole, contiguous lines. A wave's LDS
+// instructions execute in order, so its own write -> read needs no barrier.
+constexpr int kStg = 136;
 
 struct Pop {
     int members, tokens;
@@ -131,25 +156,24 @@ struct QkvArgs {
     const float *gate_w;      // [8][32] fp32
     Rank1 gate_r1;            // ve_gate noise (a [dirs][8], b [dirs][32]) or a == NULL
     Rank1 ve_r1;              // value-embedding noise (a [dirs][V], b [dirs][512]) or a == NULL
-    __bf16 *out[3];           // [m][8][T][64]
+    __bf16 *out[3];           // q, k: [m][8][T][64]; v transposed: [m][8][64][T]
 };
 
 __global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
-    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    using M = Mma<256, 256, 64>;
+    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
-    // blockIdx.x -> (feature tile, token tile); the 6 feature tiles of a token tile are adjacent, so
-    // its x rows are re-read from L2 while hot.
-    const int nt = blockIdx.x % 6, tt = blockIdx.x / 6;
+    int nt, tt;
+    tile_order(blockIdx.x, 6, p.pop.members * tiles_t, tt, nt);
     const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
     const int n0 = nt * 256, mat = n0 / 512, nl0 = n0 % 512;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
 
     f32x16 acc[4][4];
-    Mma<256, 256>::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512,
-                       sW, sX, acc, tid, wn0, wm0);
+    M::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512,
+                       lds, acc, tid, wn0, wm0);
 
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
@@ -157,6 +181,7 @@ __global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
     const int head0 = (nl0 + wn0) / 64;
     const float *arow = r1.a ? r1.a + dir * r1.a_stride + nl0 + wn0 : nullptr;
     __bf16 *outm = p.out[mat];
+    __bf16 *stg = lds + wave * 128 * kStg;
 
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -252,18 +277,42 @@ __global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
                 }
             }
         }
+        // stage: Q, K as [token][feature]; V transposed as [feature][token]
+        const int tl = 32 * tb + j;
 #pragma unroll
-        for (int hd = 0; hd < 2; ++hd) {
-            __bf16 *orow = outm + (((int64_t)m * 8 + head0 + hd) * T + t) * 64;
+        for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
-            for (int half = 0; half < 2; ++half)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
+            for (int g = 0; g < 4; ++g) {
+                const int f = 32 * fb + 8 * g + 4 * hf;
+                if (mat < 2) {
                     bf16x4 o;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = (__bf16)acc[2 * hd + half][tb][4 * g + e];
-                    store_bf16x4(orow + 32 * half + 8 * g + 4 * hf, o);
+                    for (int e = 0; e < 4; ++e) o[e] = (__bf16)acc[fb][tb][4 * g + e];
+                    store_bf16x4(stg + tl * kStg + f, o);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) stg[(f + e) * kStg + tl] = (__bf16)acc[fb][tb][4 * g + e];
                 }
+            }
+    }
+    // whole-line stores: Q, K rows [m][h][t][0:64] (128 B); V^T rows [m][h][d][t0 .. t0+128) (256 B)
+#pragma unroll
+    for (int hd = 0; hd < 2; ++hd) {
+        const int64_t hbase = ((int64_t)m * 8 + head0 + hd);
+        if (mat < 2) {
+#pragma unroll 4
+            for (int it = 0; it < 16; ++it) {
+                const int c = it * 64 + lane, row = c >> 3, ch = c & 7;
+                bf16x8 v = load_bf16x8(stg + row * kStg + 64 * hd + ch * 8);
+                store_bf16x8(outm + (hbase * T + t0 + wm0 + row) * 64 + ch * 8, v);
+            }
+        } else {
+#pragma unroll 4
+            for (int it = 0; it < 16; ++it) {
+                const int c = it * 64 + lane, d = c >> 4, ch = c & 15;
+                bf16x8 v = load_bf16x8(stg + (64 * hd + d) * kStg + ch * 8);
+                store_bf16x8(outm + (hbase * 64 + d) * T + t0 + wm0 + ch * 8, v);
+            }
         }
     }
 }
@@ -302,8 +351,8 @@ struct ResidArgs {
 };
 
 __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sW[512][kLdsRow];
-    __shared__ __attribute__((aligned(16))) __bf16 sX[128][kLdsRow];
+    using M = Mma<512, 128, 32>;
+    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 128;
     const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * 128;
@@ -311,7 +360,7 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
     const int wn0 = 128 * wave;
 
     f32x16 acc[4][4];
-    Mma<512, 128>::run(p.w, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, sW, sX, acc, tid, wn0, 0);
+    M::run(p.w, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds, acc, tid, wn0, 0);
 
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
@@ -320,8 +369,14 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
         if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
         if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
     }
-    // per-token partial statistics: [0] sum y^2, [1..3] y . b_k, reduced over lanes and waves in LDS
-    float *red = reinterpret_cast<float *>(&sX[0][0]);  // [128 tokens][4 waves][4]
+    // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
+    // hi/lo rows of the split3 output), then the per-token statistics [128 tokens][4 waves][4].
+    constexpr int kStgF = 136;
+    static_assert(32 * kStgF * 4 >= 64 * kStg * 2, "bf16 split3 staging must fit the wave's region");
+    static_assert(4 * 32 * kStgF * 4 + 128 * 4 * 4 * 4 <= M::LDS_BYTES, "epilogue LDS");
+    float *stgf = reinterpret_cast<float *>(lds) + wave * 32 * kStgF;
+    __bf16 *stgb = reinterpret_cast<__bf16 *>(reinterpret_cast<float *>(lds) + wave * 32 * kStgF);
+    float *red = reinterpret_cast<float *>(lds) + 4 * 32 * kStgF;
 
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
@@ -360,15 +415,18 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
                         for (int e = 0; e < 4; ++e) st[1 + k] += acc[fb][tb][4 * g + e] * f4get(b4, e);
                     }
                 }
+                if (p.xout)
+                    st4(stgf + j * kStgF + f0, float4{acc[fb][tb][4 * g], acc[fb][tb][4 * g + 1],
+                                                      acc[fb][tb][4 * g + 2], acc[fb][tb][4 * g + 3]});
             }
         if (p.xout) {
-            float *xo = p.xout + row * 512 + wn0;
-#pragma unroll
-            for (int fb = 0; fb < 4; ++fb)
-#pragma unroll
-                for (int g = 0; g < 4; ++g)
-                    st4(xo + 32 * fb + 8 * g + 4 * hf, float4{acc[fb][tb][4 * g], acc[fb][tb][4 * g + 1],
-                                                              acc[fb][tb][4 * g + 2], acc[fb][tb][4 * g + 3]});
+            // whole-line stores: 32 rows x 512 B of this wave's 128 features
+            float *xo = p.xout + ((int64_t)m * T + t0 + 32 * tb) * 512 + wn0;
+#pragma unroll 4
+            for (int it = 0; it < 16; ++it) {
+                const int c = it * 64 + lane, r = c >> 5, ch = c & 31;
+                st4(xo + (int64_t)r * 512 + ch * 4, ld4(stgf + r * kStgF + ch * 4));
+            }
         }
 #pragma unroll
         for (int k = 0; k < 4; ++k) st[k] += swap_halves(st[k]);
@@ -389,35 +447,33 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
 #pragma unroll
             for (int k = 0; k < 4; ++k) tot[k] += red[(tl * 4 + w) * 4 + k];
         const float rstd = rsqrtf(tot[0] * (1.0f / 512.0f) + kEps);
-        if (p.split3) {
-            __bf16 *ho = p.hout + row * 1536 + wn0;
+        // stage bf16 rows: [32][kStg] for hi (and lo after it when split3)
 #pragma unroll
-            for (int fb = 0; fb < 4; ++fb)
+        for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    bf16x4 hi, lo;
+            for (int g = 0; g < 4; ++g) {
+                bf16x4 hi, lo;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        float h = acc[fb][tb][4 * g + e] * rstd;
-                        hi[e] = (__bf16)h;
-                        lo[e] = (__bf16)(h - (float)hi[e]);
-                    }
-                    const int f0 = 32 * fb + 8 * g + 4 * hf;
-                    store_bf16x4(ho + f0, hi);
-                    store_bf16x4(ho + 512 + f0, lo);
-                    store_bf16x4(ho + 1024 + f0, hi);
+                for (int e = 0; e < 4; ++e) {
+                    const float h = acc[fb][tb][4 * g + e] * rstd;
+                    hi[e] = (__bf16)h;
+                    lo[e] = (__bf16)(h - (float)hi[e]);
                 }
-        } else {
-            __bf16 *ho = p.hout + row * 512 + wn0;
-#pragma unroll
-            for (int fb = 0; fb < 4; ++fb)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    bf16x4 hv;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) hv[e] = (__bf16)(acc[fb][tb][4 * g + e] * rstd);
-                    store_bf16x4(ho + 32 * fb + 8 * g + 4 * hf, hv);
-                }
+                const int f0 = 32 * fb + 8 * g + 4 * hf;
+                store_bf16x4(stgb + j * kStg + f0, hi);
+                if (p.split3) store_bf16x4(stgb + (32 + j) * kStg + f0, lo);
+            }
+        const int width = p.split3 ? 1536 : 512;
+        __bf16 *hb = p.hout + ((int64_t)m * T + t0 + 32 * tb) * width + wn0;
+#pragma unroll 4
+        for (int it = 0; it < 8; ++it) {
+            const int c = it * 64 + lane, r = c >> 4, ch = c & 15;
+            bf16x8 hv = load_bf16x8(stgb + r * kStg + ch * 8);
+            store_bf16x8(hb + (int64_t)r * width + ch * 8, hv);
+            if (p.split3) {
+                store_bf16x8(hb + (int64_t)r * width + 512 + ch * 8, load_bf16x8(stgb + (32 + r) * kStg + ch * 8));
+                store_bf16x8(hb + (int64_t)r * width + 1024 + ch * 8, hv);
+            }
         }
         if (wave == 0 && hf == 0) {
             for (int k = 0; k < p.nnext; ++k) p.ndots[row * p.nnext + k] = rstd * tot[1 + k];
@@ -443,18 +499,19 @@ struct FcArgs {
 };
 
 __global__ __launch_bounds__(256, 1) void fc_kernel(FcArgs p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
-    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    using M = Mma<256, 256, 64>;
+    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
-    const int nt = blockIdx.x % 8, tt = blockIdx.x / 8;
+    int nt, tt;
+    tile_order(blockIdx.x, 8, p.pop.members * tiles_t, tt, nt);
     const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
     const int n0 = nt * 256;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
 
     f32x16 acc[4][4];
-    Mma<256, 256>::run(p.w + (int64_t)n0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, sW, sX,
+    M::run(p.w + (int64_t)n0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds,
                        acc, tid, wn0, wm0);
 
     const int dir = m / p.pop.dir_div;
@@ -462,13 +519,13 @@ __global__ __launch_bounds__(256, 1) void fc_kernel(FcArgs p) {
     const int nf0 = n0 + wn0;
     const float *arow = p.r1.a ? p.r1.a + dir * p.r1.a_stride + nf0 : nullptr;
     const float *brow = p.nb ? p.nb + dir * p.nb_stride + nf0 : nullptr;
+    __bf16 *stg = lds + wave * 128 * kStg;
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
         const float corr = arow ? sgn * p.dots[row] : 0.f;
         float pd = 0.f;
-        __bf16 *ar = p.act + row * 2048 + nf0;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
@@ -484,12 +541,19 @@ __global__ __launch_bounds__(256, 1) void fc_kernel(FcArgs p) {
                     o[e] = (__bf16)y;
                     pd += (float)o[e] * f4get(b4, e);
                 }
-                store_bf16x4(ar + f, o);
+                store_bf16x4(stg + (32 * tb + j) * kStg + f, o);
             }
         if (p.pdots) {
             pd += swap_halves(pd);
             if (hf == 0) p.pdots[row * 16 + nf0 / 128] = pd;
         }
+    }
+    // whole-line stores of act rows [m][t][nf0 .. nf0 + 128) (256 B each)
+    __bf16 *abase = p.act + ((int64_t)m * T + t0 + wm0) * 2048 + nf0;
+#pragma unroll 4
+    for (int it = 0; it < 32; ++it) {
+        const int c = it * 64 + lane, row = c >> 4, ch = c & 15;
+        store_bf16x8(abase + (int64_t)row * 2048 + ch * 8, load_bf16x8(stg + row * kStg + ch * 8));
     }
 }
 
@@ -511,17 +575,18 @@ struct LowrankArgs {
 };
 
 __global__ __launch_bounds__(256, 1) void lowrank_kernel(LowrankArgs p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
-    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    using M = Mma<256, 256, 64>;
+    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
     const int T = p.pop.tokens, ntiles = p.N / 256, tiles_t = T / 256;
-    const int nt = blockIdx.x % ntiles, tt = blockIdx.x / ntiles;
+    int nt, tt;
+    tile_order(blockIdx.x, ntiles, p.pop.members * tiles_t, tt, nt);
     const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
     const int n0 = nt * 256;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
 
     f32x16 acc[4][4];
-    Mma<256, 256>::run(p.w + (int64_t)n0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, sW, sX,
+    M::run(p.w + (int64_t)n0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds,
                        acc, tid, wn0, wm0);
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;
@@ -573,8 +638,8 @@ struct HeadArgs {
 };
 
 __global__ __launch_bounds__(256, 1) void head_ce_kernel(HeadArgs p) {
-    __shared__ __attribute__((aligned(16))) __bf16 sW[256][kLdsRow];
-    __shared__ __attribute__((aligned(16))) __bf16 sX[256][kLdsRow];
+    using M = Mma<256, 256, 64>;
+    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
     const int T = p.pop.tokens, tiles_t = T / 256;
     const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * 256;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
@@ -595,8 +660,8 @@ __global__ __launch_bounds__(256, 1) void head_ce_kernel(HeadArgs p) {
     const float k1 = (2.0f / 15.0f) * kLog2e, k2 = -30.0f * kLog2e;
     f32x16 acc[4][4];
     for (int v0 = 0; v0 < p.vocab; v0 += 256) {
-        Mma<256, 256>::run(p.w + (int64_t)v0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, sW,
-                           sX, acc, tid, wn0, wm0);
+        M::run(p.w + (int64_t)v0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds,
+                           acc, tid, wn0, wm0);
         const int nf0 = v0 + wn0;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
@@ -617,7 +682,7 @@ __global__ __launch_bounds__(256, 1) void head_ce_kernel(HeadArgs p) {
             }
     }
     // combine the two lane halves and the two feature waves
-    float *red = reinterpret_cast<float *>(&sX[0][0]);  // [256 tokens][2 waves][2]
+    float *red = reinterpret_cast<float *>(lds);  // [256 tokens][2 waves][2]
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
         sum[tb] += swap_halves(sum[tb]);

@@ -230,11 +230,12 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
                   qkv_out, stream)
         # attention; its epilogue also forms y . b_o per head for c_proj's rank-1 term
         no = nz(pre + 'attn.c_proj.weight')
-        q4, k4, v4 = (B.qkv[j].transpose(1, 2) for j in range(3))  # [m, T, H, D] views of [m, H, T, D]
+        q4, k4 = (B.qkv[j].transpose(1, 2) for j in range(2))  # [m, T, H, D] views of [m, H, T, D]
+        vt = B.qkv[2].view(m, N_HEAD, HEAD_DIM, T)               # V^T as the qkv kernel writes it
         yv = B.y.view(m, T, N_HEAD, HEAD_DIM)
-        _call('noise_attention_fwd', q4.data_ptr(), k4.data_ptr(), v4.data_ptr(), yv.data_ptr(), m, N_HEAD, T,
+        _call('noise_attention_fwd', q4.data_ptr(), k4.data_ptr(), vt.data_ptr(), yv.data_ptr(), m, N_HEAD, T,
                   HEAD_DIM, q4.stride(0), q4.stride(2), q4.stride(1), k4.stride(0), k4.stride(2), k4.stride(1),
-                  v4.stride(0), v4.stride(2), v4.stride(1), 0, yv.stride(0), yv.stride(2), yv.stride(1),
+                  vt.stride(0), vt.stride(1), vt.stride(2), 1, yv.stride(0), yv.stride(2), yv.stride(1),
                   W.windows[i], 1.0 / math.sqrt(HEAD_DIM), None if no is None else no[1].data_ptr(),
                   0 if no is None else no[1].stride(0), dir_div, None if no is None else B.d_attn.data_ptr(),
                   stream, label=f'window {W.windows[i]}')
