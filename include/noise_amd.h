@@ -134,16 +134,23 @@ int noise_pop_embed(const noise_population_t *pop, int per_member, const float *
 int noise_member_dots(const noise_population_t *pop, noise_view_t x, int64_t width, const noise_rank1_t *vecs,
                       int64_t nk, float *out, noise_stream_t stream);
 
+/* Value-embedding gates of one block (eggroll.py:88 / model.py:89): gates[row*8 + h] =
+ * 2 sigmoid(x[row, :32] . gate_w[h] + sign * (x[:32] . b) * a[h]) with x the block's normalised input
+ * (bf16), gate_w fp32 [8][32] = attn.ve_gate.weight, gate_noise its rank-1 noise (a [dirs][8], b [dirs][32])
+ * or NULL. */
+int noise_pop_gate(const noise_population_t *pop, noise_view_t x, const float *gate_w, const noise_rank1_t *gate_noise,
+                   float *gates, noise_stream_t stream);
+
 /* Q, K, V of one block for every member (eggroll.py:81-90): x (= norm of the block input, bf16) times
- * c_q, c_k, c_v (w[0..2], bf16 [512][512]) + sign * dots[row*3 + i] * a_i, value-embedding gate on V
- * (ve fp32 [V][512] or NULL; gate_w fp32 [8][32] = attn.ve_gate.weight; gate_noise: rank-1 noise of
- * ve_gate, a [dirs][8], b [dirs][32]; ve_noise: lowrank_embed noise of the value table, a [dirs][V],
- * b [dirs][512]; either NULL), rotary (rope_cos/rope_sin fp32 [tokens][32] holding model.py:177-183's
- * bf16 tables) then per-head RMSNorm on Q and K. Outputs bf16 [members][8][tokens][64]. */
+ * c_q, c_k, c_v (w[0..2], bf16 [512][512]) + sign * dots[row*3 + i] * a_i; on V, + gates[row*8 + h] *
+ * (ve[idx[t], :] + lowrank_embed noise of the value table, ve_noise a [dirs][V], b [dirs][512], or NULL)
+ * when ve (fp32 [V][512]) is not NULL; rotary (rope_cos/rope_sin fp32 [tokens][32] holding
+ * model.py:177-183's bf16 tables) then per-head RMSNorm on Q and K. Outputs bf16: Q, K
+ * [members][8][tokens][64]; V transposed [members][8][64][tokens]. */
 int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3], const noise_rank1_t r1[3],
                   const float *dots, const float *rope_cos, const float *rope_sin, const float *ve,
-                  const int64_t *idx, const float *gate_w, const noise_rank1_t *gate_noise,
-                  const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream);
+                  const int64_t *idx, const float *gates, const noise_rank1_t *ve_noise, void *const out[3],
+                  noise_stream_t stream);
 
 /* Residual writer (eggroll.py:92 attn.c_proj and :93 mlp.c_proj): y = xres + x w^T + sign * (sum of
  * dots_count dots at dots[row*dots_stride]) * a; if mix: y = rl*y + ml*x0 (the next block's mixing,

@@ -123,6 +123,16 @@ __device__ __forceinline__ void tile_order(int wg, int ntiles_n, int ntiles_t, i
     }
 }
 
+// Copy the two feature blocks of head HD (blocks 2HD, 2HD+1) of token block TB into plain registers
+// (static indices keep the accumulators in registers).
+template <int TB, int HD>
+__device__ __forceinline__ void copy_head(const f32x16 (&acc)[4][4], float (&v)[2][16]) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) v[half][r] = acc[2 * HD + half][TB][r];
+}
+
 // Epilogue staging: each wave writes its finished 128 x 128 tile into a private LDS region (rows padded
 // to kStg) and re-reads it as 16 B row chunks, so global stores are whole, contiguous lines. A wave's LDS
 // instructions execute in order, so its own write -> read needs no barrier.
@@ -153,8 +163,7 @@ struct QkvArgs {
     const float *cos_t, *sin_t;  // [T][32]
     const float *ve;          // [V][512] fp32 or NULL
     const int64_t *idx;       // [T]
-    const float *gate_w;      // [8][32] fp32
-    Rank1 gate_r1;            // ve_gate noise (a [dirs][8], b [dirs][32]) or a == NULL
+    const float *gates;       // [rows][8] value-embedding gates (noise_pop_gate)
     Rank1 ve_r1;              // value-embedding noise (a [dirs][V], b [dirs][512]) or a == NULL
     __bf16 *out[3];           // q, k: [m][8][T][64]; v transposed: [m][8][64][T]
 };
@@ -183,115 +192,102 @@ __global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
     __bf16 *outm = p.out[mat];
     __bf16 *stg = lds + wave * 128 * kStg;
 
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    // one (token block, head) pair at a time: its 32 accumulators are copied out (static indices) so the
+    // body below is compiled once and only one head's values are live
+#pragma unroll 1
+    for (int it = 0; it < 8; ++it) {
+        const int tb = it >> 1, hd = it & 1;
+        float v[2][16];
+        switch (it) {
+            case 0: copy_head<0, 0>(acc, v); break;
+            case 1: copy_head<0, 1>(acc, v); break;
+            case 2: copy_head<1, 0>(acc, v); break;
+            case 3: copy_head<1, 1>(acc, v); break;
+            case 4: copy_head<2, 0>(acc, v); break;
+            case 5: copy_head<2, 1>(acc, v); break;
+            case 6: copy_head<3, 0>(acc, v); break;
+            default: copy_head<3, 1>(acc, v); break;
+        }
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
         if (arow) {
             const float corr = sgn * p.dots[row * 3 + mat];
 #pragma unroll
-            for (int fb = 0; fb < 4; ++fb)
+            for (int half = 0; half < 2; ++half)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    float4 a4 = ld4(arow + 32 * fb + 8 * g + 4 * hf);
+                    float4 a4 = ld4(arow + 64 * hd + 32 * half + 8 * g + 4 * hf);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) acc[fb][tb][4 * g + e] += corr * f4get(a4, e);
+                    for (int e = 0; e < 4; ++e) v[half][4 * g + e] += corr * f4get(a4, e);
                 }
         }
         if (mat == 2 && p.ve) {
-            // v += 2 sigmoid(x[:32] . Wg[head]) * ve[idx[t], head*64 + d]   (eggroll.py:85-89)
-            const __bf16 *xr = p.x + m * p.xs_m + (int64_t)t * p.xs_t;
-            float z[2] = {0.f, 0.f};
-#pragma unroll
-            for (int c8 = 0; c8 < 4; ++c8) {
-                bf16x8 xv = load_bf16x8(xr + 8 * c8);
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    const float xf = (float)xv[e];
-                    z[0] += xf * p.gate_w[head0 * 32 + 8 * c8 + e];
-                    z[1] += xf * p.gate_w[(head0 + 1) * 32 + 8 * c8 + e];
-                }
-            }
-            if (p.gate_r1.a) {
-                // lowrank ve_gate: + sign * (x[:32] . b_g) * a_g[head]
-                const float *gb = p.gate_r1.b + dir * p.gate_r1.b_stride;
-                float dg = 0.f;
-#pragma unroll
-                for (int c8 = 0; c8 < 4; ++c8) {
-                    bf16x8 xv = load_bf16x8(xr + 8 * c8);
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) dg += (float)xv[e] * gb[8 * c8 + e];
-                }
-                const float *ga = p.gate_r1.a + dir * p.gate_r1.a_stride;
-                z[0] += sgn * dg * ga[head0];
-                z[1] += sgn * dg * ga[head0 + 1];
-            }
+            // v += gate[row, head] * (ve[idx[t], head*64 + d] (+ lowrank_embed term))   (eggroll.py:85-89);
+            // the gates 2 sigmoid(x[:32] . Wg[head] (+ rank-1)) come precomputed (noise_pop_gate)
             const int64_t tok = p.idx[t];
-            const float *ver = p.ve + tok * 512;
+            const float gate = p.gates[row * 8 + head0 + hd];
+            const float *ver = p.ve + tok * 512 + (head0 + hd) * 64;
             // lowrank_embed of the value table (eggroll.py:61-63): + sign * a_ve[tok] * b_ve[:]
             const float ves = p.ve_r1.a ? sgn * p.ve_r1.a[dir * p.ve_r1.a_stride + tok] : 0.f;
-            const float *veb = p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride : nullptr;
+            const float *veb = p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride + (head0 + hd) * 64 : nullptr;
 #pragma unroll
-            for (int hd = 0; hd < 2; ++hd) {
-                const float gate = 2.0f / (1.0f + __expf(-z[hd]));
+            for (int half = 0; half < 2; ++half)
 #pragma unroll
-                for (int half = 0; half < 2; ++half)
+                for (int g = 0; g < 4; ++g) {
+                    const int d0 = 32 * half + 8 * g + 4 * hf;
+                    float4 e4 = ld4(ver + d0);
+                    if (veb) {
+                        float4 b4 = ld4(veb + d0);
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int d0 = (head0 + hd) * 64 + 32 * half + 8 * g + 4 * hf;
-                        float4 e4 = ld4(ver + d0);
-                        float4 b4 = veb ? ld4(veb + d0) : float4{0, 0, 0, 0};
+                        for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * (f4get(e4, e) + ves * f4get(b4, e));
+                    } else {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e)
-                            acc[2 * hd + half][tb][4 * g + e] += gate * (f4get(e4, e) + ves * f4get(b4, e));
+                        for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * f4get(e4, e);
                     }
-            }
+                }
         }
         if (mat < 2) {
             // rotary (model.py:55-58) then RMSNorm over the head (model.py:46-47)
             const float *cr = p.cos_t + (int64_t)t * 32, *sr = p.sin_t + (int64_t)t * 32;
+            float ss = 0.f;
 #pragma unroll
-            for (int hd = 0; hd < 2; ++hd) {
-                float ss = 0.f;
+            for (int g = 0; g < 4; ++g) {
+                float4 c4 = ld4(cr + 8 * g + 4 * hf), s4 = ld4(sr + 8 * g + 4 * hf);
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    float4 c4 = ld4(cr + 8 * g + 4 * hf), s4 = ld4(sr + 8 * g + 4 * hf);
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const int r = 4 * g + e;
-                        const float c = f4get(c4, e), s = f4get(s4, e);
-                        const float x1 = acc[2 * hd][tb][r], x2 = acc[2 * hd + 1][tb][r];
-                        const float o1 = x1 * c + x2 * s;
-                        const float o2 = x1 * -s + x2 * c;
-                        acc[2 * hd][tb][r] = o1;
-                        acc[2 * hd + 1][tb][r] = o2;
-                        ss += o1 * o1 + o2 * o2;
-                    }
+                for (int e = 0; e < 4; ++e) {
+                    const int r = 4 * g + e;
+                    const float c = f4get(c4, e), sn = f4get(s4, e);
+                    const float x1 = v[0][r], x2 = v[1][r];
+                    const float o1 = x1 * c + x2 * sn;
+                    const float o2 = x1 * -sn + x2 * c;
+                    v[0][r] = o1;
+                    v[1][r] = o2;
+                    ss += o1 * o1 + o2 * o2;
                 }
-                ss += swap_halves(ss);
-                const float rstd = rsqrtf(ss * (1.0f / 64.0f) + kEps);
+            }
+            ss += swap_halves(ss);
+            const float rstd = rsqrtf(ss * (1.0f / 64.0f) + kEps);
 #pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    acc[2 * hd][tb][r] *= rstd;
-                    acc[2 * hd + 1][tb][r] *= rstd;
-                }
+            for (int r = 0; r < 16; ++r) {
+                v[0][r] *= rstd;
+                v[1][r] *= rstd;
             }
         }
         // stage: Q, K as [token][feature]; V transposed as [feature][token]
         const int tl = 32 * tb + j;
 #pragma unroll
-        for (int fb = 0; fb < 4; ++fb)
+        for (int half = 0; half < 2; ++half)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
-                const int f = 32 * fb + 8 * g + 4 * hf;
+                const int f = 64 * hd + 32 * half + 8 * g + 4 * hf;
                 if (mat < 2) {
                     bf16x4 o;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = (__bf16)acc[fb][tb][4 * g + e];
+                    for (int e = 0; e < 4; ++e) o[e] = (__bf16)v[half][4 * g + e];
                     store_bf16x4(stg + tl * kStg + f, o);
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) stg[(f + e) * kStg + tl] = (__bf16)acc[fb][tb][4 * g + e];
+                    for (int e = 0; e < 4; ++e) stg[(f + e) * kStg + tl] = (__bf16)v[half][4 * g + e];
                 }
             }
     }
@@ -755,8 +751,8 @@ using namespace noise;
 
 extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3],
                              const noise_rank1_t r1[3], const float *dots, const float *rope_cos, const float *rope_sin,
-                             const float *ve, const int64_t *idx, const float *gate_w, const noise_rank1_t *gate_noise,
-                             const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream) {
+                             const float *ve, const int64_t *idx, const float *gates, const noise_rank1_t *ve_noise,
+                             void *const out[3], noise_stream_t stream) {
     clear_error();
     const char *fn = "noise_pop_qkv";
     NOISE_TRY(check_pop(pop, 256, fn));
@@ -767,7 +763,7 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
         NOISE_CHECK_ARG(!r1 || !r1[i].a || (dots && aligned(r1[i].a, 16) && r1[i].a_stride % 4 == 0),
                         "%s: perturbed matrix %d needs dots and 16 B aligned a rows", fn, i);
     }
-    NOISE_CHECK_ARG(!ve || (idx && gate_w), "%s: value embeddings need idx and gate weights", fn);
+    NOISE_CHECK_ARG(!ve || (idx && gates), "%s: value embeddings need idx and gates", fn);
     QkvArgs a;
     a.pop = make_pop(pop);
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
@@ -776,8 +772,7 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
         a.r1[i] = make_r1(r1 ? &r1[i] : nullptr);
         a.out[i] = (__bf16 *)out[i];
     }
-    a.dots = dots; a.cos_t = rope_cos; a.sin_t = rope_sin; a.ve = ve; a.idx = idx; a.gate_w = gate_w;
-    a.gate_r1 = make_r1(ve ? gate_noise : nullptr);
+    a.dots = dots; a.cos_t = rope_cos; a.sin_t = rope_sin; a.ve = ve; a.idx = idx; a.gates = gates;
     a.ve_r1 = make_r1(ve ? ve_noise : nullptr);
     NOISE_CHECK_ARG(!a.ve_r1.a || (aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
                     "%s: value-embedding noise b rows must be 16 B aligned", fn);

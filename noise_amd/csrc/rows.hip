@@ -333,3 +333,59 @@ extern "C" int noise_rank1_expand(const noise_population_t *pop, const float *ba
                        (int)pop->tokens, (int)width, total);
     return launch_status(fn);
 }
+
+namespace noise {
+namespace {
+
+// Value-embedding gates (eggroll.py:88, model.py:89): gates[row, h] = 2 sigmoid(x[row, :32] . Wg[h] (+ sign *
+// (x[:32] . b_g) * a_g[h] for lowrank ve_gate)), one thread per row.
+__global__ __launch_bounds__(256) void gate_kernel(int members, int tokens, int dir_div, const __bf16 *x, int64_t xs_m,
+                                                   int64_t xs_t, const float *wg, const float *sign, const float *ga,
+                                                   const float *gb, int64_t ga_stride, int64_t gb_stride, float *out) {
+    const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (row >= (int64_t)members * tokens) return;
+    const int m = (int)(row / tokens), t = (int)(row - (int64_t)m * tokens);
+    const __bf16 *xr = x + m * xs_m + (int64_t)t * xs_t;
+    float xf[32];
+#pragma unroll
+    for (int c8 = 0; c8 < 4; ++c8) {
+        bf16x8 v = load_bf16x8(xr + 8 * c8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xf[8 * c8 + e] = (float)v[e];
+    }
+    float dg = 0.f;
+    const int dir = m / dir_div;
+    if (ga) {
+#pragma unroll
+        for (int c = 0; c < 32; ++c) dg += xf[c] * gb[dir * gb_stride + c];
+        dg *= sign[m];
+    }
+#pragma unroll
+    for (int h = 0; h < 8; ++h) {
+        float z = 0.f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) z += xf[c] * wg[h * 32 + c];
+        if (ga) z += dg * ga[dir * ga_stride + h];
+        out[row * 8 + h] = 2.0f / (1.0f + __expf(-z));
+    }
+}
+
+}  // namespace
+}  // namespace noise
+
+extern "C" int noise_pop_gate(const noise_population_t *pop, noise_view_t x, const float *gate_w,
+                              const noise_rank1_t *gate_noise, float *gates, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_gate";
+    NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
+    NOISE_CHECK_ARG(x.ptr && aligned(x.ptr, 16) && x.sm % 8 == 0 && x.st % 8 == 0, "%s: x misaligned", fn);
+    NOISE_CHECK_ARG(gate_w && gates, "%s: NULL gate weights or output", fn);
+    const bool noisy = gate_noise && gate_noise->a;
+    NOISE_CHECK_ARG(!noisy || (pop->sign && gate_noise->b), "%s: gate noise needs sign and b", fn);
+    const int64_t rows = pop->members * pop->tokens;
+    hipLaunchKernelGGL(gate_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (int)pop->members, (int)pop->tokens, (int)pop->dir_div, (const __bf16 *)x.ptr, x.sm, x.st, gate_w,
+                       pop->sign, noisy ? gate_noise->a : nullptr, noisy ? gate_noise->b : nullptr,
+                       noisy ? gate_noise->a_stride : 0, noisy ? gate_noise->b_stride : 0, gates);
+    return launch_status(fn);
+}

@@ -142,6 +142,7 @@ class _Buffers:
         self.d_fc = torch.empty(rows, dtype=F32, device=dev)
         self.d_mp = torch.empty(rows, 16, dtype=F32, device=dev)
         self.d_head = torch.empty(rows, 1, dtype=F32, device=dev)
+        self.gates = torch.empty(rows, N_HEAD, dtype=F32, device=dev)
         self.loss_tok = torch.empty(rows, dtype=F32, device=dev)
 
 
@@ -222,12 +223,14 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
         nq = qkv_noise(i)
         x_in = _view(B.h0, sm_e, E) if i == 0 else _view(B.h, T * E, E)
         ws = (ctypes.c_void_p * 3)(blk['q'].data_ptr(), blk['k'].data_ptr(), blk['v'].data_ptr())
-        gate_r1 = _rank1(nz(pre + 'attn.ve_gate.weight'))
         ve_r1 = _rank1(nz(f'value_embeds.{i}.weight'))
+        if 've' in blk:
+            gate_r1 = _rank1(nz(pre + 'attn.ve_gate.weight'))
+            _call('noise_pop_gate', popp, x_in, blk['gate'].data_ptr(), ctypes.byref(gate_r1), B.gates.data_ptr(),
+                  stream)
         _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
-                  sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(),
-                  blk['gate'].data_ptr() if 'gate' in blk else None, ctypes.byref(gate_r1), ctypes.byref(ve_r1),
-                  qkv_out, stream)
+              sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(),
+              B.gates.data_ptr() if 've' in blk else None, ctypes.byref(ve_r1), qkv_out, stream)
         # attention; its epilogue also forms y . b_o per head for c_proj's rank-1 term
         no = nz(pre + 'attn.c_proj.weight')
         q4, k4 = (B.qkv[j].transpose(1, 2) for j in range(2))  # [m, T, H, D] views of [m, H, T, D]
