@@ -1,0 +1,79 @@
+"""The C ABI without a GPU: libnoise_amd.so loads, exports every entry point include/noise_amd.h declares,
+and rejects invalid arguments with NOISE_EINVAL and a message (argument checks run before any HIP call)."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared():
+    text = (ROOT / 'include' / 'noise_amd.h').read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    return sorted(set(re.findall(r'\b(noise_[a-z0-9_]+)\s*\(', text)))
+
+
+@pytest.fixture(scope='module')
+def lib():
+    from noise_amd import _lib
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f'{_lib.LIB_PATH} is not built (run __graft_entry__.build())')
+    return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), f'{n} declared in include/noise_amd.h but not exported'
+
+
+def test_every_declared_symbol_has_a_ctypes_signature():
+    from noise_amd import _lib
+    missing = [n for n in declared() if n not in _lib.SIGNATURES]
+    assert not missing, missing
+
+
+def test_abi_version(lib):
+    assert lib.noise_abi_version() == 1
+
+
+def _err(lib):
+    return lib.noise_last_error().decode()
+
+
+def test_invalid_arguments_return_einval(lib):
+    from noise_amd import _lib
+    # attention: head_dim must be 64
+    st = lib.noise_attention_fwd(1, 1, 1, 1, 1, 1, 64, 32, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 10, 0.1, None, 0, 1,
+                                 None, None)
+    assert st == -1 and 'head_dim' in _err(lib)
+    # randint: range outside torch's 32-bit path
+    st = lib.noise_randint(None, 4, 0, 0, 256, 2 ** 28, 0, None)
+    assert st == -1 and 'range' in _err(lib)
+    # normal fill: generator offset must be a multiple of 4
+    st = lib.noise_normal_fill(None, 4, 0, 0, 2, 256, 0.0, 1.0, None)
+    assert st == -1 and 'multiple of 4' in _err(lib)
+    # population kernels: tokens must be a multiple of the tile
+    pop = _lib.Population(2, 300, None, 2)
+    st = lib.noise_pop_fc(ctypes.byref(pop), _lib.View(16, 0, 512), 16, None, None, 16, None, None, None)
+    assert st == -1 and 'multiple of 256' in _err(lib)
+    # missing population
+    st = lib.noise_member_mean(None, 0, 10, None, None)
+    assert st == -1
+
+
+def test_python_raises_runtime_error_with_message():
+    from noise_amd import _lib
+    with pytest.raises(RuntimeError, match='invalid argument.*head_dim'):
+        _lib.call('noise_attention_fwd', 1, 1, 1, 1, 1, 1, 64, 32, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 10, 0.1,
+                  None, 0, 1, None, None)
+
+
+def test_product_does_not_import_the_oracle():
+    """The product package never routes through oracle/ (no CPU fallback)."""
+    for f in (ROOT / 'noise_amd').rglob('*.py'):
+        src = f.read_text()
+        assert not re.search(r'^\s*(from|import)\s+oracle\b', src, re.M), f

@@ -151,3 +151,28 @@ def test_repeatable(params):
     a = population_forward(W, tables, sign, idx[:-1], idx[1:], dir_div=2)
     b = population_forward(W, tables, sign, idx[:-1], idx[1:], dir_div=2)
     assert torch.equal(a, b)
+
+
+def test_matches_reference_population_fixture(params):
+    """The fused HIP forward against the reference's own population_loss output (written from
+    train/val/eggroll.py by tests/golden/make_reference_fixtures.py): all 60 parameters perturbed,
+    4 members x 256 tokens, head x30."""
+    import sys
+    from pathlib import Path
+    import numpy as np
+    from noise_amd.eggroll import Weights, population_forward
+    golden = Path(__file__).resolve().parent / 'golden'
+    sys.path.insert(0, str(golden))
+    from make_reference_fixtures import population_inputs
+    fx = np.load(golden / 'reference_fixtures.npz', allow_pickle=False)
+    P = dict(params)
+    P['lm_head.weight'] = P['lm_head.weight'] * 30
+    shapes = {n: tuple(v.shape) for n, v in params.items()}
+    flat, sign, idx = population_inputs(shapes)
+    noise = {}
+    for n, rows in flat.items():
+        rows = rows.to(DEV).contiguous()
+        noise[n] = (rows[:, :shapes[n][0]], rows[:, shapes[n][0]:]) if len(shapes[n]) == 2 else rows
+    W = Weights({k: v.to(DEV) for k, v in P.items()})
+    got = population_forward(W, noise, sign.to(DEV), idx[:-1].to(DEV), idx[1:].to(DEV), dir_div=2).cpu()
+    check(got, torch.from_numpy(fx['pop_losses']))
