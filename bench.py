@@ -51,6 +51,28 @@ def kernel_flops_per_launch(name, label, members, T):
     return None
 
 
+PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'population_forward_1024x2048.md')
+ROCPROF_NAME = {'noise_pop_qkv': 'qkv_kernel', 'noise_pop_fc': 'fc_kernel', 'noise_pop_head_ce': 'head_ce_kernel',
+                'noise_pop_residual[attn.c_proj]': 'resid_kernel<512>',
+                'noise_pop_residual[mlp.c_proj]': 'resid_kernel<2048>'}
+
+
+def profiled_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary (FETCH_SIZE + WRITE_SIZE, scaled
+    by the 1 GiB copy calibration), or None."""
+    name = ROCPROF_NAME.get(kernel) or ('attention_fwd_kernel<true>' if kernel.startswith('noise_attention') else None)
+    if not name or not os.path.exists(PROFILE):
+        return None
+    for line in open(PROFILE):
+        cells = [c.strip() for c in line.strip().strip('|').split('|')]
+        if len(cells) == 7 and cells[0] == name:
+            try:
+                return int((float(cells[5]) + float(cells[6])) * 1e9)
+            except ValueError:
+                return None
+    return None
+
+
 def block_matrix_names():
     return [f'transformer.h.{i}.{s}.weight' for i in range(8)
             for s in ('attn.c_q', 'attn.c_k', 'attn.c_v', 'attn.c_proj', 'mlp.c_fc', 'mlp.c_proj')]
@@ -83,7 +105,18 @@ def main():
     ap.add_argument('--members', type=int, default=2 * PAIRS)
     ap.add_argument('--cpu-members', type=int, default=4, help='members of the CPU-baseline sample (0: skip)')
     ap.add_argument('--profile-steps', type=int, default=1, help='extra timed steps with per-kernel events')
+    ap.add_argument('--copy-calibration', action='store_true',
+                    help='only copy 1 GiB device to device (scale reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)')
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        src = torch.ones(2 ** 28, device='cuda')
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps(dict(copy_bytes=2 ** 30)))
+        return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py measures one GPU: this build has no multi-GPU path (members shard across GPUs with one '
               'all_gather of the losses; see DESIGN.md). Run with --gpus 1.', file=sys.stderr)
@@ -150,7 +183,9 @@ def main():
         dominant = max(timed, key=lambda k: kernels[k]['ms_per_step'])
         dk = kernels[dominant]
         roofline = dict(bound='mfma', kernel=dominant, achieved=round(dk['tflops'], 1), peak=BF16_PEAK / 1e12,
-                        unit='TFLOP/s', frac=dk['mfma_frac'], traffic=None)
+                        unit='TFLOP/s', frac=dk['mfma_frac'], traffic=profiled_traffic(dominant),
+                        flops_per_launch=kernel_flops_per_launch(*(dominant.rstrip(']').split('[') + [None])[:2],
+                                                                 members, TOKENS))
 
     algo_flops = 68_318_208 * members * TOKENS
     line = dict(

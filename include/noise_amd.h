@@ -156,7 +156,7 @@ int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *con
  * dots_count dots at dots[row*dots_stride]) * a; if mix: y = rl*y + ml*x0 (the next block's mixing,
  * eggroll.py:79, lambdas + sign * eps); xout = y (fp32, may be NULL); hout = bf16(norm(y)) [m][T][512]
  * or, with split3, its [hi | lo | hi] bf16 split [m][T][1536] for the fp32 head; next_dots[row*nnext+k]
- * = norm(y) . next[k].b (0 <= nnext <= 3). w bf16 [512][K]. */
+ * = norm(y) . next[k].b (0 <= nnext <= 3). w bf16 [512][K], K = 512 (attn.c_proj) or 2048 (mlp.c_proj). */
 int noise_pop_residual(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K,
                        const noise_rank1_t *r1, const float *dots, int64_t dots_stride, int64_t dots_count,
                        noise_view_t xres, float *xout, int mix, float lam_r, float lam_x, const float *eps_r,

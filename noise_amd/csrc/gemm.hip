@@ -346,6 +346,7 @@ struct ResidArgs {
     float *ndots;             // [rows][nnext]
 };
 
+template <int KD>
 __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
     using M = Mma<512, 128, 32>;
     __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
     const int wn0 = 128 * wave;
 
     f32x16 acc[4][4];
-    M::run(p.w, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds, acc, tid, wn0, 0);
+    M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, 0);
 
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
@@ -791,7 +792,7 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     const char *fn = "noise_pop_residual";
     NOISE_TRY(check_pop(pop, 128, fn));
     NOISE_TRY(check_view(x, fn, "x"));
-    NOISE_CHECK_ARG(w && aligned(w, 16) && K % 64 == 0 && K > 0, "%s: w must be 16 B aligned, K a positive multiple of 64", fn);
+    NOISE_CHECK_ARG(w && aligned(w, 16) && (K == 512 || K == 2048), "%s: w must be 16 B aligned and K 512 or 2048", fn);
     NOISE_CHECK_ARG(xres.ptr && aligned(xres.ptr, 16) && xres.sm % 4 == 0 && xres.st % 4 == 0, "%s: bad xres", fn);
     NOISE_CHECK_ARG(!xout || aligned(xout, 16), "%s: xout must be 16 B aligned", fn);
     NOISE_CHECK_ARG(!mix || (x0.ptr && aligned(x0.ptr, 16) && x0.sm % 4 == 0 && x0.st % 4 == 0), "%s: mix needs x0", fn);
@@ -816,7 +817,10 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
         if (k < nnext) NOISE_CHECK_ARG(next[k].b && aligned(next[k].b, 16), "%s: next b %d NULL or misaligned", fn, k);
     }
     dim3 grid((unsigned)(pop->members * (pop->tokens / 128)));
-    hipLaunchKernelGGL(resid_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    if (K == 512)
+        hipLaunchKernelGGL(resid_kernel<512>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(resid_kernel<2048>, grid, dim3(256), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 

@@ -108,3 +108,16 @@ def test_eggroll_offsets_and_noise_bit_exact():
         got = noise[name] if p.dim() == 2 else (noise[name],)
         for r, o in zip(ref, got):
             assert torch.equal(bits(o), bits(r)), name
+
+
+def test_custom_ops_compile_without_graph_breaks():
+    """torch.compile(fullgraph=True) over the registered ops (the reference compiles its callers)."""
+    import noise_amd.ops  # noqa: F401
+
+    def f(q, k, v):
+        return torch.ops.noise_amd.attention(q, k, v, 64).float().sum(-1)
+
+    g = torch.Generator().manual_seed(9)
+    q, k, v = (torch.randn(1, 256, 8, 64, generator=g).bfloat16().to(DEV) for _ in range(3))
+    compiled = torch.compile(f, fullgraph=True, backend='aot_eager')
+    assert torch.equal(compiled(q, k, v), f(q, k, v))
