@@ -10,9 +10,10 @@
 // Shape of every product: out[(m,t), n] = sum_k W[n, k] x[(m,t), k], computed transposed (W rows are the
 // MFMA A operand, token rows the B operand) so that each lane of a v_mfma_f32_32x32x16_bf16 result holds
 // 16 output features of ONE token: per-token / per-head epilogue reductions stay in the lane plus one
-// exchange with lane ^ 32. A workgroup (4 waves) computes a BN x BM (features x tokens) tile, each wave
-// 128 x 128 (4 x 4 MFMA blocks, 256 fp32 accumulators); tiles are streamed through one padded LDS buffer
-// (144 B rows: conflict-free 16 B fragment reads) with the next k-step's global loads in flight.
+// exchange with lane ^ 32. A workgroup of 8 waves (two per SIMD, so one wave's LDS waits and barriers
+// overlap the other's MFMAs) computes a BN x BM (features x tokens) tile; each wave owns 128 x 64
+// (4 x 2 MFMA blocks, 128 fp32 accumulators). K is streamed through two padded LDS stages (rows +16 B:
+// conflict-free 16 B fragment reads) with the next k-step's global loads in flight.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -21,92 +22,121 @@ namespace {
 
 constexpr float kEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps, F.rms_norm's default
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kThreads = 512;                     // 8 waves
+
+constexpr int cmax(int a, int b) { return a > b ? a : b; }
 
 __device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
 __device__ __forceinline__ float f4get(const float4 &v, int e) { return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w; }
 
 // ------------------------------------------------------------------------------------------------
-// K loop: acc[fb][tb] += W[n0 + wn0 + 32fb + .., :] . X[t + wm0 + 32tb + .., :]
-// Two LDS stages of BN + BM rows x BK (rows padded by 8 bf16: conflict-free 16 B fragment reads). The
-// next k-step's tile is fetched into registers while the current stage feeds the MFMAs, then written to
-// the other stage; one barrier per k-step.
+// K loop: acc[fb][tb] += W[wn0 + 32fb + .., :] . X[wm0 + 32tb + .., :]
+// NW waves laid out WN (features) x WM (tokens); wave w owns features wn0 = 128 (w % WN) .. +128 and tokens
+// wm0 = 64 (w / WN) .. +64. The (BN + BM) x BK operand tiles stream through NS LDS stages by direct
+// global -> LDS copies (no register staging); rows are 2 BK bytes with the 16 B chunks XOR-swizzled by
+// row pair, so the 32 rows of a fragment read hit distinct banks. The fragments of the next 16-wide
+// k-step are read while the current step's MFMAs run; the wait for stage ks + 1 and the workgroup
+// barrier sit just before the read that crosses into it, and the stage just finished is refilled with
+// stage ks + NS right after that barrier. Ends with a barrier: the LDS may be reused at once.
 // ------------------------------------------------------------------------------------------------
-template <int BN, int BM, int BK>
+template <int NW, int BN, int BM, int BK, int NS>
 struct Mma {
     static constexpr int WN = BN / 128;
-    static constexpr int WM = BM / 128;
-    static_assert(WN * WM == 4, "4 waves of 128 x 128");
-    static constexpr int LD = BK + 8;           // padded LDS row (bf16)
-    static constexpr int CPR = BK / 8;          // 16 B chunks per row
-    static constexpr int CW = BN * CPR / 256;   // chunks per thread
-    static constexpr int CX = BM * CPR / 256;
-    static constexpr int STAGE = (BN + BM) * LD;  // bf16 per stage
-    static constexpr int LDS_BYTES = 2 * STAGE * 2;
+    static constexpr int WM = BM / 64;
+    static_assert(WN * WM == NW, "NW waves of 128 x 64");
+    static constexpr int RB = BK * 2;          // bytes per LDS row
+    static constexpr int CPR = BK / 8;         // 16 B chunks per row
+    static constexpr int RPI = 1024 / RB;      // rows per wave-wide copy (64 lanes x 16 B)
+    static constexpr int RPB = 256 / RB;       // rows per 256 B of banks
+    static constexpr int STAGE = (BN + BM) * RB;
+    static constexpr int NBLK = (BN + BM) / RPI;
+    static_assert(NBLK % NW == 0, "whole copies per wave");
+    static constexpr int NI = NBLK / NW;       // copies per wave per stage
+    static constexpr int SPK = BK / 16;
+    static_assert(SPK % 2 == 0, "fragment double buffer alternates within and across stages");
+    static_assert(NS >= 2 && NS <= 4 && NI * (NS - 1) < 64, "pipeline depth");
+    static constexpr int LDS_BYTES = NS * STAGE;
 
-    __device__ static void run(const __bf16 *W, int64_t ldw, const __bf16 *X, int64_t ldx, int K, __bf16 *lds,
-                               f32x16 (&acc)[4][4], int tid, int wn0, int wm0) {
-        const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    __device__ static int wn0(int wave) { return 128 * (wave % WN); }
+    __device__ static int wm0(int wave) { return 64 * (wave / WN); }
+    __device__ static int swz(int r, int c) { return c ^ ((r / RPB) % CPR); }
+
+    // W: BN rows of stride ldw; X: BM rows of stride ldx (elements, multiples of 8; 16 B aligned bases);
+    // K a multiple of BK
+    __device__ static void run(const __bf16 *W, int64_t ldw, const __bf16 *X, int64_t ldx, int K, void *lds_v,
+                               f32x16 (&acc)[4][2], int tid, int wn, int wm) {
+        char *lds = static_cast<char *>(lds_v);
+        const int wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) acc[fb][tb] = f32x16{};
-        bf16x8 rw[CW], rx[CX];
-        auto load = [&](int k0) {
+            for (int tb = 0; tb < 2; ++tb) acc[fb][tb] = f32x16{};
+        // copy i of a stage covers rows (i NW + wave) RPI .. +RPI: W for i < IW, X after. Row steps between
+        // copies are multiples of RPB * CPR, so a lane's swizzled chunk and byte offset are the same for all
+        // of its copies into one matrix; only the uniform base moves.
+        constexpr int STEP = NW * RPI;
+        static_assert(BN % STEP == 0 && BM % STEP == 0 && STEP % (RPB * CPR) == 0, "uniform copy steps");
+        constexpr int IW = BN / STEP;
+        const int rl = wave * RPI + lane / CPR;
+        const int cl = swz(rl, lane % CPR);
+        const unsigned offw = (unsigned)(rl * ldw * 2 + cl * 16), offx = (unsigned)(rl * ldx * 2 + cl * 16);
+        // fragment rows wn + 32 fb + j and BN + wm + 32 tb + j share the swizzle of row j
+        static_assert(32 % (RPB * CPR) == 0 && BN % (RPB * CPR) == 0, "fragment swizzle depends on j only");
+        int lo[SPK];
 #pragma unroll
-            for (int i = 0; i < CW; ++i) {
-                int c = tid + 256 * i;
-                rw[i] = load_bf16x8(W + (int64_t)(c / CPR) * ldw + k0 + (c % CPR) * 8);
-            }
+        for (int s = 0; s < SPK; ++s) lo[s] = j * RB + swz(j, 2 * s + hf) * 16;
+        const int nk = K / BK;
+        auto issue = [&](int p) {
+            char *st = lds + (p % NS) * STAGE;
 #pragma unroll
-            for (int i = 0; i < CX; ++i) {
-                int c = tid + 256 * i;
-                rx[i] = load_bf16x8(X + (int64_t)(c / CPR) * ldx + k0 + (c % CPR) * 8);
+            for (int i = 0; i < NI; ++i) {
+                if (i < IW)
+                    lds_dma16(W + (int64_t)(i * STEP) * ldw + p * BK, offw, st + (i * NW + wave) * 1024);
+                else
+                    lds_dma16(X + (int64_t)((i - IW) * STEP) * ldx + p * BK, offx, st + (i * NW + wave) * 1024);
             }
         };
-        auto store = [&](__bf16 *st) {
+        bf16x8 fa[2][4], fx[2][2];
+        auto fetch = [&](int buf, const char *st, int s) {
+            const char *pa = st + wn * RB + lo[s], *px = st + (BN + wm) * RB + lo[s];
 #pragma unroll
-            for (int i = 0; i < CW; ++i) {
-                int c = tid + 256 * i;
-                store_bf16x8(st + (c / CPR) * LD + (c % CPR) * 8, rw[i]);
-            }
+            for (int fb = 0; fb < 4; ++fb) fa[buf][fb] = *reinterpret_cast<const bf16x8 *>(pa + fb * 32 * RB);
 #pragma unroll
-            for (int i = 0; i < CX; ++i) {
-                int c = tid + 256 * i;
-                store_bf16x8(st + (BN + c / CPR) * LD + (c % CPR) * 8, rx[i]);
-            }
+            for (int tb = 0; tb < 2; ++tb) fx[buf][tb] = *reinterpret_cast<const bf16x8 *>(px + tb * 32 * RB);
         };
-        load(0);
-        store(lds);
+        // every stage buffer is free: stages 0 .. NS-1 in flight; stage 0 landed when min(NS-1, nk-1) remain
+#pragma unroll
+        for (int p = 0; p < NS; ++p)
+            if (p < nk) issue(p);
+        vm_wait_groups<NI, NS - 1>(nk - 1 < NS - 1 ? nk - 1 : NS - 1);
         __syncthreads();
-        int cur = 0;
-        for (int k0 = 0; k0 < K; k0 += BK) {
-            const bool more = k0 + BK < K;
-            if (more) load(k0 + BK);
-            const __bf16 *sw = lds + cur * STAGE;
-            const __bf16 *sx = sw + BN * LD;
-            // the sub-steps stay a loop: unrolling them hoists all fragment loads and spills
+        fetch(0, lds, 0);
 #pragma unroll 1
-            for (int s = 0; s < BK / 16; ++s) {
-                bf16x8 af[4], bf[4];
+        for (int ks = 0; ks < nk; ++ks) {
+            const char *st = lds + (ks % NS) * STAGE;
 #pragma unroll
-                for (int fb = 0; fb < 4; ++fb) af[fb] = load_bf16x8(sw + (wn0 + 32 * fb + j) * LD + 16 * s + 8 * hf);
-#pragma unroll
-                for (int tb = 0; tb < 4; ++tb) bf[tb] = load_bf16x8(sx + (wm0 + 32 * tb + j) * LD + 16 * s + 8 * hf);
+            for (int s = 0; s < SPK; ++s) {
+                const int cur = s & 1;
+                if (s + 1 < SPK) {
+                    fetch(cur ^ 1, st, s + 1);
+                } else if (ks + 1 < nk) {
+                    // stage ks+1 landed for every wave: stages up to min(ks + NS - 1, nk - 1) were issued
+                    vm_wait_groups<NI, NS - 2>(nk - 2 - ks < NS - 2 ? nk - 2 - ks : NS - 2);
+                    __syncthreads();
+                    // every wave has read its last fragments of stage ks: its buffer takes stage ks + NS
+                    if (ks + NS < nk) issue(ks + NS);
+                    fetch(cur ^ 1, lds + ((ks + 1) % NS) * STAGE, 0);
+                }
 #pragma unroll
                 for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
-                    for (int tb = 0; tb < 4; ++tb) acc[fb][tb] = mfma32x32x16(af[fb], bf[tb], acc[fb][tb]);
+                    for (int tb = 0; tb < 2; ++tb) acc[fb][tb] = mfma32x32x16(fa[cur][fb], fx[cur][tb], acc[fb][tb]);
             }
-            if (more) store(lds + (cur ^ 1) * STAGE);
-            __syncthreads();
-            cur ^= 1;
         }
+        __syncthreads();
     }
 };
-
-// feature offset (within a wave's 128) of accumulator register r of block fb for lane half hf
-__device__ __forceinline__ int feat(int fb, int r, int hf) { return 32 * fb + 8 * (r >> 2) + 4 * hf + (r & 3); }
 
 // Workgroup -> (token tile, feature tile). Workgroups are dispatched round-robin over the 8 XCDs, so the
 // feature tiles of one token tile are given consecutive slots of one XCD: its x rows are fetched into that
@@ -126,17 +156,18 @@ __device__ __forceinline__ void tile_order(int wg, int ntiles_n, int ntiles_t, i
 // Copy the two feature blocks of head HD (blocks 2HD, 2HD+1) of token block TB into plain registers
 // (static indices keep the accumulators in registers).
 template <int TB, int HD>
-__device__ __forceinline__ void copy_head(const f32x16 (&acc)[4][4], float (&v)[2][16]) {
+__device__ __forceinline__ void copy_head(const f32x16 (&acc)[4][2], float (&v)[2][16]) {
 #pragma unroll
     for (int half = 0; half < 2; ++half)
 #pragma unroll
         for (int r = 0; r < 16; ++r) v[half][r] = acc[2 * HD + half][TB][r];
 }
 
-// Epilogue staging: each wave writes its finished 128 x 128 tile into a private LDS region (rows padded
-// to kStg) and re-reads it as 16 B row chunks, so global stores are whole, contiguous lines. A wave's LDS
+// Epilogue staging: each wave writes its finished tile into a private LDS region (rows padded to kStg)
+// and re-reads it as 16 B row chunks, so global stores are whole, contiguous lines. A wave's LDS
 // instructions execute in order, so its own write -> read needs no barrier.
 constexpr int kStg = 136;
+constexpr int kStgV = 72;  // transposed V tile: [128 features][64 tokens]
 
 struct Pop {
     int members, tokens;
@@ -150,8 +181,8 @@ struct Rank1 {
 };
 
 // ------------------------------------------------------------------------------------------------
-// Q, K, V: rank-1 correction, value-embedding gate (V), rotary + per-head RMSNorm (Q, K),
-// written bf16 [m][H][T][64].
+// Q, K, V: rank-1 correction, value-embedding gate (V), rotary + per-head RMSNorm (Q, K); Q, K written
+// bf16 [m][H][T][64], V transposed [m][H][64][T].
 // ------------------------------------------------------------------------------------------------
 struct QkvArgs {
     Pop pop;
@@ -168,9 +199,13 @@ struct QkvArgs {
     __bf16 *out[3];           // q, k: [m][8][T][64]; v transposed: [m][8][64][T]
 };
 
-__global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
-    using M = Mma<256, 256, 64>;
-    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
+__global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
+    using M = Mma<8, 256, 256, 64, 2>;
+    // per-wave staging after the K loop: Q, K as [64 tokens][kStg], V^T as [128 features][kStgV]
+    constexpr int kWaveStg = 128 * kStgV;
+    static_assert(64 * kStg <= kWaveStg, "Q/K staging fits the wave's region");
+    constexpr int kLds = cmax(M::LDS_BYTES, 8 * kWaveStg * 2);
+    __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
     int nt, tt;
@@ -178,11 +213,11 @@ __global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
     const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
     const int n0 = nt * 256, mat = n0 / 512, nl0 = n0 % 512;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+    const int wn0 = M::wn0(wave), wm0 = M::wm0(wave);
 
-    f32x16 acc[4][4];
-    M::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512,
-                       lds, acc, tid, wn0, wm0);
+    f32x16 acc[4][2];
+    M::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds, acc, tid,
+           wn0, wm0);
 
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
@@ -190,23 +225,19 @@ __global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
     const int head0 = (nl0 + wn0) / 64;
     const float *arow = r1.a ? r1.a + dir * r1.a_stride + nl0 + wn0 : nullptr;
     __bf16 *outm = p.out[mat];
-    __bf16 *stg = lds + wave * 128 * kStg;
+    __bf16 *stg = lds + wave * kWaveStg;
 
     // one (token block, head) pair at a time: its 32 accumulators are copied out (static indices) so the
     // body below is compiled once and only one head's values are live
 #pragma unroll 1
-    for (int it = 0; it < 8; ++it) {
+    for (int it = 0; it < 4; ++it) {
         const int tb = it >> 1, hd = it & 1;
         float v[2][16];
         switch (it) {
             case 0: copy_head<0, 0>(acc, v); break;
             case 1: copy_head<0, 1>(acc, v); break;
             case 2: copy_head<1, 0>(acc, v); break;
-            case 3: copy_head<1, 1>(acc, v); break;
-            case 4: copy_head<2, 0>(acc, v); break;
-            case 5: copy_head<2, 1>(acc, v); break;
-            case 6: copy_head<3, 0>(acc, v); break;
-            default: copy_head<3, 1>(acc, v); break;
+            default: copy_head<1, 1>(acc, v); break;
         }
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
@@ -287,27 +318,23 @@ __global__ __launch_bounds__(256, 1) void qkv_kernel(QkvArgs p) {
                     store_bf16x4(stg + tl * kStg + f, o);
                 } else {
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) stg[(f + e) * kStg + tl] = (__bf16)v[half][4 * g + e];
+                    for (int e = 0; e < 4; ++e) stg[(f + e) * kStgV + tl] = (__bf16)v[half][4 * g + e];
                 }
             }
     }
-    // whole-line stores: Q, K rows [m][h][t][0:64] (128 B); V^T rows [m][h][d][t0 .. t0+128) (256 B)
+    // whole-line stores: Q, K rows [m][h][t][0:64] (128 B); V^T rows [m][h][d][t0+wm0 .. +64) (128 B)
 #pragma unroll
     for (int hd = 0; hd < 2; ++hd) {
         const int64_t hbase = ((int64_t)m * 8 + head0 + hd);
-        if (mat < 2) {
 #pragma unroll 4
-            for (int it = 0; it < 16; ++it) {
-                const int c = it * 64 + lane, row = c >> 3, ch = c & 7;
-                bf16x8 v = load_bf16x8(stg + row * kStg + 64 * hd + ch * 8);
-                store_bf16x8(outm + (hbase * T + t0 + wm0 + row) * 64 + ch * 8, v);
-            }
-        } else {
-#pragma unroll 4
-            for (int it = 0; it < 16; ++it) {
-                const int c = it * 64 + lane, d = c >> 4, ch = c & 15;
-                bf16x8 v = load_bf16x8(stg + (64 * hd + d) * kStg + ch * 8);
-                store_bf16x8(outm + (hbase * 64 + d) * T + t0 + wm0 + ch * 8, v);
+        for (int it = 0; it < 8; ++it) {
+            const int c = it * 64 + lane, r = c >> 3, ch = c & 7;
+            if (mat < 2) {
+                bf16x8 v = load_bf16x8(stg + r * kStg + 64 * hd + ch * 8);
+                store_bf16x8(outm + (hbase * T + t0 + wm0 + r) * 64 + ch * 8, v);
+            } else {
+                bf16x8 v = load_bf16x8(stg + (64 * hd + r) * kStgV + ch * 8);
+                store_bf16x8(outm + (hbase * 64 + r) * T + t0 + wm0 + ch * 8, v);
             }
         }
     }
@@ -347,17 +374,23 @@ struct ResidArgs {
 };
 
 template <int KD>
-__global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
-    using M = Mma<512, 128, 32>;
-    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
+__global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
+    using M = Mma<8, 512, 128, 64, 2>;
+    // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
+    // hi/lo rows of the split3 output), then the per-token statistics [128 tokens][4 feature waves][4].
+    constexpr int kStgF = 136;
+    constexpr int kEpi = 8 * 32 * kStgF * 4 + 128 * 4 * 4 * 4;
+    constexpr int kLds = cmax(M::LDS_BYTES, kEpi);
+    static_assert(32 * kStgF * 4 >= 64 * kStg * 2, "bf16 split3 staging must fit the wave's region");
+    __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 128;
     const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * 128;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int wn0 = 128 * wave;
+    const int wn0 = M::wn0(wave), wm0 = M::wm0(wave), wq = wave % 4;
 
-    f32x16 acc[4][4];
-    M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, 0);
+    f32x16 acc[4][2];
+    M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, wm0);
 
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
@@ -366,18 +399,14 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
         if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
         if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
     }
-    // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
-    // hi/lo rows of the split3 output), then the per-token statistics [128 tokens][4 waves][4].
-    constexpr int kStgF = 136;
-    static_assert(32 * kStgF * 4 >= 64 * kStg * 2, "bf16 split3 staging must fit the wave's region");
-    static_assert(4 * 32 * kStgF * 4 + 128 * 4 * 4 * 4 <= M::LDS_BYTES, "epilogue LDS");
     float *stgf = reinterpret_cast<float *>(lds) + wave * 32 * kStgF;
-    __bf16 *stgb = reinterpret_cast<__bf16 *>(reinterpret_cast<float *>(lds) + wave * 32 * kStgF);
-    float *red = reinterpret_cast<float *>(lds) + 4 * 32 * kStgF;
+    __bf16 *stgb = reinterpret_cast<__bf16 *>(stgf);
+    float *red = reinterpret_cast<float *>(lds) + 8 * 32 * kStgF;
 
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-        const int t = t0 + 32 * tb + j;
+    for (int tb = 0; tb < 2; ++tb) {
+        const int tl = wm0 + 32 * tb + j;
+        const int t = t0 + tl;
         const int64_t row = (int64_t)m * T + t;
         float corr = 0.f;
         if (p.r1.a) {
@@ -418,7 +447,7 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
             }
         if (p.xout) {
             // whole-line stores: 32 rows x 512 B of this wave's 128 features
-            float *xo = p.xout + ((int64_t)m * T + t0 + 32 * tb) * 512 + wn0;
+            float *xo = p.xout + ((int64_t)m * T + t0 + wm0 + 32 * tb) * 512 + wn0;
 #pragma unroll 4
             for (int it = 0; it < 16; ++it) {
                 const int c = it * 64 + lane, r = c >> 5, ch = c & 31;
@@ -429,13 +458,13 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
         for (int k = 0; k < 4; ++k) st[k] += swap_halves(st[k]);
         if (hf == 0) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) red[((32 * tb + j) * 4 + wave) * 4 + k] = st[k];
+            for (int k = 0; k < 4; ++k) red[(tl * 4 + wq) * 4 + k] = st[k];
         }
     }
     __syncthreads();
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-        const int tl = 32 * tb + j;
+    for (int tb = 0; tb < 2; ++tb) {
+        const int tl = wm0 + 32 * tb + j;
         const int t = t0 + tl;
         const int64_t row = (int64_t)m * T + t;
         float tot[4] = {0.f, 0.f, 0.f, 0.f};
@@ -461,7 +490,7 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
                 if (p.split3) store_bf16x4(stgb + (32 + j) * kStg + f0, lo);
             }
         const int width = p.split3 ? 1536 : 512;
-        __bf16 *hb = p.hout + ((int64_t)m * T + t0 + 32 * tb) * width + wn0;
+        __bf16 *hb = p.hout + ((int64_t)m * T + t0 + wm0 + 32 * tb) * width + wn0;
 #pragma unroll 4
         for (int it = 0; it < 8; ++it) {
             const int c = it * 64 + lane, r = c >> 4, ch = c & 15;
@@ -472,7 +501,7 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
                 store_bf16x8(hb + (int64_t)r * width + 1024 + ch * 8, hv);
             }
         }
-        if (wave == 0 && hf == 0) {
+        if (wq == 0 && hf == 0) {
             for (int k = 0; k < p.nnext; ++k) p.ndots[row * p.nnext + k] = rstd * tot[1 + k];
         }
     }
@@ -480,7 +509,7 @@ __global__ __launch_bounds__(256, 1) void resid_kernel(ResidArgs p) {
 
 // ------------------------------------------------------------------------------------------------
 // MLP hidden (mlp.c_fc, N = 2048): act = relu(x W^T + sign * dot * a)^2 as bf16, and the partial dots
-// act . b of the following mlp.c_proj over this wave's 128 features: pdots[row][n / 128].
+// act . b of the following mlp.c_proj over each wave's 128 features: pdots[row][n / 128].
 // ------------------------------------------------------------------------------------------------
 struct FcArgs {
     Pop pop;
@@ -495,9 +524,10 @@ struct FcArgs {
     float *pdots;             // [rows][16]
 };
 
-__global__ __launch_bounds__(256, 1) void fc_kernel(FcArgs p) {
-    using M = Mma<256, 256, 64>;
-    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
+__global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
+    using M = Mma<8, 256, 256, 64, 2>;
+    constexpr int kLds = cmax(M::LDS_BYTES, 8 * 64 * kStg * 2);  // K loop, then per-wave act staging
+    __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
     int nt, tt;
@@ -505,20 +535,20 @@ __global__ __launch_bounds__(256, 1) void fc_kernel(FcArgs p) {
     const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
     const int n0 = nt * 256;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+    const int wn0 = M::wn0(wave), wm0 = M::wm0(wave);
 
-    f32x16 acc[4][4];
-    M::run(p.w + (int64_t)n0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds,
-                       acc, tid, wn0, wm0);
+    f32x16 acc[4][2];
+    M::run(p.w + (int64_t)n0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds, acc, tid, wn0,
+           wm0);
 
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
     const int nf0 = n0 + wn0;
     const float *arow = p.r1.a ? p.r1.a + dir * p.r1.a_stride + nf0 : nullptr;
     const float *brow = p.nb ? p.nb + dir * p.nb_stride + nf0 : nullptr;
-    __bf16 *stg = lds + wave * 128 * kStg;
+    __bf16 *stg = lds + wave * 64 * kStg;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tb = 0; tb < 2; ++tb) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
         const float corr = arow ? sgn * p.dots[row] : 0.f;
@@ -548,9 +578,9 @@ __global__ __launch_bounds__(256, 1) void fc_kernel(FcArgs p) {
     // whole-line stores of act rows [m][t][nf0 .. nf0 + 128) (256 B each)
     __bf16 *abase = p.act + ((int64_t)m * T + t0 + wm0) * 2048 + nf0;
 #pragma unroll 4
-    for (int it = 0; it < 32; ++it) {
-        const int c = it * 64 + lane, row = c >> 4, ch = c & 15;
-        store_bf16x8(abase + (int64_t)row * 2048 + ch * 8, load_bf16x8(stg + row * kStg + ch * 8));
+    for (int it = 0; it < 16; ++it) {
+        const int c = it * 64 + lane, r = c >> 4, ch = c & 15;
+        store_bf16x8(abase + (int64_t)r * 2048 + ch * 8, load_bf16x8(stg + r * kStg + ch * 8));
     }
 }
 
@@ -571,8 +601,8 @@ struct LowrankArgs {
     int64_t ys_m, ys_t;
 };
 
-__global__ __launch_bounds__(256, 1) void lowrank_kernel(LowrankArgs p) {
-    using M = Mma<256, 256, 64>;
+__global__ __launch_bounds__(kThreads) void lowrank_kernel(LowrankArgs p) {
+    using M = Mma<8, 256, 256, 64, 2>;
     __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
     const int T = p.pop.tokens, ntiles = p.N / 256, tiles_t = T / 256;
     int nt, tt;
@@ -580,16 +610,16 @@ __global__ __launch_bounds__(256, 1) void lowrank_kernel(LowrankArgs p) {
     const int m = tt / tiles_t, t0 = (tt % tiles_t) * 256;
     const int n0 = nt * 256;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+    const int wn0 = M::wn0(wave), wm0 = M::wm0(wave);
 
-    f32x16 acc[4][4];
-    M::run(p.w + (int64_t)n0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds,
-                       acc, tid, wn0, wm0);
+    f32x16 acc[4][2];
+    M::run(p.w + (int64_t)n0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds, acc, tid, wn0,
+           wm0);
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;
     const int nf0 = n0 + wn0;
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tb = 0; tb < 2; ++tb) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
         const float corr = p.r1.a ? sgn * p.dots[row] : 0.f;
@@ -634,31 +664,31 @@ struct HeadArgs {
     float *loss;              // [m][T] per-token CE (0 where target < 0)
 };
 
-__global__ __launch_bounds__(256, 1) void head_ce_kernel(HeadArgs p) {
-    using M = Mma<256, 256, 64>;
+__global__ __launch_bounds__(kThreads) void head_ce_kernel(HeadArgs p) {
+    using M = Mma<8, 256, 256, 64, 2>;
     __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
     const int T = p.pop.tokens, tiles_t = T / 256;
     const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * 256;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int wn0 = 128 * (wave & 1), wm0 = 128 * (wave >> 1);
+    const int wn0 = M::wn0(wave), wm0 = M::wm0(wave), wq = wave % 2;
     const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;
 
-    float corr[4];
-    int64_t tgt[4];
-    float sum[4] = {0.f, 0.f, 0.f, 0.f}, zt[4] = {0.f, 0.f, 0.f, 0.f};
+    float corr[2];
+    int64_t tgt[2];
+    float sum[2] = {0.f, 0.f}, zt[2] = {0.f, 0.f};
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tb = 0; tb < 2; ++tb) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
         corr[tb] = p.r1.a ? sgn * p.dots[row] : 0.f;
         tgt[tb] = p.targets[m * p.targets_sm + t];
     }
     const float k1 = (2.0f / 15.0f) * kLog2e, k2 = -30.0f * kLog2e;
-    f32x16 acc[4][4];
+    f32x16 acc[4][2];
     for (int v0 = 0; v0 < p.vocab; v0 += 256) {
-        M::run(p.w + (int64_t)v0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds,
-                           acc, tid, wn0, wm0);
+        M::run(p.w + (int64_t)v0 * p.K, p.K, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, p.K, lds, acc, tid, wn0,
+               wm0);
         const int nf0 = v0 + wn0;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
@@ -667,7 +697,7 @@ __global__ __launch_bounds__(256, 1) void head_ce_kernel(HeadArgs p) {
                 const int f = nf0 + 32 * fb + 8 * g + 4 * hf;
                 float4 a4 = p.r1.a ? ld4(p.r1.a + dir * p.r1.a_stride + f) : float4{0, 0, 0, 0};
 #pragma unroll
-                for (int tb = 0; tb < 4; ++tb)
+                for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float l = acc[fb][tb][4 * g + e] + corr[tb] * f4get(a4, e);
@@ -679,21 +709,21 @@ __global__ __launch_bounds__(256, 1) void head_ce_kernel(HeadArgs p) {
             }
     }
     // combine the two lane halves and the two feature waves
-    float *red = reinterpret_cast<float *>(lds);  // [256 tokens][2 waves][2]
+    float *red = reinterpret_cast<float *>(lds);  // [256 tokens][2 feature waves][2]
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tb = 0; tb < 2; ++tb) {
         sum[tb] += swap_halves(sum[tb]);
         zt[tb] += swap_halves(zt[tb]);
         if (hf == 0) {
             const int tl = wm0 + 32 * tb + j;
-            red[(tl * 2 + (wave & 1)) * 2 + 0] = sum[tb];
-            red[(tl * 2 + (wave & 1)) * 2 + 1] = zt[tb];
+            red[(tl * 2 + wq) * 2 + 0] = sum[tb];
+            red[(tl * 2 + wq) * 2 + 1] = zt[tb];
         }
     }
     __syncthreads();
-    if ((wave & 1) == 0 && hf == 0) {
+    if (wq == 0 && hf == 0) {
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
+        for (int tb = 0; tb < 2; ++tb) {
             const int tl = wm0 + 32 * tb + j;
             const float s = red[(tl * 2) * 2] + red[(tl * 2 + 1) * 2];
             const float z = red[(tl * 2) * 2 + 1] + red[(tl * 2 + 1) * 2 + 1];
@@ -778,7 +808,7 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
     NOISE_CHECK_ARG(!a.ve_r1.a || (aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
                     "%s: value-embedding noise b rows must be 16 B aligned", fn);
     dim3 grid((unsigned)(6 * pop->members * (pop->tokens / 256)));
-    hipLaunchKernelGGL(qkv_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(qkv_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 
@@ -818,9 +848,9 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     }
     dim3 grid((unsigned)(pop->members * (pop->tokens / 128)));
     if (K == 512)
-        hipLaunchKernelGGL(resid_kernel<512>, grid, dim3(256), 0, (hipStream_t)stream, a);
+        hipLaunchKernelGGL(resid_kernel<512>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     else
-        hipLaunchKernelGGL(resid_kernel<2048>, grid, dim3(256), 0, (hipStream_t)stream, a);
+        hipLaunchKernelGGL(resid_kernel<2048>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 
@@ -845,7 +875,7 @@ extern "C" int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const
     a.nb_stride = (next && next->b) ? next->b_stride : 0;
     a.pdots = a.nb ? partial_dots : nullptr;
     dim3 grid((unsigned)(8 * pop->members * (pop->tokens / 256)));
-    hipLaunchKernelGGL(fc_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(fc_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 
@@ -868,7 +898,7 @@ extern "C" int noise_pop_linear(const noise_population_t *pop, noise_view_t x, c
     a.dots = dots; a.y = y; a.y_fp32 = y_fp32; a.ys_m = ys_m; a.ys_t = ys_t;
     int64_t grid = (N / 256) * pop->members * (pop->tokens / 256);
     NOISE_CHECK_ARG(grid < (1ll << 31), "%s: too many tiles", fn);
-    hipLaunchKernelGGL(lowrank_kernel, dim3((unsigned)grid), dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(lowrank_kernel, dim3((unsigned)grid), dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 
@@ -889,6 +919,6 @@ extern "C" int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, 
     a.r1 = make_r1(r1);
     a.dots = dots; a.targets = targets; a.targets_sm = targets_sm; a.loss = token_loss;
     dim3 grid((unsigned)(pop->members * (pop->tokens / 256)));
-    hipLaunchKernelGGL(head_ce_kernel, grid, dim3(256), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(head_ce_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }

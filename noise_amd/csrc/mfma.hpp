@@ -39,6 +39,45 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 lo, bf16x4 hi) {
     return bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// Direct global -> LDS copy (global_load_lds_dwordx4): lane i fetches 16 B from base + off_i (base wave-uniform,
+// off_i a 32-bit byte offset); the wave's 64 results land contiguously at LDS address l + 16 * i (l
+// wave-uniform). Issued through inline asm so that the compiler's wait-count pass, which would otherwise
+// wait for every outstanding copy before each LDS read, leaves the pipeline to the explicit vm_wait below.
+// Such loads only add to vmcnt, so the compiler's own waits for its loads stay correct (they can only
+// become stricter). M0 is saved and restored.
+__device__ __forceinline__ void lds_dma16(const void *base, unsigned off, const void *l) {
+    const unsigned la =
+        __builtin_amdgcn_readfirstlane((unsigned)(size_t)((__attribute__((address_space(3))) const void *)l));
+    unsigned save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "v"(off), "s"(base), "s"(la)
+                 : "memory");
+}
+
+// s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone)
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+// wait until at most r groups of G loads remain in flight (0 <= r <= RMAX, r known at run time only)
+template <int G, int RMAX>
+__device__ __forceinline__ void vm_wait_groups(int r) {
+    static_assert(RMAX <= 3, "extend for deeper pipelines");
+    if constexpr (RMAX >= 3) {
+        if (r >= 3) { vm_wait<3 * G>(); return; }
+    }
+    if constexpr (RMAX >= 2) {
+        if (r == 2) { vm_wait<2 * G>(); return; }
+    }
+    if constexpr (RMAX >= 1) {
+        if (r == 1) { vm_wait<G>(); return; }
+    }
+    vm_wait<0>();
+}
+
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Value of lane (l ^ 32): the other half of a 32x32 MFMA column.
