@@ -74,14 +74,20 @@ int noise_gather_slices(float *out, int64_t nrows, int64_t width, const int64_t 
  * `attention(q, k, v, window)` (flex_attention with the block mask q >= k & q - k <= window,
  * model.py:17-21; scale 1/sqrt(head_dim), torch: nn/attention/flex_attention.py:1543-1544).
  * q, k, o: element (b, t, h, d) at b*s_b + h*s_h + t*s_t + d (the reference's [B, T, H, D] and its
- * transposes are all expressible). v: the same with vs_x = token stride when v_transposed == 0, or
- * element (b, t, h, d) at b*vs_b + h*vs_h + d*vs_x + t when v_transposed == 1. head_dim must be 64.
- * Optional fused output (dot_out != NULL): dot_out[(b*seq + t)*heads + h] = sum_d o[b,t,h,d] *
- * dot_vec[(b / dot_div)*dot_vec_stride + h*64 + d], with o the bf16 output values; this is the
- * per-head part of the next perturbed linear's x.b (eggroll.py:58), NULL to skip. */
+ * transposes are all expressible). v: the same with vs_x = token stride, or, with flag
+ * NOISE_ATTN_V_TRANSPOSED, element (b, t, h, d) at b*vs_b + h*vs_h + d*vs_x + t. head_dim must be 64.
+ * NOISE_ATTN_QK_NORMED: the caller guarantees every q and k row has RMS <= 1, as RMSNorm outputs do (the
+ * reference normalises both, utils/model.py:94); scores are then bounded and the softmax runs with a
+ * fixed shift instead of a running maximum (same result; rows that break the promise by less than a
+ * factor of about 3 in RMS still stay finite). Optional fused output (dot_out != NULL):
+ * dot_out[(b*seq + t)*heads + h] = sum_d o[b,t,h,d] * dot_vec[(b / dot_div)*dot_vec_stride + h*64 + d],
+ * with o the bf16 output values; this is the per-head part of the next perturbed linear's x.b
+ * (eggroll.py:58), NULL to skip. */
+#define NOISE_ATTN_V_TRANSPOSED 1
+#define NOISE_ATTN_QK_NORMED 2
 int noise_attention_fwd(const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
                         int64_t seq, int64_t head_dim, int64_t qs_b, int64_t qs_h, int64_t qs_t, int64_t ks_b,
-                        int64_t ks_h, int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_x, int v_transposed,
+                        int64_t ks_h, int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_x, int flags,
                         int64_t os_b, int64_t os_h, int64_t os_t, int64_t window, float scale,
                         const float *dot_vec, int64_t dot_vec_stride, int64_t dot_div, float *dot_out,
                         noise_stream_t stream);

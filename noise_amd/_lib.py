@@ -39,6 +39,10 @@ SIGNATURES = {
 }
 _RESTYPES = {'noise_last_error': ctypes.c_char_p}
 
+# noise_attention_fwd flags (include/noise_amd.h)
+ATTN_V_TRANSPOSED = 1
+ATTN_QK_NORMED = 2
+
 
 class View(ctypes.Structure):
     """noise_view_t: element (m, t, j) at ptr + m*sm + t*st + j."""

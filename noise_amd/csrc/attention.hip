@@ -40,6 +40,7 @@ struct AttnArgs {
     int window;
     int xcd_grouped;                    // 1: bh_total % 8 == 0, map heads onto XCDs
     float scale_log2;                   // softmax scale * log2(e)
+    float shift;                        // fixed log2-domain shift of the bounded-score kernel
     // optional fused output: dot[b, t, h] = sum_d O[b,t,h,d] * dvec[(b / ddiv) * ds_b + h*D + d]
     const float *dvec;
     float *dot;
@@ -260,6 +261,213 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
     }
 }
 
+
+// ------------------------------------------------------------------------------------------------
+// Transposed-V kernel (the population layout; seq a multiple of 64). K and V^T tiles are copied
+// global -> LDS directly (global_load_lds_dwordx4) into a ring of three stages, rows of 128 B with the
+// 16 B chunks XOR-swizzled by row pair (conflict-free fragment reads). The K rows of each 32-key block
+// are read in the order sigma (bits 2 and 3 of the key index swapped), which makes register r of a
+// lane's S^T block hold key 16 (r / 8) + 8 hf + (r % 8): the 8 scores P^T needs as one B fragment of
+// O^T = V^T P^T are consecutive keys, so V^T is read as plain 16 B fragments and P is packed with four
+// v_cvt_pk_bf16_f32. BOUNDED: the caller guarantees q and k rows of RMS <= 1 (RMSNorm outputs, as
+// utils/model.py:94 applies to both), so |score * scale * log2 e| <= D * scale * log2 e (+ bf16 rounding)
+// = shift, and exp2(score * scale * log2 e - shift) <= 1 needs no running maximum (softmax is
+// shift-invariant; fp32 and bf16 keep full relative precision down to 2^-126).
+// ------------------------------------------------------------------------------------------------
+constexpr int kStage = 2 * 64 * 128;  // K [64 keys][64 d] then V^T [64 d][64 keys], 128 B rows
+constexpr int kNS = 3;
+
+__device__ __forceinline__ int key_sigma(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
+
+template <bool BOUNDED>
+__global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
+    __shared__ __attribute__((aligned(16))) char lds[kNS * kStage];
+
+    int wg = blockIdx.x;
+    int bh, qt;
+    if (a.xcd_grouped) {
+        int xcd = wg & 7, slot = wg >> 3;
+        bh = (slot / a.qtiles) * 8 + xcd;
+        qt = a.qtiles - 1 - (slot % a.qtiles);
+    } else {
+        bh = wg / a.qtiles;
+        qt = a.qtiles - 1 - (wg % a.qtiles);
+    }
+    const int b = bh / a.heads, h = bh - b * a.heads;
+    const __bf16 *Qb = a.q + b * a.qs_b + h * a.qs_h;
+    const __bf16 *Kb = a.k + b * a.ks_b + h * a.ks_h;
+    const __bf16 *Vb = a.v + b * a.vs_b + h * a.vs_h;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int j = lane & 31, hf = lane >> 5;
+    const int T = a.seq, W = a.window;
+    const int q0w = qt * kBQ + wave * kQW;
+
+    bf16x8 qf[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qf[qb][s] = load_bf16x8(Qb + (int64_t)(q0w + 32 * qb + j) * a.qs_t + 16 * s + 8 * hf);
+
+    // copies: per stage 16 of 1 KB (8 rows); wave w issues copies c = 4 i + w, rows 8 (c % 8) .. of K (c < 8)
+    // or V^T. Row R's slot P holds chunk P ^ ((R >> 1) & 7); for this lane R = 8 c' + lane / 8, so the chunk
+    // it fetches is (lane % 8) ^ (4 (c' & 1) + lane / 16), the same for all of a wave's copies (c' & 1 = w & 1).
+    const int chunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
+    const unsigned koff = (unsigned)((lane >> 3) * a.ks_t * 2 + chunk * 16);
+    const unsigned voff = (unsigned)((lane >> 3) * a.vs_x * 2 + chunk * 16);
+    auto issue = [&](int k0, char *st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int c = 4 * i + wave;
+            if (c < 8)
+                lds_dma16(Kb + (int64_t)(k0 + 8 * c) * a.ks_t, koff, st + c * 1024);
+            else
+                lds_dma16(Vb + (int64_t)(8 * (c - 8)) * a.vs_x + k0, voff, st + c * 1024);
+        }
+    };
+    // fragment byte offsets within a stage for k-step s: K row sigma(j) (+32 kb), V^T row j (+32 db)
+    const int sj = key_sigma(j);
+    int kfo[4], vfo[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        kfo[s] = sj * 128 + (((2 * s + hf) ^ ((sj >> 1) & 7)) << 4);
+        vfo[s] = 64 * 128 + j * 128 + (((2 * s + hf) ^ ((j >> 1) & 7)) << 4);
+    }
+
+    float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};
+    f32x16 o[2][2];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x16{};
+
+    const int wg_q_lo = qt * kBQ;
+    const int wg_q_hi = wg_q_lo + kBQ - 1;
+    const int kv_first = max(0, wg_q_lo - W) / kBKV;
+    const int kv_last = wg_q_hi / kBKV;
+    const int nt = kv_last - kv_first + 1;
+    const int wq_lo = q0w, wq_hi = q0w + kQW - 1;
+    const float c2 = a.scale_log2, shift = a.shift;
+
+    issue(kv_first * kBKV, lds);
+    if (nt > 1) issue((kv_first + 1) * kBKV, lds + kStage);
+
+#pragma unroll 1
+    for (int it = 0; it < nt; ++it) {
+        vm_wait_groups<4, 1>(it + 1 < nt ? 1 : 0);  // tile it landed; tile it + 1 may be in flight
+        __syncthreads();                              // ... for every wave; tile it - 1 fully read
+        if (it + 2 < nt) issue((kv_first + it + 2) * kBKV, lds + ((it + 2) % kNS) * kStage);
+        const char *st = lds + (it % kNS) * kStage;
+        const int k0 = (kv_first + it) * kBKV;
+        const bool active = k0 <= wq_hi && k0 + kBKV - 1 >= wq_lo - W;
+        if (!active) continue;
+        const bool edge = (k0 + kBKV - 1 > wq_lo) || (k0 < wq_hi - W);
+
+        f32x16 sc[2][2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int qb = 0; qb < 2; ++qb) sc[kb][qb] = f32x16{};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(st + kfo[s] + kb * 32 * 128);
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) sc[kb][qb] = mfma32x32x16(ka, qf[qb][s], sc[kb][qb]);
+            }
+        }
+
+        bf16x8 pf[2][4];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            const int q = q0w + 32 * qb + j;
+            if (edge) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) {
+                        const int kv = k0 + 32 * kb + 16 * (r >> 3) + 8 * hf + (r & 7);
+                        const bool vis = kv <= q && q - kv <= W;
+                        sc[kb][qb][r] = vis ? sc[kb][qb][r] : -__builtin_inff();
+                    }
+            }
+            float mb;
+            if constexpr (BOUNDED) {
+                mb = shift;
+            } else {
+                float mx = -__builtin_inff();
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][qb][r]);
+                mx = fmaxf(mx, swap_halves(mx));
+                const float m_new = fmaxf(m[qb], mx * c2);
+                const float alpha = exp2_fast(m[qb] - m_new);
+                m[qb] = m_new;
+                l[qb] *= alpha;
+#pragma unroll
+                for (int db = 0; db < 2; ++db) o[db][qb] *= alpha;
+                mb = m_new;
+            }
+            float rs = 0.f;
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const float p = exp2_fast(__builtin_fmaf(sc[kb][qb][r], c2, -mb));
+                    sc[kb][qb][r] = p;
+                    rs += p;
+                }
+            l[qb] += rs;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                bf16x8 v;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = (__bf16)sc[s >> 1][qb][8 * (s & 1) + e];
+                pf[qb][s] = v;
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+#pragma unroll
+            for (int db = 0; db < 2; ++db) {
+                const bf16x8 va = *reinterpret_cast<const bf16x8 *>(st + vfo[s] + db * 32 * 128);
+#pragma unroll
+                for (int qb = 0; qb < 2; ++qb) o[db][qb] = mfma32x32x16(va, pf[qb][s], o[db][qb]);
+            }
+        }
+    }
+
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int q = q0w + 32 * qb + j;
+        const float lt = l[qb] + swap_halves(l[qb]);
+        const float inv = 1.0f / lt;  // the diagonal key is always visible: lt > 0
+        float dsum = 0.f;
+        const float *dv = a.dot ? a.dvec + (int64_t)(b / a.ddiv) * a.ds_b + h * kD : nullptr;
+        __bf16 *orow = a.o + b * a.os_b + h * a.os_h + (int64_t)q * a.os_t;
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                bf16x4 v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = (__bf16)(o[db][qb][4 * g + e] * inv);
+                const int d = 32 * db + 8 * g + 4 * hf;
+                store_bf16x4(orow + d, v);
+                if (dv) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dsum += (float)v[e] * dv[d + e];
+                }
+            }
+        if (a.dot) {
+            dsum += swap_halves(dsum);
+            if (hf == 0) a.dot[((int64_t)b * T + q) * a.heads + h] = dsum;
+        }
+    }
+}
+
 }  // namespace
 }  // namespace noise
 
@@ -268,11 +476,14 @@ using namespace noise;
 extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, void *o, int64_t batch,
                                    int64_t heads, int64_t seq, int64_t head_dim, int64_t qs_b, int64_t qs_h,
                                    int64_t qs_t, int64_t ks_b, int64_t ks_h, int64_t ks_t, int64_t vs_b,
-                                   int64_t vs_h, int64_t vs_x, int v_transposed, int64_t os_b, int64_t os_h,
+                                   int64_t vs_h, int64_t vs_x, int flags, int64_t os_b, int64_t os_h,
                                    int64_t os_t, int64_t window, float scale, const float *dot_vec,
                                    int64_t dot_vec_stride, int64_t dot_div, float *dot_out,
                                    noise_stream_t stream) {
     clear_error();
+    NOISE_CHECK_ARG((flags & ~(NOISE_ATTN_V_TRANSPOSED | NOISE_ATTN_QK_NORMED)) == 0,
+                    "noise_attention_fwd: unknown flags 0x%x", flags);
+    const bool v_transposed = flags & NOISE_ATTN_V_TRANSPOSED;
     NOISE_CHECK_ARG(head_dim == kD, "noise_attention_fwd: head_dim must be 64, got %lld", (long long)head_dim);
     NOISE_CHECK_ARG(batch >= 0 && heads > 0 && seq >= 0, "noise_attention_fwd: bad batch/heads/seq");
     NOISE_CHECK_ARG(seq <= (1 << 30) && window >= 0, "noise_attention_fwd: seq too large or window < 0");
@@ -306,8 +517,15 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     a.xcd_grouped = (bh % 8 == 0) ? 1 : 0;
     a.scale_log2 = scale * kLog2e;
     a.dvec = dot_vec; a.dot = dot_out; a.ds_b = dot_vec_stride; a.ddiv = (int)dot_div;
+    // rows of RMS <= 1 (rounded to bf16): |q . k| <= D (1 + 2^-8)^2 < 1.0079 D
+    a.shift = kD * fabsf(scale) * kLog2e * 1.0079f;
     dim3 grid((unsigned)(bh * qtiles));
-    if (v_transposed)
+    if (v_transposed && seq % kBQ == 0) {
+        if (flags & NOISE_ATTN_QK_NORMED)
+            hipLaunchKernelGGL(attention_vt_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(attention_vt_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, a);
+    } else if (v_transposed)
         hipLaunchKernelGGL(attention_fwd_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
     else
         hipLaunchKernelGGL(attention_fwd_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, a);

@@ -18,6 +18,7 @@ import math
 import torch
 
 from . import _lib
+from ._lib import ATTN_QK_NORMED, ATTN_V_TRANSPOSED
 from .model import rotary_tables, window_sizes, has_ve, N_EMBD, N_HEAD, HEAD_DIM, VOCAB
 from .noise import DeviceGenerator
 
@@ -238,7 +239,8 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
         yv = B.y.view(m, T, N_HEAD, HEAD_DIM)
         _call('noise_attention_fwd', q4.data_ptr(), k4.data_ptr(), vt.data_ptr(), yv.data_ptr(), m, N_HEAD, T,
                   HEAD_DIM, q4.stride(0), q4.stride(2), q4.stride(1), k4.stride(0), k4.stride(2), k4.stride(1),
-                  vt.stride(0), vt.stride(1), vt.stride(2), 1, yv.stride(0), yv.stride(2), yv.stride(1),
+                  vt.stride(0), vt.stride(1), vt.stride(2), ATTN_V_TRANSPOSED | ATTN_QK_NORMED,
+                  yv.stride(0), yv.stride(2), yv.stride(1),
                   W.windows[i], 1.0 / math.sqrt(HEAD_DIM), None if no is None else no[1].data_ptr(),
                   0 if no is None else no[1].stride(0), dir_div, None if no is None else B.d_attn.data_ptr(),
                   stream, label=f'window {W.windows[i]}')

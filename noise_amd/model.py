@@ -11,6 +11,7 @@ import torch
 from torch import nn
 
 from . import _lib
+from ._lib import ATTN_QK_NORMED, ATTN_V_TRANSPOSED
 
 BF16 = torch.bfloat16
 N_LAYER, N_HEAD, HEAD_DIM, N_EMBD, VOCAB, SEQ = 8, 8, 64, 512, 4096, 2048
@@ -160,9 +161,11 @@ def attention(q, k, v, window):
     return out if q.dtype == BF16 else out.to(q.dtype)
 
 
-def attention_raw(q, k, v, out, window, v_transposed=False, dot_vec=None, dot_div=1, dot_out=None):
+def attention_raw(q, k, v, out, window, v_transposed=False, dot_vec=None, dot_div=1, dot_out=None,
+                  qk_normed=False):
     """Kernel-level entry used by the population path: q, k, out [B, H, T, D] or [B, T, H, D] views,
-    v [B, H, D, T] when v_transposed; optional fused per-head dot with dot_vec [B / dot_div, H*D]."""
+    v [B, H, D, T] when v_transposed; optional fused per-head dot with dot_vec [B / dot_div, H*D].
+    qk_normed promises q and k rows of RMS <= 1 (RMSNorm outputs): the softmax then needs no running max."""
     B, T, H, D = out.shape
     if v_transposed:
         vs = (v.stride(0), v.stride(1), v.stride(2))  # v viewed as [B, H, D, T]
@@ -170,7 +173,8 @@ def attention_raw(q, k, v, out, window, v_transposed=False, dot_vec=None, dot_di
         vs = (v.stride(0), v.stride(2), v.stride(1))
     _lib.call('noise_attention_fwd', q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, T, D,
               q.stride(0), q.stride(2), q.stride(1), k.stride(0), k.stride(2), k.stride(1), *vs,
-              1 if v_transposed else 0, out.stride(0), out.stride(2), out.stride(1), int(window),
+              (ATTN_V_TRANSPOSED if v_transposed else 0) | (ATTN_QK_NORMED if qk_normed else 0),
+              out.stride(0), out.stride(2), out.stride(1), int(window),
               1.0 / math.sqrt(D), _lib.ptr(dot_vec), 0 if dot_vec is None else dot_vec.stride(0), dot_div,
               _lib.ptr(dot_out), _lib.stream_ptr(out.device))
     return out

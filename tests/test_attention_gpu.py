@@ -74,23 +74,75 @@ def test_strided_views_and_fp32_inputs():
     rel_ok(out, fp32_reference_gpu(q.bfloat16(), k.bfloat16(), v.bfloat16(), 200))
 
 
-def test_transposed_v_and_fused_dot():
-    """Population layout: q, k [B, H, T, D], v^T [B, H, D, T], fused x.b dot per head."""
-    from noise_amd.model import attention, attention_raw
+def _rms_normed(x):
+    return (x.float() / torch.sqrt((x.float() ** 2).mean(-1, keepdim=True) + torch.finfo(torch.float32).eps)).bfloat16()
+
+
+@pytest.mark.parametrize('qk_normed', [False, True])
+def test_transposed_v_and_fused_dot(qk_normed):
+    """Population layout: q, k [B, H, T, D], v^T [B, H, D, T], fused x.b dot per head; with and without the
+    RMS-normed promise (q, k are RMSNorm outputs, as utils/model.py:94 makes them)."""
+    from noise_amd.model import attention_raw
     g = torch.Generator().manual_seed(3)
     B, H, T = 4, 8, 256
     q, k, v = (torch.randn(B, T, H, 64, generator=g).bfloat16().to(DEV) for _ in range(3))
-    ref = attention(q, k, v, 100)
+    q, k = _rms_normed(q), _rms_normed(k)
     qh, kh = q.transpose(1, 2).contiguous(), k.transpose(1, 2).contiguous()
     vt = v.permute(0, 2, 3, 1).contiguous()  # [B, H, D, T]
     out = torch.empty(B, T, H, 64, dtype=torch.bfloat16, device=DEV)
     dvec = torch.randn(B // 2, H * 64, generator=g).to(DEV)
     dot = torch.empty(B, T, H, device=DEV)
     attention_raw(qh.transpose(1, 2), kh.transpose(1, 2), vt, out, 100, v_transposed=True, dot_vec=dvec,
-                  dot_div=2, dot_out=dot)
-    assert torch.equal(out, ref)
+                  dot_div=2, dot_out=dot, qk_normed=qk_normed)
+    rel_ok(out, fp32_reference_gpu(q, k, v, 100))
     expect = (out.float().view(B, T, H, 64) * dvec.repeat_interleave(2, 0).view(B, 1, H, 64)).sum(-1)
     assert torch.allclose(dot, expect, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize('window', [1024, 2048])
+def test_transposed_v_population_shape(window):
+    """[2 members, 8 heads, 2048 tokens], RMS-normed q, k (seed 5): the fixed-shift softmax and the
+    running-max softmax of the transposed-V kernel both match the fp32 reference, and each other closely."""
+    from noise_amd.model import attention_raw
+    g = torch.Generator().manual_seed(5)
+    B, H, T = 2, 8, 2048
+    q, k = (_rms_normed(torch.randn(B, T, H, 64, generator=g)).to(DEV) for _ in range(2))
+    v = torch.randn(B, T, H, 64, generator=g).bfloat16().to(DEV)
+    vt = v.permute(0, 2, 3, 1).contiguous()
+    ref = fp32_reference_gpu(q, k, v, window)
+    outs = []
+    for normed in (True, False):
+        out = torch.empty(B, T, H, 64, dtype=torch.bfloat16, device=DEV)
+        attention_raw(q, k, vt, out, window, v_transposed=True, qk_normed=normed)
+        rel_ok(out, ref)
+        outs.append(out.float())
+    assert (outs[0] - outs[1]).abs().max().item() <= 2e-2 * ref.abs().max().item()
+
+
+def test_transposed_v_normed_promise_broken_stays_finite():
+    """q, k of RMS 2.5 (scores up to ~6x the normed bound) under the fixed shift: still finite and right."""
+    from noise_amd.model import attention_raw
+    g = torch.Generator().manual_seed(6)
+    B, H, T = 1, 8, 512
+    q, k = ((2.5 * _rms_normed(torch.randn(B, T, H, 64, generator=g)).float()).bfloat16().to(DEV) for _ in range(2))
+    v = torch.randn(B, T, H, 64, generator=g).bfloat16().to(DEV)
+    out = torch.empty(B, T, H, 64, dtype=torch.bfloat16, device=DEV)
+    attention_raw(q, k, v.permute(0, 2, 3, 1).contiguous(), out, 300, v_transposed=True, qk_normed=True)
+    assert torch.isfinite(out.float()).all()
+    rel_ok(out, fp32_reference_gpu(q, k, v, 300))
+
+
+def test_transposed_v_ragged_length():
+    """T = 300 (not a multiple of the 256-query tile) in the transposed layout takes the general kernel."""
+    from noise_amd.model import attention_raw
+    g = torch.Generator().manual_seed(7)
+    B, H, T = 2, 3, 300
+    q, k, v = (torch.randn(B, T, H, 64, generator=g).bfloat16().to(DEV) for _ in range(3))
+    vt = torch.zeros(B, H, 64, 304, dtype=torch.bfloat16, device=DEV)  # token stride 304: 16 B aligned rows
+    vt[..., :T] = v.permute(0, 2, 3, 1)
+    out = torch.empty(B, T, H, 64, dtype=torch.bfloat16, device=DEV)
+    attention_raw(q, k, vt, out, 77, v_transposed=True, qk_normed=False)
+    rel_ok(out, fp32_reference_gpu(q, k, v, 77))
 
 
 def test_deterministic():

@@ -1,7 +1,7 @@
 """Population forward (eggroll.py:66-103) on the GPU vs the fp32 CPU oracle (oracle/model.py).
 
-Bar: per-member mean CE within 1e-3 absolute (BASELINE: per-member losses within 1e-3 of fp32), and the
-antithetic fitness L[2i+1] - L[2i] within 1e-3. At the seed-0 init the head is tiny (std 0.001) and
+Bar: per-member mean CE within 1e-3 absolute of the fp32 oracle, and the antithetic fitness
+L[2i+1] - L[2i], a difference of two such losses, within 2e-3. At the seed-0 init the head is tiny (std 0.001) and
 every loss sits at ln 4096 whatever the blocks compute, so most cases also scale the head (x30: logits of
 order 1, the loss ~0.3 off ln 4096) to make the loss depend on the hidden state; a wrong block then moves
 the loss by far more than the tolerance. (With x300, bf16 rounding of the head's inputs alone moves the
@@ -81,12 +81,13 @@ def run_both(P, names, m, T, sigma, seed=0, fp32_head=False, oracle_chunk=2):
 
 
 def check(got, ref, tol=TOL):
+    """Per-member losses within tol; fitness (difference of two members' losses) within 2 tol."""
     assert torch.isfinite(got).all()
     err = (got - ref).abs().max().item()
     fit_err = ((got[1::2] - got[0::2]) - (ref[1::2] - ref[0::2])).abs().max().item()
     print(f'max |loss - oracle| = {err:.3e}, fitness err {fit_err:.3e}, loss {ref.mean().item():.4f}')
     assert err <= tol, f'max |loss - oracle| = {err:.3e}; got {got.tolist()} ref {ref.tolist()}'
-    assert fit_err <= tol, f'max fitness error {fit_err:.3e}'
+    assert fit_err <= 2 * tol, f'max fitness error {fit_err:.3e}'
     return err, fit_err
 
 
