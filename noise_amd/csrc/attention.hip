@@ -6,15 +6,18 @@
 // reference; here any strides with a contiguous head dim (and, for V, optionally the transposed
 // [.., dim, token] layout the population path writes).
 //
-// Work decomposition: one 256-thread workgroup per (batch*head, 256-query tile); each of its 4 waves owns
-// 64 queries. Per 64-key tile a wave computes S^T = K Q^T (2x2 blocks of v_mfma_f32_32x32x16_bf16,
-// 4 k-steps over D = 64), so a lane holds 32 scores of one query and the row max / sum need only one
-// exchange with lane ^ 32. P = exp2(S*scale*log2e - m) is fed, in registers, as the B operand of
-// O^T = V^T P^T, with the key index permuted identically in V^T (read from LDS) so no LDS round trip
-// is needed. K and V^T tiles are double buffered in LDS (rows padded to 144 B: conflict-free 16 B reads).
-// Key tiles outside every query's band are skipped; masking is applied only on band-edge tiles.
-// All query tiles of one head run on one XCD (workgroups are dispatched round-robin over the 8 XCDs),
-// heaviest tile first, so that head's K/V stay in that XCD's L2.
+// Two kernels share one decomposition: a workgroup per (batch*head, 256-query tile), S^T = K Q^T per
+// 64-key tile with v_mfma_f32_32x32x16_bf16 (4 k-steps over D = 64), so a lane holds the scores of one
+// query and row reductions need one exchange with lane ^ 32; P is fed from registers as the B operand of
+// O^T = V^T P^T with the key index permuted identically on both sides, so P never touches LDS.
+//  - attention_fwd_kernel (any layout and length): 4 waves of 64 queries, K / V tiles register-staged
+//    into double-buffered LDS (rows padded to 144 B), running-max softmax.
+//  - attention_vt_kernel (transposed V, length a multiple of 256; the population path): 8 waves of 32
+//    queries (four waves per SIMD), K / V^T copied global -> LDS into a three-stage swizzled ring, and
+//    an optional fixed-shift softmax for RMS-normed q, k (described at the kernel).
+// Key tiles outside a wave's band are skipped; masking runs only on band-edge tiles. All query tiles of
+// one head run on one XCD (workgroups are dispatched round-robin over the 8 XCDs), heaviest tile first,
+// so that head's K/V stay in that XCD's L2.
 #include "common.hpp"
 #include "mfma.hpp"
 
@@ -276,11 +279,16 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
 // ------------------------------------------------------------------------------------------------
 constexpr int kStage = 2 * 64 * 128;  // K [64 keys][64 d] then V^T [64 d][64 keys], 128 B rows
 constexpr int kNS = 3;
+constexpr int kVtQB = 1;  // 32-query waves: ~128 VGPRs, four waves per SIMD
 
 __device__ __forceinline__ int key_sigma(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-template <bool BOUNDED>
-__global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
+// QB 32-query blocks per wave: NW = 8 / QB waves cover the workgroup's 256 queries (QB = 1: 8 waves of ~128
+// VGPRs, four waves per SIMD with two workgroups per CU; QB = 2: 4 waves of ~250 VGPRs).
+template <bool BOUNDED, int QB>
+__global__ __launch_bounds__(512 / QB) __attribute__((amdgpu_waves_per_eu(4 / QB, 4 / QB))) void attention_vt_kernel(AttnArgs a) {
+    constexpr int NW = 8 / QB, QW = 32 * QB, CPW = 16 / NW;  // waves, queries per wave, copies per wave
+    static_assert(NW * QW == kBQ && NW % 2 == 0, "whole tile; copy parity follows the wave parity");
     __shared__ __attribute__((aligned(16))) char lds[kNS * kStage];
 
     int wg = blockIdx.x;
@@ -301,15 +309,15 @@ __global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, hf = lane >> 5;
     const int T = a.seq, W = a.window;
-    const int q0w = qt * kBQ + wave * kQW;
+    const int q0w = qt * kBQ + wave * QW;
 
-    bf16x8 qf[2][4];
+    bf16x8 qf[QB][4];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int s = 0; s < 4; ++s) qf[qb][s] = load_bf16x8(Qb + (int64_t)(q0w + 32 * qb + j) * a.qs_t + 16 * s + 8 * hf);
 
-    // copies: per stage 16 of 1 KB (8 rows); wave w issues copies c = 4 i + w, rows 8 (c % 8) .. of K (c < 8)
+    // copies: per stage 16 of 1 KB (8 rows); wave w issues copies c = NW i + w, rows 8 (c % 8) .. of K (c < 8)
     // or V^T. Row R's slot P holds chunk P ^ ((R >> 1) & 7); for this lane R = 8 c' + lane / 8, so the chunk
     // it fetches is (lane % 8) ^ (4 (c' & 1) + lane / 16), the same for all of a wave's copies (c' & 1 = w & 1).
     const int chunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
@@ -317,8 +325,8 @@ __global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
     const unsigned voff = (unsigned)((lane >> 3) * a.vs_x * 2 + chunk * 16);
     auto issue = [&](int k0, char *st) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int c = 4 * i + wave;
+        for (int i = 0; i < CPW; ++i) {
+            const int c = NW * i + wave;
             if (c < 8)
                 lds_dma16(Kb + (int64_t)(k0 + 8 * c) * a.ks_t, koff, st + c * 1024);
             else
@@ -334,19 +342,22 @@ __global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
         vfo[s] = 64 * 128 + j * 128 + (((2 * s + hf) ^ ((j >> 1) & 7)) << 4);
     }
 
-    float m[2] = {-1e30f, -1e30f}, l[2] = {0.f, 0.f};
-    f32x16 o[2][2];
+    float m[QB], l[QB];
+    f32x16 o[2][QB];
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+    for (int qb = 0; qb < QB; ++qb) {
+        m[qb] = -1e30f;
+        l[qb] = 0.f;
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) o[db][qb] = f32x16{};
+        for (int db = 0; db < 2; ++db) o[db][qb] = f32x16{};
+    }
 
     const int wg_q_lo = qt * kBQ;
     const int wg_q_hi = wg_q_lo + kBQ - 1;
     const int kv_first = max(0, wg_q_lo - W) / kBKV;
     const int kv_last = wg_q_hi / kBKV;
     const int nt = kv_last - kv_first + 1;
-    const int wq_lo = q0w, wq_hi = q0w + kQW - 1;
+    const int wq_lo = q0w, wq_hi = q0w + QW - 1;
     const float c2 = a.scale_log2, shift = a.shift;
 
     issue(kv_first * kBKV, lds);
@@ -354,7 +365,7 @@ __global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
 
 #pragma unroll 1
     for (int it = 0; it < nt; ++it) {
-        vm_wait_groups<4, 1>(it + 1 < nt ? 1 : 0);  // tile it landed; tile it + 1 may be in flight
+        vm_wait_groups<CPW, 1>(it + 1 < nt ? 1 : 0);  // tile it landed; tile it + 1 may be in flight
         __syncthreads();                              // ... for every wave; tile it - 1 fully read
         if (it + 2 < nt) issue((kv_first + it + 2) * kBKV, lds + ((it + 2) % kNS) * kStage);
         const char *st = lds + (it % kNS) * kStage;
@@ -363,33 +374,35 @@ __global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
         if (!active) continue;
         const bool edge = (k0 + kBKV - 1 > wq_lo) || (k0 < wq_hi - W);
 
-        f32x16 sc[2][2];
+        f32x16 sc[2][QB];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int qb = 0; qb < 2; ++qb) sc[kb][qb] = f32x16{};
+            for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = f32x16{};
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 const bf16x8 ka = *reinterpret_cast<const bf16x8 *>(st + kfo[s] + kb * 32 * 128);
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb) sc[kb][qb] = mfma32x32x16(ka, qf[qb][s], sc[kb][qb]);
+                for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = mfma32x32x16(ka, qf[qb][s], sc[kb][qb]);
             }
         }
 
-        bf16x8 pf[2][4];
+        bf16x8 pf[QB][4];
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb) {
+        for (int qb = 0; qb < QB; ++qb) {
             const int q = q0w + 32 * qb + j;
             if (edge) {
+                // key of register r in block kb: k0 + 32 kb + 16 (r / 8) + 8 hf + r % 8; visible iff
+                // 0 <= q - key <= W, one unsigned compare
+                const int d0 = q - k0 - 8 * hf;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        const int kv = k0 + 32 * kb + 16 * (r >> 3) + 8 * hf + (r & 7);
-                        const bool vis = kv <= q && q - kv <= W;
-                        sc[kb][qb][r] = vis ? sc[kb][qb][r] : -__builtin_inff();
+                        const unsigned dq = (unsigned)(d0 - (32 * kb + 16 * (r >> 3) + (r & 7)));
+                        sc[kb][qb][r] = dq <= (unsigned)W ? sc[kb][qb][r] : -__builtin_inff();
                     }
             }
             float mb;
@@ -434,13 +447,13 @@ __global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
             for (int db = 0; db < 2; ++db) {
                 const bf16x8 va = *reinterpret_cast<const bf16x8 *>(st + vfo[s] + db * 32 * 128);
 #pragma unroll
-                for (int qb = 0; qb < 2; ++qb) o[db][qb] = mfma32x32x16(va, pf[qb][s], o[db][qb]);
+                for (int qb = 0; qb < QB; ++qb) o[db][qb] = mfma32x32x16(va, pf[qb][s], o[db][qb]);
             }
         }
     }
 
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
+    for (int qb = 0; qb < QB; ++qb) {
         const int q = q0w + 32 * qb + j;
         const float lt = l[qb] + swap_halves(l[qb]);
         const float inv = 1.0f / lt;  // the diagonal key is always visible: lt > 0
@@ -467,6 +480,7 @@ __global__ __launch_bounds__(256, 2) void attention_vt_kernel(AttnArgs a) {
         }
     }
 }
+
 
 }  // namespace
 }  // namespace noise
@@ -521,10 +535,11 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     a.shift = kD * fabsf(scale) * kLog2e * 1.0079f;
     dim3 grid((unsigned)(bh * qtiles));
     if (v_transposed && seq % kBQ == 0) {
+        constexpr int QB = kVtQB;
         if (flags & NOISE_ATTN_QK_NORMED)
-            hipLaunchKernelGGL(attention_vt_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((attention_vt_kernel<true, QB>), grid, dim3(512 / QB), 0, (hipStream_t)stream, a);
         else
-            hipLaunchKernelGGL(attention_vt_kernel<false>, grid, dim3(256), 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((attention_vt_kernel<false, QB>), grid, dim3(512 / QB), 0, (hipStream_t)stream, a);
     } else if (v_transposed)
         hipLaunchKernelGGL(attention_fwd_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
     else

@@ -71,9 +71,15 @@ __device__ __forceinline__ void vm_wait() {
 // wait until at most r groups of G loads remain in flight (0 <= r <= RMAX, r known at run time only)
 template <int G, int RMAX>
 __device__ __forceinline__ void vm_wait_groups(int r) {
-    static_assert(RMAX <= 3, "extend for deeper pipelines");
+    static_assert(RMAX <= 5 && G * RMAX < 64, "vmcnt is 6 bits");
+    if constexpr (RMAX >= 5) {
+        if (r >= 5) { vm_wait<5 * G>(); return; }
+    }
+    if constexpr (RMAX >= 4) {
+        if (r == 4) { vm_wait<4 * G>(); return; }
+    }
     if constexpr (RMAX >= 3) {
-        if (r >= 3) { vm_wait<3 * G>(); return; }
+        if (r == 3) { vm_wait<3 * G>(); return; }
     }
     if constexpr (RMAX >= 2) {
         if (r == 2) { vm_wait<2 * G>(); return; }
