@@ -65,6 +65,18 @@ int noise_randint(int64_t *out, int64_t n, uint64_t seed, uint64_t offset, int64
 int noise_gather_slices(float *out, int64_t nrows, int64_t width, const int64_t *offsets, const int64_t *rows,
                         int64_t numel, uint64_t seed, uint64_t offset, int64_t threads, noise_stream_t stream);
 
+/* Orthogonal draws of DUST.orthogonal_noise (run.py:223-238; hadamard run.py:143-152): out[i][f][j] for
+ * draws i < n, frame positions f < bt (the reference's b*t tokens) and coordinates j < d (a power of two):
+ *   index = index0 + i (the reference's rank*draws + chunk*n + i), row = (offset[f] + index) mod d,
+ *   out = H_d[row][j] * (2*pattern[index / d][j] - 1) * (2*sign[i*bt + f] - 1)
+ * with H_d the Sylvester Hadamard matrix (entry (-1)^popcount(row & j)), pattern [cycles][d] and offset
+ * [bt] the raw torch.randint(0, 2) / randint(0, d) outputs of the shared generator, sign [n][bt] the raw
+ * randint(0, 2) of the rank generator (int64 as torch returns them; noise_randint produces them bit for
+ * bit). out is fp32, or bf16 when out_bf16 (+-1 is exact in both). index0 + n must be <= cycles*d. */
+int noise_orthogonal_draws(void *out, int out_bf16, int64_t n, int64_t bt, int64_t d, int64_t index0,
+                           const int64_t *offset, const int64_t *pattern, int64_t cycles, const int64_t *sign,
+                           noise_stream_t stream);
+
 /* ------------------------------------------------------------------------------------------------
  * Attention
  * ---------------------------------------------------------------------------------------------- */

@@ -21,6 +21,7 @@ SIGNATURES = {
     'noise_normal_fill': [_p, _i64, _i64, _u64, _u64, _i64, _f32, _f32, _p],
     'noise_randint': [_p, _i64, _u64, _u64, _i64, _u64, _i64, _p],
     'noise_gather_slices': [_p, _i64, _i64, _p, _p, _i64, _u64, _u64, _i64, _p],
+    'noise_orthogonal_draws': [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p],
     'noise_attention_fwd': [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _p, _p],
     'noise_pop_embed': [_p, _i32, _p, _p, _p, _f32, _f32, _p, _p, _i64, _p, _p, _p, _p],

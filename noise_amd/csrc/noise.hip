@@ -4,7 +4,7 @@
 //   Eggroll.__init__  buffer = torch.randn(2**28, generator=cuda seed)           eggroll.py:114
 //   Eggroll.offsets   torch.randint(0, NOISE - sum(p.shape), (P,), generator=g)  eggroll.py:117-120
 //   Eggroll.noise     buffer[offsets[name][directions, None] + arange(width)]    eggroll.py:122-128
-//   DUST.noise / signs / orthogonal_noise offsets                                run.py:215-233
+//   DUST.noise / signs / orthogonal_noise (Hadamard rows, patterns, signs)      run.py:143-152, 215-238
 // The draw layout is torch's grid-stride distribution kernel (torch: ATen/native/hip/
 // DistributionTemplates.h:52-89) and rocRAND's Philox4x32-10 + Box-Muller (rocrand_philox4x32_10.h,
 // rocrand_normal.h:53-68); philox.hpp states the closed form.
@@ -74,6 +74,30 @@ __global__ __launch_bounds__(kBlock) void gather_slices_kernel(float *__restrict
     int64_t L = offsets[src] + j;
     float v = (L >= 0 && L < numel) ? draw_normal(d, (uint64_t)L, 0.0f, 1.0f) : __builtin_nanf("");
     out[r * width + j] = v;
+}
+
+// Orthogonal draws (run.py:223-238): out[(i * bt + f) * d + j] = H[row][j] * pattern * sign with
+// H[r][j] = (-1)^popcount(r & j), the Sylvester Hadamard matrix of run.py:143-152 (its recursion
+// [[H, H], [H, -H]] flips the sign exactly where both indices have the new top bit set).
+__global__ __launch_bounds__(kBlock) void orthogonal_kernel(void *__restrict__ out, int out_bf16, int64_t n,
+                                                            int64_t bt, int64_t d, int64_t index0,
+                                                            const int64_t *__restrict__ offset,
+                                                            const int64_t *__restrict__ pattern,
+                                                            const int64_t *__restrict__ sign) {
+    const int64_t total = n * bt * d;
+    for (int64_t e = (int64_t)blockIdx.x * kBlock + threadIdx.x; e < total; e += (int64_t)gridDim.x * kBlock) {
+        const int64_t j = e % d, f = (e / d) % bt, i = e / (d * bt);
+        const int64_t index = index0 + i;
+        const int64_t row = (offset[f] + index) & (d - 1);  // d a power of two
+        int neg = __builtin_popcountll((uint64_t)(row & j)) & 1;
+        neg ^= (int)((pattern[(index / d) * d + j] & 1) ^ 1);  // randint(0, 2) * 2 - 1
+        neg ^= (int)((sign[i * bt + f] & 1) ^ 1);
+        const float v = neg ? -1.0f : 1.0f;
+        if (out_bf16)
+            static_cast<__bf16 *>(out)[e] = (__bf16)v;
+        else
+            static_cast<float *>(out)[e] = v;
+    }
 }
 
 int grid_for(int64_t work) {
@@ -164,4 +188,25 @@ extern "C" int noise_gather_slices(float *out, int64_t nrows, int64_t width, con
     hipLaunchKernelGGL(gather_slices_kernel, grid, dim3(kBlock), 0, (hipStream_t)stream, out, width, offsets, rows,
                        numel, d);
     return launch_status("noise_gather_slices");
+}
+
+extern "C" int noise_orthogonal_draws(void *out, int out_bf16, int64_t n, int64_t bt, int64_t d, int64_t index0,
+                                      const int64_t *offset, const int64_t *pattern, int64_t cycles,
+                                      const int64_t *sign, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(n >= 0 && bt >= 0 && index0 >= 0, "noise_orthogonal_draws: n, bt and index0 must be >= 0");
+    NOISE_CHECK_ARG(d >= 1 && (d & (d - 1)) == 0,
+                    "noise_orthogonal_draws: orthogonal draws need a power-of-two width, not %lld", (long long)d);
+    NOISE_CHECK_ARG(cycles >= 1 && index0 + n <= cycles * d,
+                    "noise_orthogonal_draws: draws %lld..%lld need %lld cycles of patterns, got %lld",
+                    (long long)index0, (long long)(index0 + n), (long long)((index0 + n + d - 1) / d),
+                    (long long)cycles);
+    NOISE_CHECK_ARG(n * bt * d < (1ll << 40), "noise_orthogonal_draws: output too large");
+    if (n == 0 || bt == 0) return NOISE_OK;
+    NOISE_CHECK_ARG(out && offset && pattern && sign, "noise_orthogonal_draws: NULL pointer");
+    NOISE_CHECK_ARG(aligned(out, out_bf16 ? 2 : 4) && aligned(offset, 8) && aligned(pattern, 8) && aligned(sign, 8),
+                    "noise_orthogonal_draws: misaligned pointer");
+    hipLaunchKernelGGL(orthogonal_kernel, dim3(grid_for(n * bt * d)), dim3(kBlock), 0, (hipStream_t)stream, out,
+                       out_bf16, n, bt, d, index0, offset, pattern, sign);
+    return launch_status("noise_orthogonal_draws");
 }

@@ -20,7 +20,7 @@ import torch
 from . import _lib
 from ._lib import ATTN_QK_NORMED, ATTN_V_TRANSPOSED
 from .model import rotary_tables, window_sizes, has_ve, N_EMBD, N_HEAD, HEAD_DIM, VOCAB
-from .noise import DeviceGenerator
+from .noise import DeviceGenerator, OrthogonalDraws
 
 BF16 = torch.bfloat16
 F32 = torch.float32
@@ -420,3 +420,47 @@ class Eggroll:
 
 
 SIGMA = 0.002   # eggroll.py:31
+
+
+BLOCK_MATRIX_SUFFIXES = ('attn.c_q.weight', 'attn.c_k.weight', 'attn.c_v.weight', 'attn.c_proj.weight',
+                         'mlp.c_fc.weight', 'mlp.c_proj.weight')
+
+
+def block_matrix_shapes(params):
+    """name -> (out, in) of the 48 block matrices (run.py:647's perturbed set), in named_parameters order."""
+    return {n: tuple(p.shape) for n, p in params.items()
+            if n.startswith('transformer.h.') and n.endswith(BLOCK_MATRIX_SUFFIXES)}
+
+
+def orthogonal_directions(shapes, pairs, seed=SEED, rank=0, world=1, device=None, dtype=torch.float32):
+    """Weight-space orthogonal perturbation directions: name -> (a [pairs, out], b [pairs, in]) of +-1.
+
+    Each matrix's rank-1 factors are two sites of DUST.orthogonal_noise (run.py:223-238) with a one-token
+    frame (b = t = 1): a at site (name, 'a') of width out, then b at site (name, 'b') of width in, matrices
+    visited in `shapes` order, all of this rank's `pairs` draws in one call per site (chunk 0), so
+    direction i is draw rank * pairs + i. Within a cycle of d draws the directions are exactly orthogonal
+    (distinct Hadamard rows); E[a a^T] = I as for Gaussian draws, so sigma keeps its meaning."""
+    od = OrthogonalDraws(seed, rank, world, device)
+    out = {}
+    for name, (o, i) in shapes.items():
+        a = od((name, 'a'), pairs, 0, pairs, 1, 1, o, dtype=dtype).view(pairs, o)
+        b = od((name, 'b'), pairs, 0, pairs, 1, 1, i, dtype=dtype).view(pairs, i)
+        out[name] = (a, b)
+    return out
+
+
+def orthogonal_population(W, noise, x, y, sigma=SIGMA, chunk=1024, directions=None):
+    """Losses of the antithetic members of orthogonal directions `noise` (orthogonal_directions): member
+    2i is +sigma and 2i+1 is -sigma along direction i (eggroll.py:138-142's pairing), all scored on one
+    sequence x -> y, evaluated `chunk` members at a time. directions: optional subset (int tensor) of the
+    directions to evaluate; the result then holds their 2 * len(directions) members in that order."""
+    dev = x.device
+    dirs = torch.arange(next(iter(noise.values()))[0].shape[0], device=dev) if directions is None else \
+        directions.to(dev)
+    losses = []
+    for start in range(0, len(dirs), chunk // 2):
+        d = dirs[start:start + chunk // 2]
+        sub = {k: (a[d], b[d]) for k, (a, b) in noise.items()}
+        sign = torch.tensor([sigma, -sigma], device=dev).repeat(len(d))
+        losses.append(population_forward(W, sub, sign, x, y, dir_div=2))
+    return torch.cat(losses)
