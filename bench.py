@@ -8,6 +8,10 @@ Workload (the reference's EGGROLL population evaluation, train/val/eggroll.py:13
             matrices, sliced from the seed-0 noise buffer at the step-0 offsets (eggroll.py:114-128)
 A step = offsets draw + noise regeneration + weight prep + the fused population forward -> 1024 losses.
 The CPU baseline is the fp32 oracle restatement of the same forward on a bounded member sample.
+
+--workload orthogonal-fp32-head: the large-population variant, 2048 members = 1024 orthogonal antithetic
+pairs (Hadamard draws of run.py:223-238 mapped to weight space, noise_amd.eggroll.orthogonal_directions)
+with the fp32 head as split-bf16x3; a step = orthogonal draws + the forward in two 1024-member chunks.
 """
 import argparse
 import json
@@ -60,7 +64,7 @@ ROCPROF_NAME = {'noise_pop_qkv': 'qkv_kernel', 'noise_pop_fc': 'fc_kernel', 'noi
 def profiled_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 summary (FETCH_SIZE + WRITE_SIZE, scaled
     by the 1 GiB copy calibration), or None."""
-    name = ROCPROF_NAME.get(kernel) or ('attention_fwd_kernel<true>' if kernel.startswith('noise_attention') else None)
+    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel' if kernel.startswith('noise_attention') else None)
     if not name or not os.path.exists(PROFILE):
         return None
     for line in open(PROFILE):
@@ -102,8 +106,11 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--members', type=int, default=2 * PAIRS)
-    ap.add_argument('--cpu-members', type=int, default=4, help='members of the CPU-baseline sample (0: skip)')
+    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head'), default='population')
+    ap.add_argument('--members', type=int, default=None,
+                    help='population size (default 1024; 2048 for orthogonal-fp32-head)')
+    ap.add_argument('--cpu-members', type=int, default=32,
+                    help='members of the CPU-baseline sample, about 15 s of CPU work (0: skip)')
     ap.add_argument('--profile-steps', type=int, default=1, help='extra timed steps with per-kernel events')
     ap.add_argument('--copy-calibration', action='store_true',
                     help='only copy 1 GiB device to device (scale reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)')
@@ -134,14 +141,21 @@ def main():
     seq = zipf_tokens(TOKENS + 1)
     x, y = seq[:-1].to(dev), seq[1:].to(dev)
     names = block_matrix_names()
-    members = args.members
+    orthogonal = args.workload == 'orthogonal-fp32-head'
+    members = args.members or (4 * PAIRS if orthogonal else 2 * PAIRS)
     pairs = members // 2
+    chunk = min(members, 2 * PAIRS)   # members per population_forward call
     es = eg.Eggroll(model, pairs)
     rope = None
     sign = torch.tensor([SIGMA, -SIGMA], device=dev).repeat(pairs)
     directions = torch.arange(0, members, 2, device=dev) % (2 * pairs) // 2
+    shapes = {n: tuple(P[n].shape) for n in names}
 
     def step():
+        if orthogonal:
+            tables = eg.orthogonal_directions(shapes, pairs, seed=0, device=dev)
+            W = eg.Weights(P, fp32_head=True)
+            return eg.orthogonal_population(W, tables, x, y, sigma=SIGMA, chunk=chunk), tables
         offsets = es.offsets(0)
         tables = {}
         for n in names:
@@ -171,7 +185,7 @@ def main():
     kernels = {}
     for (name, label), (n, ms) in timer.totals().items():
         key = name if label is None else f'{name}[{label}]'
-        flops = kernel_flops_per_launch(name, label, members, TOKENS)
+        flops = kernel_flops_per_launch(name, label, chunk, TOKENS)
         entry = dict(launches=n // args.profile_steps, ms_per_step=round(ms / args.profile_steps, 4))
         if flops is not None:
             tf = flops * n / (ms * 1e-3)
@@ -185,17 +199,26 @@ def main():
         roofline = dict(bound='mfma', kernel=dominant, achieved=round(dk['tflops'], 1), peak=BF16_PEAK / 1e12,
                         unit='TFLOP/s', frac=dk['mfma_frac'], traffic=profiled_traffic(dominant),
                         flops_per_launch=kernel_flops_per_launch(*(dominant.rstrip(']').split('[') + [None])[:2],
-                                                                 members, TOKENS))
+                                                                 chunk, TOKENS))
 
     algo_flops = 68_318_208 * members * TOKENS
+    if orthogonal:
+        metric = 'member-tokens/sec forward at 2048 members (1024 orthogonal pairs), fp32 head, T=2048 on 1 GPU'
+        workload = ('large population, fp32 head: fixed 37.7M GPT (seed-0 init), 2048 members (1024 orthogonal '
+                    'antithetic pairs of Hadamard draws, sigma 0.002, rank-1 on the 48 block matrices) x 2048 '
+                    'Zipf(1.1) tokens, head fp32 as split-bf16x3, fused per-member CE')
+    else:
+        metric = 'member-tokens/sec forward at P=1024,T=2048 on 1 GPU; attn/GEMM % MFMA peak'
+        workload = ('population fitness: fixed 37.7M GPT (seed-0 init), 1024 members (512 antithetic pairs, '
+                    'sigma 0.002, rank-1 noise on the 48 block matrices) x 2048 Zipf(1.1) tokens, fused '
+                    'per-member CE')
     line = dict(
-        metric='member-tokens/sec forward at P=1024,T=2048 on 1 GPU; attn/GEMM % MFMA peak',
+        metric=metric,
         value=round(value, 1), unit='member-tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
         ms_per_step=round(dt * 1e3, 3), higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
         data='synthetic',
-        config=dict(workload='population fitness: fixed 37.7M GPT (seed-0 init), 1024 members (512 antithetic '
-                             'pairs, sigma 0.002, rank-1 noise on the 48 block matrices) x 2048 Zipf(1.1) tokens, '
-                             'fused per-member CE', members=members, tokens=TOKENS, pairs=pairs),
+        config=dict(workload=workload, members=members, tokens=TOKENS, pairs=pairs,
+                    head='fp32 (split-bf16x3)' if orthogonal else 'bf16'),
         roofline=roofline,
         whole_forward=dict(algorithmic_tflops=round(algo_flops / dt / 1e12, 1),
                            mfma_frac=round(algo_flops / dt / BF16_PEAK, 4)),
