@@ -204,7 +204,8 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     // per-wave staging after the K loop: Q, K as [64 tokens][kStg], V^T as [128 features][kStgV]
     constexpr int kWaveStg = 128 * kStgV;
     static_assert(64 * kStg <= kWaveStg, "Q/K staging fits the wave's region");
-    constexpr int kLds = cmax(M::LDS_BYTES, 8 * kWaveStg * 2);
+    constexpr int kMain = cmax(M::LDS_BYTES, 8 * kWaveStg * 2);
+    constexpr int kLds = kMain + 2 * 256 * 4;  // + the tile's a vector and value-embedding b vector
     __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
@@ -214,16 +215,39 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     const int n0 = nt * 256, mat = n0 / 512, nl0 = n0 % 512;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int wn0 = M::wn0(wave), wm0 = M::wm0(wave);
+    const int dir = m / p.pop.dir_div;
+    const Rank1 r1 = p.r1[mat];
+    const int head0 = (nl0 + wn0) / 64;
+    const bool ve_on = mat == 2 && p.ve;
+
+    // epilogue inputs fetched ahead of the K loop: per-feature vectors by direct copy into LDS (the K loop's
+    // waits and barriers cover them), per-token scalars into registers
+    float *vec = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + kMain);
+    const float *a0 = r1.a ? r1.a + dir * r1.a_stride + nl0 : nullptr;
+    const float *vb0 = ve_on && p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride + nl0 : nullptr;
+    if (wave == 0 && a0) lds_dma16(a0, lane * 16, vec);
+    if (wave == 1 && vb0) lds_dma16(vb0, lane * 16, vec + 256);
+    float dt[2] = {0.f, 0.f}, gt[2][2] = {{0.f, 0.f}, {0.f, 0.f}}, vesc[2] = {0.f, 0.f};
+    int64_t tokv[2] = {0, 0};
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+        const int t = t0 + wm0 + 32 * tb + j;
+        const int64_t row = (int64_t)m * T + t;
+        if (a0) dt[tb] = p.dots[row * 3 + mat];
+        if (ve_on) {
+            tokv[tb] = p.idx[t];
+            gt[tb][0] = p.gates[row * 8 + head0];
+            gt[tb][1] = p.gates[row * 8 + head0 + 1];
+            if (p.ve_r1.a) vesc[tb] = p.ve_r1.a[dir * p.ve_r1.a_stride + tokv[tb]];
+        }
+    }
 
     f32x16 acc[4][2];
     M::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds, acc, tid,
            wn0, wm0);
 
-    const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
-    const Rank1 r1 = p.r1[mat];
-    const int head0 = (nl0 + wn0) / 64;
-    const float *arow = r1.a ? r1.a + dir * r1.a_stride + nl0 + wn0 : nullptr;
+    const float *arow = a0 ? vec + wn0 : nullptr;
     __bf16 *outm = p.out[mat];
     __bf16 *stg = lds + wave * kWaveStg;
 
@@ -240,9 +264,8 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
             default: copy_head<1, 1>(acc, v); break;
         }
         const int t = t0 + wm0 + 32 * tb + j;
-        const int64_t row = (int64_t)m * T + t;
         if (arow) {
-            const float corr = sgn * p.dots[row * 3 + mat];
+            const float corr = sgn * (tb ? dt[1] : dt[0]);
 #pragma unroll
             for (int half = 0; half < 2; ++half)
 #pragma unroll
@@ -252,15 +275,15 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
                     for (int e = 0; e < 4; ++e) v[half][4 * g + e] += corr * f4get(a4, e);
                 }
         }
-        if (mat == 2 && p.ve) {
+        if (ve_on) {
             // v += gate[row, head] * (ve[idx[t], head*64 + d] (+ lowrank_embed term))   (eggroll.py:85-89);
             // the gates 2 sigmoid(x[:32] . Wg[head] (+ rank-1)) come precomputed (noise_pop_gate)
-            const int64_t tok = p.idx[t];
-            const float gate = p.gates[row * 8 + head0 + hd];
+            const int64_t tok = tb ? tokv[1] : tokv[0];
+            const float gate = tb ? (hd ? gt[1][1] : gt[1][0]) : (hd ? gt[0][1] : gt[0][0]);
             const float *ver = p.ve + tok * 512 + (head0 + hd) * 64;
             // lowrank_embed of the value table (eggroll.py:61-63): + sign * a_ve[tok] * b_ve[:]
-            const float ves = p.ve_r1.a ? sgn * p.ve_r1.a[dir * p.ve_r1.a_stride + tok] : 0.f;
-            const float *veb = p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride + (head0 + hd) * 64 : nullptr;
+            const float ves = sgn * (tb ? vesc[1] : vesc[0]);
+            const float *veb = vb0 ? vec + 256 + wn0 + hd * 64 : nullptr;
 #pragma unroll
             for (int half = 0; half < 2; ++half)
 #pragma unroll
@@ -526,7 +549,8 @@ struct FcArgs {
 
 __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     using M = Mma<8, 256, 256, 64, 2>;
-    constexpr int kLds = cmax(M::LDS_BYTES, 8 * 64 * kStg * 2);  // K loop, then per-wave act staging
+    constexpr int kMain = cmax(M::LDS_BYTES, 8 * 64 * kStg * 2);  // K loop, then per-wave act staging
+    constexpr int kLds = kMain + 2 * 256 * 4;                      // + the tile's a and next-b vectors
     __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
@@ -536,22 +560,36 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     const int n0 = nt * 256;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int wn0 = M::wn0(wave), wm0 = M::wm0(wave);
+    const int dir = m / p.pop.dir_div;
+
+    // the epilogue's per-feature vectors go to LDS by direct copy ahead of the K loop (whose waits and
+    // barriers then cover them), so the epilogue reads them without a global round trip per use
+    float *vec = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + kMain);
+    const float *a0 = p.r1.a ? p.r1.a + dir * p.r1.a_stride + n0 : nullptr;
+    const float *b0 = p.nb ? p.nb + dir * p.nb_stride + n0 : nullptr;
+    if (wave == 0 && a0) lds_dma16(a0, lane * 16, vec);
+    if (wave == 1 && b0) lds_dma16(b0, lane * 16, vec + 256);
+    // this lane's two tokens' x . b dots, loaded now and used after the K loop
+    float dt[2] = {0.f, 0.f};
+    if (a0) {
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) dt[tb] = p.dots[(int64_t)m * T + t0 + wm0 + 32 * tb + j];
+    }
 
     f32x16 acc[4][2];
     M::run(p.w + (int64_t)n0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds, acc, tid, wn0,
            wm0);
 
-    const int dir = m / p.pop.dir_div;
     const float sgn = p.pop.sign[m];
     const int nf0 = n0 + wn0;
-    const float *arow = p.r1.a ? p.r1.a + dir * p.r1.a_stride + nf0 : nullptr;
-    const float *brow = p.nb ? p.nb + dir * p.nb_stride + nf0 : nullptr;
+    const float *arow = a0 ? vec + wn0 : nullptr;
+    const float *brow = b0 ? vec + 256 + wn0 : nullptr;
     __bf16 *stg = lds + wave * 64 * kStg;
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
-        const float corr = arow ? sgn * p.dots[row] : 0.f;
+        const float corr = arow ? sgn * dt[tb] : 0.f;
         float pd = 0.f;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
@@ -864,6 +902,10 @@ extern "C" int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const
     NOISE_CHECK_ARG(w && aligned(w, 16) && act && aligned(act, 8), "%s: w/act NULL or misaligned", fn);
     NOISE_CHECK_ARG(!r1 || !r1->a || dots, "%s: perturbation needs dots", fn);
     NOISE_CHECK_ARG(!next || !next->b || partial_dots, "%s: next b needs partial_dots", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || (aligned(r1->a, 16) && r1->a_stride % 4 == 0),
+                    "%s: a rows must be 16 B aligned (stride a multiple of 4)", fn);
+    NOISE_CHECK_ARG(!next || !next->b || (aligned(next->b, 16) && next->b_stride % 4 == 0),
+                    "%s: next b rows must be 16 B aligned (stride a multiple of 4)", fn);
     FcArgs a;
     a.pop = make_pop(pop);
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
