@@ -398,12 +398,14 @@ struct ResidArgs {
 
 template <int KD>
 __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
-    using M = Mma<8, 512, 128, 64, 2>;
+    using M = Mma<8, 512, 128, 32, 3>;
     // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
-    // hi/lo rows of the split3 output), then the per-token statistics [128 tokens][4 feature waves][4].
+    // hi/lo rows of the split3 output), then the per-token statistics [128 tokens][4 feature waves][4];
+    // above both, the a vector and up to three next b vectors (512 floats each), copied before the K loop.
     constexpr int kStgF = 136;
     constexpr int kEpi = 8 * 32 * kStgF * 4 + 128 * 4 * 4 * 4;
-    constexpr int kLds = cmax(M::LDS_BYTES, kEpi);
+    constexpr int kMain = cmax(M::LDS_BYTES, kEpi);
+    constexpr int kLds = kMain + 4 * 512 * 4;
     static_assert(32 * kStgF * 4 >= 64 * kStg * 2, "bf16 split3 staging must fit the wave's region");
     __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
@@ -411,17 +413,36 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * 128;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
     const int wn0 = M::wn0(wave), wm0 = M::wm0(wave), wq = wave % 4;
-
-    f32x16 acc[4][2];
-    M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, wm0);
-
     const int dir = m / p.pop.dir_div;
+
+    // epilogue inputs fetched ahead of the K loop: the per-feature vectors by direct copy into LDS (wave
+    // 2v + h copies half h of vector v; the K loop's waits and barriers cover them), the per-token rank-1
+    // dot sums and the mixing scalars into registers
+    float *vec = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + kMain);
+    {
+        const int v = wave >> 1, h = wave & 1;
+        const float *src = v == 0 ? (p.r1.a ? p.r1.a + dir * p.r1.a_stride : nullptr)
+                                  : (v - 1 < p.nnext ? p.nb[v - 1] + dir * p.nb_stride[v - 1] : nullptr);
+        if (src) lds_dma16(src + 256 * h, lane * 16, vec + 512 * v + 256 * h);
+    }
     const float sgn = p.pop.sign[m];
+    float dsum[2] = {0.f, 0.f};
+    if (p.r1.a) {
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const int64_t row = (int64_t)m * T + t0 + wm0 + 32 * tb + j;
+            for (int i = 0; i < p.dots_count; ++i) dsum[tb] += p.dots[row * p.dots_stride + i];
+        }
+    }
     float rl = p.lam_r, ml = p.lam_x;
     if (p.mix) {
         if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
         if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
     }
+
+    f32x16 acc[4][2];
+    M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, wm0);
+
     float *stgf = reinterpret_cast<float *>(lds) + wave * 32 * kStgF;
     __bf16 *stgb = reinterpret_cast<__bf16 *>(stgf);
     float *red = reinterpret_cast<float *>(lds) + 8 * 32 * kStgF;
@@ -431,15 +452,10 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
         const int tl = wm0 + 32 * tb + j;
         const int t = t0 + tl;
         const int64_t row = (int64_t)m * T + t;
-        float corr = 0.f;
-        if (p.r1.a) {
-            float c = 0.f;
-            for (int i = 0; i < p.dots_count; ++i) c += p.dots[row * p.dots_stride + i];
-            corr = sgn * c;
-        }
+        const float corr = p.r1.a ? sgn * (tb ? dsum[1] : dsum[0]) : 0.f;
         const float *xr = p.xres + m * p.xr_m + (int64_t)t * p.xr_t + wn0;
         const float *x0r = p.mix ? p.x0 + m * p.x0_m + (int64_t)t * p.x0_t + wn0 : nullptr;
-        const float *ar = p.r1.a ? p.r1.a + dir * p.r1.a_stride + wn0 : nullptr;
+        const float *ar = p.r1.a ? vec + wn0 : nullptr;
         float st[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
@@ -459,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
 #pragma unroll
                 for (int k = 0; k < 3; ++k) {
                     if (k < p.nnext) {
-                        float4 b4 = ld4(p.nb[k] + dir * p.nb_stride[k] + wn0 + f0);
+                        float4 b4 = ld4(vec + 512 * (k + 1) + wn0 + f0);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) st[1 + k] += acc[fb][tb][4 * g + e] * f4get(b4, e);
                     }
@@ -866,7 +882,8 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     NOISE_CHECK_ARG(!mix || (x0.ptr && aligned(x0.ptr, 16) && x0.sm % 4 == 0 && x0.st % 4 == 0), "%s: mix needs x0", fn);
     NOISE_CHECK_ARG(hout && aligned(hout, 8), "%s: hout NULL or misaligned", fn);
     NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || (next && next_dots)), "%s: bad next-dot request", fn);
-    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && dots_count >= 1 && aligned(r1->a, 16)), "%s: perturbation needs dots", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && dots_count >= 1 && aligned(r1->a, 16) && r1->a_stride % 4 == 0),
+                    "%s: perturbation needs dots and 16 B aligned a rows", fn);
     ResidArgs a;
     a.pop = make_pop(pop);
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
@@ -882,7 +899,9 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     for (int k = 0; k < 3; ++k) {
         a.nb[k] = (k < nnext) ? next[k].b : nullptr;
         a.nb_stride[k] = (k < nnext) ? next[k].b_stride : 0;
-        if (k < nnext) NOISE_CHECK_ARG(next[k].b && aligned(next[k].b, 16), "%s: next b %d NULL or misaligned", fn, k);
+        if (k < nnext)
+            NOISE_CHECK_ARG(next[k].b && aligned(next[k].b, 16) && next[k].b_stride % 4 == 0,
+                            "%s: next b %d NULL or misaligned", fn, k);
     }
     dim3 grid((unsigned)(pop->members * (pop->tokens / 128)));
     if (K == 512)
