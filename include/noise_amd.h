@@ -162,11 +162,11 @@ int noise_pop_gate(const noise_population_t *pop, noise_view_t x, const float *g
 /* Q, K, V of one block for every member (eggroll.py:81-90): x (= norm of the block input, bf16) times
  * c_q, c_k, c_v (w[0..2], bf16 [512][512]) + sign * dots[row*3 + i] * a_i; on V, + gates[row*8 + h] *
  * (ve[idx[t], :] + lowrank_embed noise of the value table, ve_noise a [dirs][V], b [dirs][512], or NULL)
- * when ve (fp32 [V][512]) is not NULL; rotary (rope_cos/rope_sin fp32 [tokens][32] holding
- * model.py:177-183's bf16 tables) then per-head RMSNorm on Q and K. Outputs bf16: Q, K
+ * when ve (fp32 [V][512]) is not NULL; rotary (rope_cos/rope_sin: model.py:177-183's bf16 tables,
+ * [tokens][32] bf16, 16 B aligned) then per-head RMSNorm on Q and K. Outputs bf16: Q, K
  * [members][8][tokens][64]; V transposed [members][8][64][tokens]. */
 int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3], const noise_rank1_t r1[3],
-                  const float *dots, const float *rope_cos, const float *rope_sin, const float *ve,
+                  const float *dots, const void *rope_cos, const void *rope_sin, const float *ve,
                   const int64_t *idx, const float *gates, const noise_rank1_t *ve_noise, void *const out[3],
                   noise_stream_t stream);
 

@@ -191,7 +191,7 @@ struct QkvArgs {
     const __bf16 *w[3];
     Rank1 r1[3];
     const float *dots;        // [rows][3]: x . b_q, x . b_k, x . b_v
-    const float *cos_t, *sin_t;  // [T][32]
+    const __bf16 *cos_t, *sin_t;  // [T][32] bf16 (model.py:177-183's tables)
     const float *ve;          // [V][512] fp32 or NULL
     const int64_t *idx;       // [T]
     const float *gates;       // [rows][8] value-embedding gates (noise_pop_gate)
@@ -199,13 +199,20 @@ struct QkvArgs {
     __bf16 *out[3];           // q, k: [m][8][T][64]; v transposed: [m][8][64][T]
 };
 
+// rotary rows of a 256-token tile in LDS: [token][32] bf16, 64 B rows whose four 16 B chunks are
+// XOR-swizzled by (token / 4) mod 4, so the 8 B reads of 16 consecutive tokens hit distinct banks
+__device__ __forceinline__ int rope_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
+
 __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
-    using M = Mma<8, 256, 256, 64, 2>;
-    // per-wave staging after the K loop: Q, K as [64 tokens][kStg], V^T as [128 features][kStgV]
-    constexpr int kWaveStg = 128 * kStgV;
-    static_assert(64 * kStg <= kWaveStg, "Q/K staging fits the wave's region");
+    using M = Mma<8, 256, 256, 32, 3>;
+    // LDS: the K loop's stages, reused after it as per-wave, per-head staging ([64][72] bf16: Q, K as
+    // tokens x dims, V^T as dims x tokens); above them the tile's rotary rows (cos then sin) and the a and
+    // value-embedding b vectors, all copied before the K loop
+    constexpr int kStgH = 72;
+    constexpr int kWaveStg = 64 * kStgH;
     constexpr int kMain = cmax(M::LDS_BYTES, 8 * kWaveStg * 2);
-    constexpr int kLds = kMain + 2 * 256 * 4;  // + the tile's a vector and value-embedding b vector
+    constexpr int kRope = 2 * 256 * 64;
+    constexpr int kLds = kMain + kRope + 2 * 256 * 4;
     __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
@@ -220,9 +227,22 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     const int head0 = (nl0 + wn0) / 64;
     const bool ve_on = mat == 2 && p.ve;
 
-    // epilogue inputs fetched ahead of the K loop: per-feature vectors by direct copy into LDS (the K loop's
-    // waits and barriers cover them), per-token scalars into registers
-    float *vec = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + kMain);
+    // epilogue inputs fetched ahead of the K loop (its waits and barriers cover the copies): rotary rows and
+    // per-feature vectors by direct copy into LDS, per-token scalars into registers
+    char *rope = reinterpret_cast<char *>(lds) + kMain;
+    float *vec = reinterpret_cast<float *>(rope + kRope);
+    if (mat < 2) {
+        // 32 copies of 16 rows (1 KiB): copy i covers rows 16 (i % 16) .. of table i / 16; lane l fetches
+        // row 16 (i % 16) + l / 4, chunk (l % 4) ^ (l / 16) (the row's swizzle, rows 16 apart share it)
+        const int chunk = (lane & 3) ^ (lane >> 4);
+        const unsigned off = (unsigned)((lane >> 2) * 64 + chunk * 16);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 8 * k + wave;
+            const __bf16 *tab = i < 16 ? p.cos_t : p.sin_t;
+            lds_dma16(tab + (int64_t)(t0 + 16 * (i & 15)) * 32, off, rope + i * 1024);
+        }
+    }
     const float *a0 = r1.a ? r1.a + dir * r1.a_stride + nl0 : nullptr;
     const float *vb0 = ve_on && p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride + nl0 : nullptr;
     if (wave == 0 && a0) lds_dma16(a0, lane * 16, vec);
@@ -251,114 +271,113 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     __bf16 *outm = p.out[mat];
     __bf16 *stg = lds + wave * kWaveStg;
 
-    // one (token block, head) pair at a time: its 32 accumulators are copied out (static indices) so the
-    // body below is compiled once and only one head's values are live
+    // one head at a time: its two token blocks (32 accumulators each, copied out with static indices so
+    // the body is compiled once and only one block's values are live), staged, then stored
+#pragma unroll
+    for (int hd = 0; hd < 2; ++hd) {
 #pragma unroll 1
-    for (int it = 0; it < 4; ++it) {
-        const int tb = it >> 1, hd = it & 1;
-        float v[2][16];
-        switch (it) {
-            case 0: copy_head<0, 0>(acc, v); break;
-            case 1: copy_head<0, 1>(acc, v); break;
-            case 2: copy_head<1, 0>(acc, v); break;
-            default: copy_head<1, 1>(acc, v); break;
-        }
-        const int t = t0 + wm0 + 32 * tb + j;
-        if (arow) {
-            const float corr = sgn * (tb ? dt[1] : dt[0]);
+        for (int tb = 0; tb < 2; ++tb) {
+            float v[2][16];
+            if (hd == 0) {
+                if (tb == 0) copy_head<0, 0>(acc, v); else copy_head<1, 0>(acc, v);
+            } else {
+                if (tb == 0) copy_head<0, 1>(acc, v); else copy_head<1, 1>(acc, v);
+            }
+            const int tl = wm0 + 32 * tb + j;  // token within the tile
+            if (arow) {
+                const float corr = sgn * (tb ? dt[1] : dt[0]);
 #pragma unroll
-            for (int half = 0; half < 2; ++half)
+                for (int half = 0; half < 2; ++half)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        float4 a4 = ld4(arow + 64 * hd + 32 * half + 8 * g + 4 * hf);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) v[half][4 * g + e] += corr * f4get(a4, e);
+                    }
+            }
+            if (ve_on) {
+                // v += gate[row, head] * (ve[idx[t], head*64 + d] (+ lowrank_embed term))   (eggroll.py:85-89);
+                // the gates 2 sigmoid(x[:32] . Wg[head] (+ rank-1)) come precomputed (noise_pop_gate)
+                const int64_t tok = tb ? tokv[1] : tokv[0];
+                const float gate = tb ? (hd ? gt[1][1] : gt[1][0]) : (hd ? gt[0][1] : gt[0][0]);
+                const float *ver = p.ve + tok * 512 + (head0 + hd) * 64;
+                // lowrank_embed of the value table (eggroll.py:61-63): + sign * a_ve[tok] * b_ve[:]
+                const float ves = sgn * (tb ? vesc[1] : vesc[0]);
+                const float *veb = vb0 ? vec + 256 + wn0 + hd * 64 : nullptr;
+#pragma unroll
+                for (int half = 0; half < 2; ++half)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int d0 = 32 * half + 8 * g + 4 * hf;
+                        float4 e4 = ld4(ver + d0);
+                        if (veb) {
+                            float4 b4 = ld4(veb + d0);
+#pragma unroll
+                            for (int e = 0; e < 4; ++e)
+                                v[half][4 * g + e] += gate * (f4get(e4, e) + ves * f4get(b4, e));
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * f4get(e4, e);
+                        }
+                    }
+            }
+            if (mat < 2) {
+                // rotary (model.py:55-58) then RMSNorm over the head (model.py:46-47)
+                float ss = 0.f;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    float4 a4 = ld4(arow + 64 * hd + 32 * half + 8 * g + 4 * hf);
+                    const int o = rope_off(tl, g) + 8 * hf;
+                    const bf16x4 c4 = *reinterpret_cast<const bf16x4 *>(rope + o);
+                    const bf16x4 s4 = *reinterpret_cast<const bf16x4 *>(rope + 256 * 64 + o);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[half][4 * g + e] += corr * f4get(a4, e);
+                    for (int e = 0; e < 4; ++e) {
+                        const int r = 4 * g + e;
+                        const float c = (float)c4[e], sn = (float)s4[e];
+                        const float x1 = v[0][r], x2 = v[1][r];
+                        const float o1 = x1 * c + x2 * sn;
+                        const float o2 = x1 * -sn + x2 * c;
+                        v[0][r] = o1;
+                        v[1][r] = o2;
+                        ss += o1 * o1 + o2 * o2;
+                    }
                 }
-        }
-        if (ve_on) {
-            // v += gate[row, head] * (ve[idx[t], head*64 + d] (+ lowrank_embed term))   (eggroll.py:85-89);
-            // the gates 2 sigmoid(x[:32] . Wg[head] (+ rank-1)) come precomputed (noise_pop_gate)
-            const int64_t tok = tb ? tokv[1] : tokv[0];
-            const float gate = tb ? (hd ? gt[1][1] : gt[1][0]) : (hd ? gt[0][1] : gt[0][0]);
-            const float *ver = p.ve + tok * 512 + (head0 + hd) * 64;
-            // lowrank_embed of the value table (eggroll.py:61-63): + sign * a_ve[tok] * b_ve[:]
-            const float ves = sgn * (tb ? vesc[1] : vesc[0]);
-            const float *veb = vb0 ? vec + 256 + wn0 + hd * 64 : nullptr;
+                ss += swap_halves(ss);
+                const float rstd = rsqrtf(ss * (1.0f / 64.0f) + kEps);
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    v[0][r] *= rstd;
+                    v[1][r] *= rstd;
+                }
+            }
+            // stage the head: Q, K as [token][dim]; V transposed as [dim][token]
+            const int tw = 32 * tb + j;  // token within the wave
 #pragma unroll
             for (int half = 0; half < 2; ++half)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    const int d0 = 32 * half + 8 * g + 4 * hf;
-                    float4 e4 = ld4(ver + d0);
-                    if (veb) {
-                        float4 b4 = ld4(veb + d0);
+                    const int d = 32 * half + 8 * g + 4 * hf;
+                    if (mat < 2) {
+                        bf16x4 o;
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * (f4get(e4, e) + ves * f4get(b4, e));
+                        for (int e = 0; e < 4; ++e) o[e] = (__bf16)v[half][4 * g + e];
+                        store_bf16x4(stg + tw * kStgH + d, o);
                     } else {
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * f4get(e4, e);
+                        for (int e = 0; e < 4; ++e) stg[(d + e) * kStgH + tw] = (__bf16)v[half][4 * g + e];
                     }
                 }
         }
-        if (mat < 2) {
-            // rotary (model.py:55-58) then RMSNorm over the head (model.py:46-47)
-            const float *cr = p.cos_t + (int64_t)t * 32, *sr = p.sin_t + (int64_t)t * 32;
-            float ss = 0.f;
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float4 c4 = ld4(cr + 8 * g + 4 * hf), s4 = ld4(sr + 8 * g + 4 * hf);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int r = 4 * g + e;
-                    const float c = f4get(c4, e), sn = f4get(s4, e);
-                    const float x1 = v[0][r], x2 = v[1][r];
-                    const float o1 = x1 * c + x2 * sn;
-                    const float o2 = x1 * -sn + x2 * c;
-                    v[0][r] = o1;
-                    v[1][r] = o2;
-                    ss += o1 * o1 + o2 * o2;
-                }
-            }
-            ss += swap_halves(ss);
-            const float rstd = rsqrtf(ss * (1.0f / 64.0f) + kEps);
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                v[0][r] *= rstd;
-                v[1][r] *= rstd;
-            }
-        }
-        // stage: Q, K as [token][feature]; V transposed as [feature][token]
-        const int tl = 32 * tb + j;
-#pragma unroll
-        for (int half = 0; half < 2; ++half)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int f = 64 * hd + 32 * half + 8 * g + 4 * hf;
-                if (mat < 2) {
-                    bf16x4 o;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) o[e] = (__bf16)v[half][4 * g + e];
-                    store_bf16x4(stg + tl * kStg + f, o);
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) stg[(f + e) * kStgV + tl] = (__bf16)v[half][4 * g + e];
-                }
-            }
-    }
-    // whole-line stores: Q, K rows [m][h][t][0:64] (128 B); V^T rows [m][h][d][t0+wm0 .. +64) (128 B)
-#pragma unroll
-    for (int hd = 0; hd < 2; ++hd) {
+        // whole-line stores of the head: Q, K rows [m][h][t][0:64] (128 B); V^T rows [m][h][d][t0+wm0 .. +64)
+        // (a wave's own LDS writes and reads stay in order: no barrier)
         const int64_t hbase = ((int64_t)m * 8 + head0 + hd);
 #pragma unroll 4
         for (int it = 0; it < 8; ++it) {
             const int c = it * 64 + lane, r = c >> 3, ch = c & 7;
-            if (mat < 2) {
-                bf16x8 v = load_bf16x8(stg + r * kStg + 64 * hd + ch * 8);
+            const bf16x8 v = load_bf16x8(stg + r * kStgH + ch * 8);
+            if (mat < 2)
                 store_bf16x8(outm + (hbase * T + t0 + wm0 + r) * 64 + ch * 8, v);
-            } else {
-                bf16x8 v = load_bf16x8(stg + (64 * hd + r) * kStgV + ch * 8);
+            else
                 store_bf16x8(outm + (hbase * 64 + r) * T + t0 + wm0 + ch * 8, v);
-            }
         }
     }
 }
@@ -835,7 +854,7 @@ int check_view(const noise_view_t &v, const char *fn, const char *name) {
 using namespace noise;
 
 extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3],
-                             const noise_rank1_t r1[3], const float *dots, const float *rope_cos, const float *rope_sin,
+                             const noise_rank1_t r1[3], const float *dots, const void *rope_cos, const void *rope_sin,
                              const float *ve, const int64_t *idx, const float *gates, const noise_rank1_t *ve_noise,
                              void *const out[3], noise_stream_t stream) {
     clear_error();
@@ -843,6 +862,7 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
     NOISE_TRY(check_pop(pop, 256, fn));
     NOISE_TRY(check_view(x, fn, "x"));
     NOISE_CHECK_ARG(w && out && rope_cos && rope_sin, "%s: NULL weight/output/rotary pointer", fn);
+    NOISE_CHECK_ARG(aligned(rope_cos, 16) && aligned(rope_sin, 16), "%s: rotary tables must be 16 B aligned", fn);
     for (int i = 0; i < 3; ++i) {
         NOISE_CHECK_ARG(w[i] && out[i] && aligned(w[i], 16) && aligned(out[i], 8), "%s: weight/output %d NULL or misaligned", fn, i);
         NOISE_CHECK_ARG(!r1 || !r1[i].a || (dots && aligned(r1[i].a, 16) && r1[i].a_stride % 4 == 0),
@@ -857,7 +877,8 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
         a.r1[i] = make_r1(r1 ? &r1[i] : nullptr);
         a.out[i] = (__bf16 *)out[i];
     }
-    a.dots = dots; a.cos_t = rope_cos; a.sin_t = rope_sin; a.ve = ve; a.idx = idx; a.gates = gates;
+    a.dots = dots; a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin; a.ve = ve; a.idx = idx;
+    a.gates = gates;
     a.ve_r1 = make_r1(ve ? ve_noise : nullptr);
     NOISE_CHECK_ARG(!a.ve_r1.a || (aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
                     "%s: value-embedding noise b rows must be 16 B aligned", fn);

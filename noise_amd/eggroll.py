@@ -165,7 +165,7 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     W: Weights. noise: name -> (a [dirs, out], b [dirs, in]) fp32 row views for matrices and embeddings,
     or eps [dirs, L] for 'resid_lambdas' / 'x0_lambdas'; absent names are unperturbed. sign: [m] fp32
     (+-sigma). Member m uses noise row m // dir_div. idx, targets: [T] int64 token ids shared by all
-    members."""
+    members. rope: (cos, sin) bf16 [T][32] rotary tables on the device (default: rotary_tables(T))."""
     dev = W.device
     m, T = sign.shape[0], idx.shape[0]
     if T % 256:
@@ -178,7 +178,7 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     popp = ctypes.byref(pop)
     if rope is None:
         cos, sin = rotary_tables(T)
-        rope = (cos.to(dev).contiguous(), sin.to(dev).contiguous())
+        rope = (cos.to(dev).bfloat16().contiguous(), sin.to(dev).bfloat16().contiguous())
     cos_t, sin_t = rope
     L = W.n_layer
     E = N_EMBD
