@@ -415,7 +415,9 @@ struct ResidArgs {
     float *ndots;             // [rows][nnext]
 };
 
-template <int KD>
+// MIX: apply the next block's mixing (x0 read); NNEXT: number of next-matrix dots (0..3). Both fixed at
+// compile time so the epilogue's loads carry no per-group branches and can be issued in batches.
+template <int KD, bool MIX, int NNEXT>
 __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     using M = Mma<8, 512, 128, 32, 3>;
     // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
@@ -441,8 +443,11 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     {
         const int v = wave >> 1, h = wave & 1;
         const float *src = v == 0 ? (p.r1.a ? p.r1.a + dir * p.r1.a_stride : nullptr)
-                                  : (v - 1 < p.nnext ? p.nb[v - 1] + dir * p.nb_stride[v - 1] : nullptr);
-        if (src) lds_dma16(src + 256 * h, lane * 16, vec + 512 * v + 256 * h);
+                                  : (v - 1 < NNEXT ? p.nb[v - 1] + dir * p.nb_stride[v - 1] : nullptr);
+        if (src)
+            lds_dma16(src + 256 * h, lane * 16, vec + 512 * v + 256 * h);
+        else if (v == 0)
+            st4(vec + 256 * h + 4 * lane, float4{0.f, 0.f, 0.f, 0.f});  // no perturbation: a = 0
     }
     const float sgn = p.pop.sign[m];
     float dsum[2] = {0.f, 0.f};
@@ -454,7 +459,7 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
         }
     }
     float rl = p.lam_r, ml = p.lam_x;
-    if (p.mix) {
+    if (MIX) {
         if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
         if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
     }
@@ -470,39 +475,36 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     for (int tb = 0; tb < 2; ++tb) {
         const int tl = wm0 + 32 * tb + j;
         const int t = t0 + tl;
-        const int64_t row = (int64_t)m * T + t;
-        const float corr = p.r1.a ? sgn * (tb ? dsum[1] : dsum[0]) : 0.f;
+        const float corr = sgn * (tb ? dsum[1] : dsum[0]);  // dsum = 0 without perturbation
         const float *xr = p.xres + m * p.xr_m + (int64_t)t * p.xr_t + wn0;
-        const float *x0r = p.mix ? p.x0 + m * p.x0_m + (int64_t)t * p.x0_t + wn0 : nullptr;
-        const float *ar = p.r1.a ? vec + wn0 : nullptr;
-        float st[4] = {0.f, 0.f, 0.f, 0.f};
+        const float *x0r = MIX ? p.x0 + m * p.x0_m + (int64_t)t * p.x0_t + wn0 : nullptr;
+        float ssq = 0.f;
+        // one feature block (4 groups of 4) at a time: its residual (and x0) loads are issued, then used
 #pragma unroll
-        for (int fb = 0; fb < 4; ++fb)
+        for (int fb = 0; fb < 4; ++fb) {
+            float4 xv[4], zv[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int f0 = 32 * fb + 8 * g + 4 * hf;
-                float4 xv = ld4(xr + f0);
-                float4 a4 = ar ? ld4(ar + f0) : float4{0, 0, 0, 0};
-                float4 z4 = x0r ? ld4(x0r + f0) : float4{0, 0, 0, 0};
+                xv[g] = ld4(xr + f0);
+                if constexpr (MIX) zv[g] = ld4(x0r + f0);
+            }
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int f0 = 32 * fb + 8 * g + 4 * hf;
+                const float4 a4 = ld4(vec + wn0 + f0);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float y = f4get(xv, e) + (acc[fb][tb][4 * g + e] + corr * f4get(a4, e));
-                    if (p.mix) y = rl * y + ml * f4get(z4, e);
+                    float y = f4get(xv[g], e) + (acc[fb][tb][4 * g + e] + corr * f4get(a4, e));
+                    if constexpr (MIX) y = rl * y + ml * f4get(zv[g], e);
                     acc[fb][tb][4 * g + e] = y;
-                    st[0] += y * y;
-                }
-#pragma unroll
-                for (int k = 0; k < 3; ++k) {
-                    if (k < p.nnext) {
-                        float4 b4 = ld4(vec + 512 * (k + 1) + wn0 + f0);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) st[1 + k] += acc[fb][tb][4 * g + e] * f4get(b4, e);
-                    }
+                    ssq += y * y;
                 }
                 if (p.xout)
                     st4(stgf + j * kStgF + f0, float4{acc[fb][tb][4 * g], acc[fb][tb][4 * g + 1],
                                                       acc[fb][tb][4 * g + 2], acc[fb][tb][4 * g + 3]});
             }
+        }
         if (p.xout) {
             // whole-line stores: 32 rows x 512 B of this wave's 128 features
             float *xo = p.xout + ((int64_t)m * T + t0 + wm0 + 32 * tb) * 512 + wn0;
@@ -512,11 +514,22 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
                 st4(xo + (int64_t)r * 512 + ch * 4, ld4(stgf + r * kStgF + ch * 4));
             }
         }
+        // per-token partials over this wave's 128 features: sum of squares, then y . b_k of each next matrix
+        ssq += swap_halves(ssq);
+        if (hf == 0) red[(tl * 4 + wq) * 4] = ssq;
+#pragma unroll 1
+        for (int k = 0; k < NNEXT; ++k) {
+            float d = 0.f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) st[k] += swap_halves(st[k]);
-        if (hf == 0) {
+            for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) red[(tl * 4 + wq) * 4 + k] = st[k];
+                for (int g = 0; g < 4; ++g) {
+                    const float4 b4 = ld4(vec + 512 * (k + 1) + wn0 + 32 * fb + 8 * g + 4 * hf);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) d += acc[fb][tb][4 * g + e] * f4get(b4, e);
+                }
+            d += swap_halves(d);
+            if (hf == 0) red[(tl * 4 + wq) * 4 + 1 + k] = d;
         }
     }
     __syncthreads();
@@ -525,11 +538,13 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
         const int tl = wm0 + 32 * tb + j;
         const int t = t0 + tl;
         const int64_t row = (int64_t)m * T + t;
-        float tot[4] = {0.f, 0.f, 0.f, 0.f};
+        float tot[1 + NNEXT];
+#pragma unroll
+        for (int k = 0; k <= NNEXT; ++k) tot[k] = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; ++w)
 #pragma unroll
-            for (int k = 0; k < 4; ++k) tot[k] += red[(tl * 4 + w) * 4 + k];
+            for (int k = 0; k <= NNEXT; ++k) tot[k] += red[(tl * 4 + w) * 4 + k];
         const float rstd = rsqrtf(tot[0] * (1.0f / 512.0f) + kEps);
         // stage bf16 rows: [32][kStg] for hi (and lo after it when split3)
 #pragma unroll
@@ -560,7 +575,8 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
             }
         }
         if (wq == 0 && hf == 0) {
-            for (int k = 0; k < p.nnext; ++k) p.ndots[row * p.nnext + k] = rstd * tot[1 + k];
+#pragma unroll
+            for (int k = 0; k < NNEXT; ++k) p.ndots[row * NNEXT + k] = rstd * tot[1 + k];
         }
     }
 }
@@ -842,6 +858,24 @@ int check_view(const noise_view_t &v, const char *fn, const char *name) {
     return NOISE_OK;
 }
 
+template <int KD, bool MIX>
+void launch_resid_mix(const ResidArgs &a, dim3 grid, hipStream_t s) {
+    switch (a.nnext) {
+        case 0: hipLaunchKernelGGL((resid_kernel<KD, MIX, 0>), grid, dim3(kThreads), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((resid_kernel<KD, MIX, 1>), grid, dim3(kThreads), 0, s, a); break;
+        case 2: hipLaunchKernelGGL((resid_kernel<KD, MIX, 2>), grid, dim3(kThreads), 0, s, a); break;
+        default: hipLaunchKernelGGL((resid_kernel<KD, MIX, 3>), grid, dim3(kThreads), 0, s, a); break;
+    }
+}
+
+template <int KD>
+void launch_resid(const ResidArgs &a, dim3 grid, hipStream_t s) {
+    if (a.mix)
+        launch_resid_mix<KD, true>(a, grid, s);
+    else
+        launch_resid_mix<KD, false>(a, grid, s);
+}
+
 #define NOISE_TRY(x)                 \
     do {                             \
         int _s = (x);                \
@@ -926,9 +960,9 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     }
     dim3 grid((unsigned)(pop->members * (pop->tokens / 128)));
     if (K == 512)
-        hipLaunchKernelGGL(resid_kernel<512>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+        launch_resid<512>(a, grid, (hipStream_t)stream);
     else
-        hipLaunchKernelGGL(resid_kernel<2048>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+        launch_resid<2048>(a, grid, (hipStream_t)stream);
     return launch_status(fn);
 }
 
