@@ -278,18 +278,24 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
 // shift-invariant; fp32 and bf16 keep full relative precision down to 2^-126).
 // ------------------------------------------------------------------------------------------------
 constexpr int kStage = 2 * 64 * 128;  // K [64 keys][64 d] then V^T [64 d][64 keys], 128 B rows
-constexpr int kNS = 3;
-constexpr int kVtQB = 1;  // 32-query waves: ~128 VGPRs, four waves per SIMD
+#ifndef NOISE_VT_QT
+#define NOISE_VT_QT 256
+#endif
+#ifndef NOISE_VT_NS
+#define NOISE_VT_NS 3
+#endif
+constexpr int kVtQT = NOISE_VT_QT;  // queries per workgroup of the transposed-V kernel
+constexpr int kVtNS = NOISE_VT_NS;  // its ring depth
 
 __device__ __forceinline__ int key_sigma(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-// QB 32-query blocks per wave: NW = 8 / QB waves cover the workgroup's 256 queries (QB = 1: 8 waves of ~128
-// VGPRs, four waves per SIMD with two workgroups per CU; QB = 2: 4 waves of ~250 VGPRs).
-template <bool BOUNDED, int QB>
-__global__ __launch_bounds__(512 / QB) __attribute__((amdgpu_waves_per_eu(4 / QB, 4 / QB))) void attention_vt_kernel(AttnArgs a) {
-    constexpr int NW = 8 / QB, QW = 32 * QB, CPW = 16 / NW;  // waves, queries per wave, copies per wave
-    static_assert(NW * QW == kBQ && NW % 2 == 0, "whole tile; copy parity follows the wave parity");
-    __shared__ __attribute__((aligned(16))) char lds[kNS * kStage];
+// QT queries per workgroup in waves of 32 (~128 VGPRs: four waves per SIMD), NS-stage K / V^T ring.
+template <bool BOUNDED, int QT, int NS>
+__global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_vt_kernel(AttnArgs a) {
+    constexpr int QB = 1, NW = QT / 32, QW = 32, CPW = 16 / NW;  // waves, queries per wave, copies per wave
+    static_assert(NW * QW == QT && NW % 2 == 0 && 16 % NW == 0, "whole tile; copy parity follows the wave parity");
+    static_assert(NS >= 2 && NS <= 4, "ring depth");
+    __shared__ __attribute__((aligned(16))) char lds[NS * kStage];
 
     int wg = blockIdx.x;
     int bh, qt;
@@ -309,7 +315,7 @@ __global__ __launch_bounds__(512 / QB) __attribute__((amdgpu_waves_per_eu(4 / QB
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int j = lane & 31, hf = lane >> 5;
     const int T = a.seq, W = a.window;
-    const int q0w = qt * kBQ + wave * QW;
+    const int q0w = qt * QT + wave * QW;
 
     bf16x8 qf[QB][4];
 #pragma unroll
@@ -352,23 +358,26 @@ __global__ __launch_bounds__(512 / QB) __attribute__((amdgpu_waves_per_eu(4 / QB
         for (int db = 0; db < 2; ++db) o[db][qb] = f32x16{};
     }
 
-    const int wg_q_lo = qt * kBQ;
-    const int wg_q_hi = wg_q_lo + kBQ - 1;
+    const int wg_q_lo = qt * QT;
+    const int wg_q_hi = wg_q_lo + QT - 1;
     const int kv_first = max(0, wg_q_lo - W) / kBKV;
     const int kv_last = wg_q_hi / kBKV;
     const int nt = kv_last - kv_first + 1;
     const int wq_lo = q0w, wq_hi = q0w + QW - 1;
     const float c2 = a.scale_log2, shift = a.shift;
 
-    issue(kv_first * kBKV, lds);
-    if (nt > 1) issue((kv_first + 1) * kBKV, lds + kStage);
+    // tiles 0 .. NS-2 in flight; iteration it waits for tile it, then refills the slot of tile it - 1
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t)
+        if (t < nt) issue((kv_first + t) * kBKV, lds + t * kStage);
 
 #pragma unroll 1
     for (int it = 0; it < nt; ++it) {
-        vm_wait_groups<CPW, 1>(it + 1 < nt ? 1 : 0);  // tile it landed; tile it + 1 may be in flight
-        __syncthreads();                              // ... for every wave; tile it - 1 fully read
-        if (it + 2 < nt) issue((kv_first + it + 2) * kBKV, lds + ((it + 2) % kNS) * kStage);
-        const char *st = lds + (it % kNS) * kStage;
+        // tile it landed: at most min(NS - 2, nt - 1 - it) later tiles in flight
+        vm_wait_groups<CPW, NS - 2>(nt - 1 - it < NS - 2 ? nt - 1 - it : NS - 2);
+        __syncthreads();  // ... for every wave; tile it - 1 fully read
+        if (it + NS - 1 < nt) issue((kv_first + it + NS - 1) * kBKV, lds + ((it + NS - 1) % NS) * kStage);
+        const char *st = lds + (it % NS) * kStage;
         const int k0 = (kv_first + it) * kBKV;
         const bool active = k0 <= wq_hi && k0 + kBKV - 1 >= wq_lo - W;
         if (!active) continue;
@@ -518,7 +527,9 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     NOISE_CHECK_ARG(dot_out == nullptr || (dot_vec != nullptr && dot_div >= 1),
                     "noise_attention_fwd: dot_out needs dot_vec and dot_div >= 1");
     int64_t bh = batch * heads;
-    int64_t qtiles = (seq + kBQ - 1) / kBQ;
+    const bool vt_path = v_transposed && seq % kVtQT == 0;
+    const int64_t qtile = vt_path ? kVtQT : kBQ;
+    int64_t qtiles = (seq + qtile - 1) / qtile;
     NOISE_CHECK_ARG(bh * qtiles < (1ll << 31), "noise_attention_fwd: too many workgroups");
     AttnArgs a;
     a.q = (const __bf16 *)q; a.k = (const __bf16 *)k; a.v = (const __bf16 *)v; a.o = (__bf16 *)o;
@@ -534,12 +545,13 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     // rows of RMS <= 1 (rounded to bf16): |q . k| <= D (1 + 2^-8)^2 < 1.0079 D
     a.shift = kD * fabsf(scale) * kLog2e * 1.0079f;
     dim3 grid((unsigned)(bh * qtiles));
-    if (v_transposed && seq % kBQ == 0) {
-        constexpr int QB = kVtQB;
+    if (vt_path) {
         if (flags & NOISE_ATTN_QK_NORMED)
-            hipLaunchKernelGGL((attention_vt_kernel<true, QB>), grid, dim3(512 / QB), 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((attention_vt_kernel<true, kVtQT, kVtNS>), grid, dim3(kVtQT * 2), 0,
+                               (hipStream_t)stream, a);
         else
-            hipLaunchKernelGGL((attention_vt_kernel<false, QB>), grid, dim3(512 / QB), 0, (hipStream_t)stream, a);
+            hipLaunchKernelGGL((attention_vt_kernel<false, kVtQT, kVtNS>), grid, dim3(kVtQT * 2), 0,
+                               (hipStream_t)stream, a);
     } else if (v_transposed)
         hipLaunchKernelGGL(attention_fwd_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
     else

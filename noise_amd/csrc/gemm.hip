@@ -245,8 +245,14 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     }
     const float *a0 = r1.a ? r1.a + dir * r1.a_stride + nl0 : nullptr;
     const float *vb0 = ve_on && p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride + nl0 : nullptr;
-    if (wave == 0 && a0) lds_dma16(a0, lane * 16, vec);
-    if (wave == 1 && vb0) lds_dma16(vb0, lane * 16, vec + 256);
+    // (an absent vector reads as zeros, so the epilogue needs no branches)
+    if (wave < 2) {
+        const float *src = wave == 0 ? a0 : vb0;
+        if (src)
+            lds_dma16(src, lane * 16, vec + 256 * wave);
+        else
+            st4(vec + 256 * wave + 4 * lane, float4{0.f, 0.f, 0.f, 0.f});
+    }
     float dt[2] = {0.f, 0.f}, gt[2][2] = {{0.f, 0.f}, {0.f, 0.f}}, vesc[2] = {0.f, 0.f};
     int64_t tokv[2] = {0, 0};
 #pragma unroll
@@ -267,7 +273,7 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
            wn0, wm0);
 
     const float sgn = p.pop.sign[m];
-    const float *arow = a0 ? vec + wn0 : nullptr;
+    const float *arow = vec + wn0;  // zeros when unperturbed
     __bf16 *outm = p.out[mat];
     __bf16 *stg = lds + wave * kWaveStg;
 
@@ -284,13 +290,13 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
                 if (tb == 0) copy_head<0, 1>(acc, v); else copy_head<1, 1>(acc, v);
             }
             const int tl = wm0 + 32 * tb + j;  // token within the tile
-            if (arow) {
-                const float corr = sgn * (tb ? dt[1] : dt[0]);
+            {
+                const float corr = sgn * (tb ? dt[1] : dt[0]);  // dt = 0 without perturbation
 #pragma unroll
                 for (int half = 0; half < 2; ++half)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
-                        float4 a4 = ld4(arow + 64 * hd + 32 * half + 8 * g + 4 * hf);
+                        const float4 a4 = ld4(arow + 64 * hd + 32 * half + 8 * g + 4 * hf);
 #pragma unroll
                         for (int e = 0; e < 4; ++e) v[half][4 * g + e] += corr * f4get(a4, e);
                     }
@@ -302,24 +308,18 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
                 const float gate = tb ? (hd ? gt[1][1] : gt[1][0]) : (hd ? gt[0][1] : gt[0][0]);
                 const float *ver = p.ve + tok * 512 + (head0 + hd) * 64;
                 // lowrank_embed of the value table (eggroll.py:61-63): + sign * a_ve[tok] * b_ve[:]
-                const float ves = sgn * (tb ? vesc[1] : vesc[0]);
-                const float *veb = vb0 ? vec + 256 + wn0 + hd * 64 : nullptr;
+                const float ves = sgn * (tb ? vesc[1] : vesc[0]);     // 0 without value-table noise
+                const float *veb = vec + 256 + wn0 + hd * 64;           // zeros without value-table noise
+                float4 e4[8];
 #pragma unroll
-                for (int half = 0; half < 2; ++half)
+                for (int q = 0; q < 8; ++q) e4[q] = ld4(ver + 32 * (q >> 2) + 8 * (q & 3) + 4 * hf);
 #pragma unroll
-                    for (int g = 0; g < 4; ++g) {
-                        const int d0 = 32 * half + 8 * g + 4 * hf;
-                        float4 e4 = ld4(ver + d0);
-                        if (veb) {
-                            float4 b4 = ld4(veb + d0);
+                for (int q = 0; q < 8; ++q) {
+                    const int half = q >> 2, g = q & 3;
+                    const float4 b4 = ld4(veb + 32 * half + 8 * g + 4 * hf);
 #pragma unroll
-                            for (int e = 0; e < 4; ++e)
-                                v[half][4 * g + e] += gate * (f4get(e4, e) + ves * f4get(b4, e));
-                        } else {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * f4get(e4, e);
-                        }
-                    }
+                    for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * (f4get(e4[q], e) + ves * f4get(b4, e));
+                }
             }
             if (mat < 2) {
                 // rotary (model.py:55-58) then RMSNorm over the head (model.py:46-47)
@@ -618,8 +618,14 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     float *vec = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + kMain);
     const float *a0 = p.r1.a ? p.r1.a + dir * p.r1.a_stride + n0 : nullptr;
     const float *b0 = p.nb ? p.nb + dir * p.nb_stride + n0 : nullptr;
-    if (wave == 0 && a0) lds_dma16(a0, lane * 16, vec);
-    if (wave == 1 && b0) lds_dma16(b0, lane * 16, vec + 256);
+    // (an absent vector reads as zeros, so the epilogue needs no branches)
+    if (wave < 2) {
+        const float *src = wave == 0 ? a0 : b0;
+        if (src)
+            lds_dma16(src, lane * 16, vec + 256 * wave);
+        else
+            st4(vec + 256 * wave + 4 * lane, float4{0.f, 0.f, 0.f, 0.f});
+    }
     // this lane's two tokens' x . b dots, loaded now and used after the K loop
     float dt[2] = {0.f, 0.f};
     if (a0) {
@@ -633,22 +639,20 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
 
     const float sgn = p.pop.sign[m];
     const int nf0 = n0 + wn0;
-    const float *arow = a0 ? vec + wn0 : nullptr;
-    const float *brow = b0 ? vec + 256 + wn0 : nullptr;
+    const float *arow = vec + wn0, *brow = vec + 256 + wn0;  // zeros when absent
     __bf16 *stg = lds + wave * 64 * kStg;
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
-        const float corr = arow ? sgn * dt[tb] : 0.f;
+        const float corr = sgn * dt[tb];  // dt = 0 without perturbation
         float pd = 0.f;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int f = 32 * fb + 8 * g + 4 * hf;
-                float4 a4 = arow ? ld4(arow + f) : float4{0, 0, 0, 0};
-                float4 b4 = brow ? ld4(brow + f) : float4{0, 0, 0, 0};
+                const float4 a4 = ld4(arow + f), b4 = ld4(brow + f);
                 bf16x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
