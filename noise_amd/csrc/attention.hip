@@ -312,7 +312,7 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     const __bf16 *Kb = a.k + b * a.ks_b + h * a.ks_h;
     const __bf16 *Vb = a.v + b * a.vs_b + h * a.vs_h;
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int j = lane & 31, hf = lane >> 5;
     const int T = a.seq, W = a.window;
     const int q0w = qt * QT + wave * QW;
@@ -329,14 +329,15 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     const int chunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
     const unsigned koff = (unsigned)((lane >> 3) * a.ks_t * 2 + chunk * 16);
     const unsigned voff = (unsigned)((lane >> 3) * a.vs_x * 2 + chunk * 16);
-    auto issue = [&](int k0, char *st) {
+    const unsigned lb = lds_addr(lds);
+    auto issue = [&](int k0, unsigned st) {  // st: LDS byte address of the stage
 #pragma unroll
         for (int i = 0; i < CPW; ++i) {
             const int c = NW * i + wave;
             if (c < 8)
-                lds_dma16(Kb + (int64_t)(k0 + 8 * c) * a.ks_t, koff, st + c * 1024);
+                lds_dma16_at(Kb + (int64_t)(k0 + 8 * c) * a.ks_t, koff, st + c * 1024);
             else
-                lds_dma16(Vb + (int64_t)(8 * (c - 8)) * a.vs_x + k0, voff, st + c * 1024);
+                lds_dma16_at(Vb + (int64_t)(8 * (c - 8)) * a.vs_x + k0, voff, st + c * 1024);
         }
     };
     // fragment byte offsets within a stage for k-step s: K row sigma(j) (+32 kb), V^T row j (+32 db)
@@ -369,14 +370,14 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     // tiles 0 .. NS-2 in flight; iteration it waits for tile it, then refills the slot of tile it - 1
 #pragma unroll
     for (int t = 0; t < NS - 1; ++t)
-        if (t < nt) issue((kv_first + t) * kBKV, lds + t * kStage);
+        if (t < nt) issue((kv_first + t) * kBKV, lb + t * kStage);
 
 #pragma unroll 1
     for (int it = 0; it < nt; ++it) {
         // tile it landed: at most min(NS - 2, nt - 1 - it) later tiles in flight
         vm_wait_groups<CPW, NS - 2>(nt - 1 - it < NS - 2 ? nt - 1 - it : NS - 2);
         __syncthreads();  // ... for every wave; tile it - 1 fully read
-        if (it + NS - 1 < nt) issue((kv_first + it + NS - 1) * kBKV, lds + ((it + NS - 1) % NS) * kStage);
+        if (it + NS - 1 < nt) issue((kv_first + it + NS - 1) * kBKV, lb + ((it + NS - 1) % NS) * kStage);
         const char *st = lds + (it % NS) * kStage;
         const int k0 = (kv_first + it) * kBKV;
         const bool active = k0 <= wq_hi && k0 + kBKV - 1 >= wq_lo - W;

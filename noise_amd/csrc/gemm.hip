@@ -67,7 +67,9 @@ struct Mma {
     __device__ static void run(const __bf16 *W, int64_t ldw, const __bf16 *X, int64_t ldx, int K, void *lds_v,
                                f32x16 (&acc)[4][2], int tid, int wn, int wm) {
         char *lds = static_cast<char *>(lds_v);
-        const int wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+        const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
+        const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets stay scalar
+        const unsigned lbase = lds_addr(lds);
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
@@ -88,13 +90,13 @@ struct Mma {
         for (int s = 0; s < SPK; ++s) lo[s] = j * RB + swz(j, 2 * s + hf) * 16;
         const int nk = K / BK;
         auto issue = [&](int p) {
-            char *st = lds + (p % NS) * STAGE;
+            const unsigned st = lbase + (p % NS) * STAGE + wave * 1024;
 #pragma unroll
             for (int i = 0; i < NI; ++i) {
                 if (i < IW)
-                    lds_dma16(W + (int64_t)(i * STEP) * ldw + p * BK, offw, st + (i * NW + wave) * 1024);
+                    lds_dma16_at(W + (int64_t)(i * STEP) * ldw + p * BK, offw, st + i * NW * 1024);
                 else
-                    lds_dma16(X + (int64_t)((i - IW) * STEP) * ldx + p * BK, offx, st + (i * NW + wave) * 1024);
+                    lds_dma16_at(X + (int64_t)((i - IW) * STEP) * ldx + p * BK, offx, st + i * NW * 1024);
             }
         };
         bf16x8 fa[2][4], fx[2][2];

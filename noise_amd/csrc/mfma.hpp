@@ -45,20 +45,29 @@ __device__ __forceinline__ bf16x8 cat(bf16x4 lo, bf16x4 hi) {
 // wait for every outstanding copy before each LDS read, leaves the pipeline to the explicit vm_wait below.
 // Such loads only add to vmcnt, so the compiler's own waits for its loads stay correct (they can only
 // become stricter). M0 is saved and restored.
-__device__ __forceinline__ void lds_dma16(const void *base, unsigned off, const void *l) {
-    // base and l are wave-uniform by contract; readfirstlane lets the compiler hold them in SGPRs. The
+// LDS byte address of a pointer into a __shared__ array
+__device__ __forceinline__ unsigned lds_addr(const void *l) {
+    return (unsigned)(size_t)((__attribute__((address_space(3))) const void *)l);
+}
+
+// As lds_dma16 below, with the destination given as an LDS byte address (wave-uniform).
+__device__ __forceinline__ void lds_dma16_at(const void *base, unsigned off, unsigned la) {
+    // base and la are wave-uniform by contract; readfirstlane lets the compiler hold them in SGPRs. The
     // builtin returns a signed int: both halves are zero-extended before the 64-bit address is formed.
     const uint64_t b = (uint64_t)base;
     const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
     const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
     const uint64_t ub = ((uint64_t)hi << 32) | (uint64_t)lo;
-    const unsigned la =
-        __builtin_amdgcn_readfirstlane((unsigned)(size_t)((__attribute__((address_space(3))) const void *)l));
+    const unsigned l = (unsigned)__builtin_amdgcn_readfirstlane((int)la);
     unsigned save;
     asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dwordx4 %1, %2\n\ts_mov_b32 m0, %0"
                  : "=&s"(save)
-                 : "v"(off), "s"(ub), "s"(la)
+                 : "v"(off), "s"(ub), "s"(l)
                  : "memory");
+}
+
+__device__ __forceinline__ void lds_dma16(const void *base, unsigned off, const void *l) {
+    lds_dma16_at(base, off, lds_addr(l));
 }
 
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone)
