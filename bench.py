@@ -106,7 +106,10 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head'), default='population')
+    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update'), default='population')
+    ap.add_argument('--pairs', type=int, default=None,
+                    help='update workload: antithetic pairs (default 512; the reference trains with 131072)')
+    ap.add_argument('--update-chunk', type=int, default=8192, help='update workload: directions per GEMM pass')
     ap.add_argument('--members', type=int, default=None,
                     help='population size (default 1024; 2048 for orthogonal-fp32-head)')
     ap.add_argument('--cpu-members', type=int, default=32,
@@ -129,6 +132,8 @@ def main():
               'all_gather of the losses; see DESIGN.md). Run with --gpus 1.', file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == 'update':
+        return bench_update(args)
     import torch
     from noise_amd import eggroll as eg
     from noise_amd.model import make_model, window_sizes
@@ -233,6 +238,46 @@ def main():
     else:
         line['cpu_baseline'] = None
     print(json.dumps(line), flush=True)
+
+
+def bench_update(args):
+    """EGGROLL's update reassembly (eggroll.py:151-165) for the fixed model: fitness weights, then every
+    parameter's -(1/F) sum_d w_d a_d b_d^T with the noise regenerated in-kernel. A step is one update from
+    losses already resident on the GPU."""
+    import torch
+    from noise_amd.eggroll import Eggroll
+    from noise_amd.model import make_model
+    dev = torch.device('cuda', 0)
+    torch.cuda.set_device(dev)
+    model = make_model('cpu', 0).to(dev)
+    pairs = args.pairs or PAIRS
+    es = Eggroll(model, pairs)
+    offsets = es.offsets(0)
+    g = torch.Generator().manual_seed(0)
+    losses = (8.3 + 0.01 * torch.randn(2 * pairs, generator=g)).to(dev)
+    for _ in range(args.warmup):
+        es.update(losses, offsets, chunk=args.update_chunk)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        grads = es.update(losses, offsets, chunk=args.update_chunk)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    big = sum(p.shape[0] * p.shape[1] for p in es.params.values()
+              if p.dim() == 2 and p.shape[0] % 256 == 0 and p.shape[1] % 256 == 0)
+    algo = 2 * pairs * sum(p.numel() for p in es.params.values())
+    executed = 3 * 2 * pairs * big  # split-bf16x3 products of the GEMM path
+    print(json.dumps(dict(
+        metric='EGGROLL update reassembly: gradient TFLOP/s (2 x pairs x parameters) on 1 GPU',
+        value=round(algo / dt / 1e12, 2), unit='TFLOP/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(dt * 1e3, 3), higher_is_better=True, scaling='weak', vs_baseline=None,
+        dtype='fp32 (split-bf16x3 MFMA)', data='synthetic',
+        config=dict(workload=f'update of the fixed 37.7M GPT (60 parameters) from {2 * pairs} member losses, '
+                             f'{pairs} directions regenerated in-kernel, chunk {args.update_chunk}',
+                    pairs=pairs, chunk=args.update_chunk),
+        executed_mfma=dict(tflops=round(executed / dt / 1e12, 1), frac=round(executed / dt / BF16_PEAK, 4)),
+        grad_finite=bool(all(torch.isfinite(t).all().item() for t in grads.values())),
+    )), flush=True)
 
 
 if __name__ == '__main__':

@@ -223,6 +223,39 @@ int noise_lowrank_embed(float *out, const float *w, int64_t vocab, int64_t width
 int noise_rank1_expand(const noise_population_t *pop, const float *base, int64_t width, const float *dots,
                        const noise_rank1_t *r1, void *y, int y_fp32, noise_stream_t stream);
 
+/* ---- EGGROLL update reassembly (eggroll.py:151-163) ---------------------------------------------------- */
+
+/* Fitness weights (eggroll.py:151-154): f_i = losses[2i+1] - losses[2i] (i < members/2),
+ * z = f / (std(f) + 1e-8) with the unbiased std, weight[d] = sum of z_i over i = d (mod pairs), d < pairs.
+ * members even and >= 4. */
+int noise_update_weights(const float *losses, int64_t members, int64_t pairs, float *weight, noise_stream_t stream);
+
+/* One parameter of an update: its [pairs] noise offsets (Eggroll.offsets, eggroll.py:117-120) and its
+ * gradient, fp32 [rows][cols], or [rows] for a 1-D parameter (cols = 0). */
+typedef struct {
+    const int64_t *offsets;
+    float *grad;
+    int64_t rows, cols;
+} noise_update_param_t;
+
+/* Bytes of workspace noise_update_gradients needs for these parameters at this chunk of directions. */
+int64_t noise_update_workspace_bytes(const noise_update_param_t *params, int nparams, int64_t pairs,
+                                     int64_t chunk);
+
+/* Gradients of eggroll.py:155-163 for up to 64 parameters: grad = scale * sum_{d < pairs} weight[d] a_d b_d^T
+ * with a_d = elements [off_d, off_d + rows) and b_d = [off_d + rows, off_d + rows + cols) of the normal draw
+ * (seed, offset, threads, numel) — the reference's buffer slices (eggroll.py:126) — and
+ * grad = scale * sum_d weight[d] a_d for 1-D parameters. The reference's p.grad is scale = -1/len(fitness).
+ * Parameters with both sides multiples of 256 run as split-bf16x3 MFMA GEMMs over chunks of `chunk`
+ * directions (rounded up to 256), accumulated in order; others (<= 65536 entries) are summed directly.
+ * The matrices' slices are regenerated from the Philox counter in-kernel, or, when `buffer` is non-NULL,
+ * read from that materialised draw (fp32 [numel], noise_normal_fill of the same draw): cheaper once
+ * pairs * sum(rows + cols) exceeds numel, since every buffer element then serves several directions. */
+int noise_update_gradients(const noise_update_param_t *params, int nparams, int64_t pairs, const float *weight,
+                           float scale, int64_t chunk, int64_t numel, uint64_t seed, uint64_t offset,
+                           int64_t threads, const float *buffer, void *workspace, int64_t workspace_bytes,
+                           noise_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,8 +37,11 @@ SIGNATURES = {
     'noise_split3': [_p, _i64, _i64, _i32, _i32, _p, _p],
     'noise_lowrank_embed': [_p, _p, _i64, _i64, _p, _p, _p, _p],
     'noise_rank1_expand': [_p, _p, _i64, _p, _p, _p, _i32, _p],
+    'noise_update_weights': [_p, _i64, _i64, _p, _p],
+    'noise_update_workspace_bytes': [_p, _i32, _i64, _i64],
+    'noise_update_gradients': [_p, _i32, _i64, _p, _f32, _i64, _i64, _u64, _u64, _i64, _p, _p, _i64, _p],
 }
-_RESTYPES = {'noise_last_error': ctypes.c_char_p}
+_RESTYPES = {'noise_last_error': ctypes.c_char_p, 'noise_update_workspace_bytes': ctypes.c_int64}
 
 # noise_attention_fwd flags (include/noise_amd.h)
 ATTN_V_TRANSPOSED = 1
@@ -60,6 +63,13 @@ class Population(ctypes.Structure):
     """noise_population_t."""
     _fields_ = [('members', ctypes.c_int64), ('tokens', ctypes.c_int64), ('sign', ctypes.c_void_p),
                 ('dir_div', ctypes.c_int64)]
+
+
+class UpdateParam(ctypes.Structure):
+    """noise_update_param_t: a parameter's [pairs] noise offsets and its fp32 gradient [rows][cols]."""
+    _fields_ = [('offsets', ctypes.c_void_p), ('grad', ctypes.c_void_p), ('rows', ctypes.c_int64),
+                ('cols', ctypes.c_int64)]
+
 
 _lib = None
 

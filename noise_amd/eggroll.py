@@ -418,6 +418,65 @@ class Eggroll:
                 W, noise, sign, x[seq], y[seq], dir_div=2)
         return losses
 
+    def update(self, losses, offsets, chunk=8192, materialise=None):
+        """The gradients of eggroll.py:151-165 (name -> p.grad, fp32 in the parameter's shape) from one
+        update's gathered losses [members] and its offsets (self.offsets(step)).
+
+        noise_update_weights turns the antithetic losses into per-direction weights (z-scored fitness summed
+        per direction); noise_update_gradients forms -(1/F) sum_d w_d a_d b_d^T for every matrix and
+        -(1/F) sum_d w_d eps_d for the 1-D scalars, matrices as split-bf16x3 MFMA GEMMs over chunks of
+        `chunk` directions. The matrices' slices are regenerated from the Philox counter when the update
+        draws fewer elements than the buffer holds; past that (materialise None) the draw is materialised
+        once (1 GiB, kept for later updates, as the reference keeps its buffer) and read instead."""
+        losses = losses.to(device=self.device, dtype=torch.float32).contiguous()
+        members = losses.numel()
+        fitness_count = members // 2
+        stream = _lib.stream_ptr(self.device)
+        weight = torch.empty(self.pairs, device=self.device, dtype=torch.float32)
+        _lib.call('noise_update_weights', _lib.ptr(losses), members, self.pairs, _lib.ptr(weight), stream)
+        grads = {n: torch.empty(p.shape, device=self.device, dtype=torch.float32) for n, p in self.params.items()}
+        names = list(self.params)
+        d = self.buffer
+        if materialise is None:
+            materialise = self.pairs * sum(sum(p.shape) for p in self.params.values()) > d.numel
+        if materialise and getattr(self, '_materialised', None) is None:
+            self._materialised = d.normal()
+        buf = self._materialised if materialise else None
+        keep = []
+        for start in range(0, len(names), 64):
+            group = names[start:start + 64]
+            table = (_lib.UpdateParam * len(group))()
+            for i, n in enumerate(group):
+                p = self.params[n]
+                off = offsets[n].to(device=self.device, dtype=torch.int64).contiguous()
+                if off.numel() != self.pairs:
+                    raise ValueError(f'{n}: {off.numel()} offsets for {self.pairs} pairs')
+                keep.append(off)
+                table[i] = _lib.UpdateParam(off.data_ptr(), grads[n].data_ptr(), p.shape[0],
+                                            p.shape[1] if p.dim() == 2 else 0)
+            need = _lib.lib().noise_update_workspace_bytes(table, len(group), self.pairs, chunk)
+            if need < 0:
+                raise ValueError('noise_update_workspace_bytes: invalid arguments')
+            ws = torch.empty(max(need, 1), device=self.device, dtype=torch.uint8)
+            _lib.call('noise_update_gradients', table, len(group), self.pairs, _lib.ptr(weight),
+                      -1.0 / fitness_count, chunk, d.numel, d.seed, d.offset, d.threads, _lib.ptr(buf), _lib.ptr(ws),
+                      need, stream)
+        return grads
+
+    def step(self, x, y, optimizer, step, chunk=512, update_chunk=4096):
+        """eggroll.py:131-168 on one GPU: evaluate the population, rebuild the update, step the optimizer;
+        returns the mean loss."""
+        if self.world != 1:
+            raise NotImplementedError('Eggroll.step gathers losses across ranks in the reference; this build '
+                                      'runs one GPU (call population() per rank and gather the losses first)')
+        losses = self.population(step, x, y, chunk=chunk)
+        grads = self.update(losses, self.offsets(step), chunk=update_chunk)
+        optimizer.zero_grad(set_to_none=True)
+        for name, p in self.params.items():
+            p.grad = grads[name]
+        optimizer.step()
+        return losses.mean().item()
+
 
 SIGMA = 0.002   # eggroll.py:31
 

@@ -1,0 +1,158 @@
+"""EGGROLL's update reassembly on the GPU (noise_update_weights / noise_update_gradients through the C ABI)
+against the oracle (oracle/update.py) and against the reference's own loop (eggroll.py:151-165) run with
+torch ops over Eggroll.noise's device slices.
+
+Tolerance: the gradients are fp32 sums over the directions; the device forms the matrices' products as
+split-bf16x3 MFMA GEMMs (each value hi + lo to 2^-16), so entries agree with the float64 oracle to 1e-4 of
+the largest entry (the reference's own products are TF32 under set_float32_matmul_precision('high'),
+about 2^-11 per factor)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import update as oupdate
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-4
+
+
+def _rel(a, b):
+    a, b = np.asarray(a, dtype=np.float64), np.asarray(b, dtype=np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def _losses(members, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    return (8.3 + 0.01 * torch.randn(members, generator=g)).cuda()
+
+
+class _Params(torch.nn.Module):
+    """A handful of parameters of the model's shapes (both update paths, several chunks)."""
+
+    def __init__(self):
+        super().__init__()
+        self.q = torch.nn.Parameter(torch.zeros(512, 512))
+        self.fc = torch.nn.Parameter(torch.zeros(2048, 512))
+        self.proj = torch.nn.Parameter(torch.zeros(512, 2048))
+        self.gate = torch.nn.Parameter(torch.zeros(8, 32))
+        self.lam = torch.nn.Parameter(torch.zeros(8))
+
+
+def _oracle(es, losses, offsets):
+    d = es.buffer
+    shapes = {n: tuple(p.shape) for n, p in es.params.items()}
+    return oupdate.update_gradients(losses.cpu().numpy(), es.pairs, {n: o.cpu().numpy() for n, o in offsets.items()},
+                                    shapes, (d.seed, d.offset, d.threads))
+
+
+def test_weights_match_torch():
+    from noise_amd import _lib
+    for members, pairs in ((128, 64), (256, 64), (1024, 512)):
+        losses = _losses(members, seed=members)
+        w = torch.empty(pairs, device='cuda')
+        _lib.call('noise_update_weights', _lib.ptr(losses), members, pairs, _lib.ptr(w), _lib.stream_ptr())
+        fitness = losses[1::2] - losses[0::2]
+        fitness = fitness / (fitness.std() + 1e-8)
+        ref = torch.zeros(pairs, device='cuda').index_add_(0, torch.arange(len(fitness), device='cuda') % pairs, fitness)
+        torch.cuda.synchronize()
+        print(f'weights members {members} pairs {pairs}', flush=True)
+        assert torch.allclose(w, ref, rtol=1e-5, atol=1e-6)
+
+
+def test_full_model_matches_oracle():
+    from noise_amd.eggroll import Eggroll
+    from noise_amd.model import make_model
+    model = make_model('cpu', 0).cuda()
+    es = Eggroll(model, 64)
+    offsets = es.offsets(3)
+    losses = _losses(128)
+    grads = es.update(losses, offsets)
+    torch.cuda.synchronize()
+    ref = _oracle(es, losses, offsets)
+    assert set(grads) == set(ref) and len(grads) == 60
+    worst = max((_rel(grads[n].cpu().numpy(), ref[n]), n) for n in grads)
+    print('full model worst', worst, flush=True)
+    assert worst[0] <= TOL
+
+
+def test_chunks_accumulate_and_match_the_reference_loop():
+    # pairs 600 in chunks of 256: three GEMM passes (the last partial), 1-D and small parameters alongside
+    from noise_amd.eggroll import Eggroll
+    es = Eggroll(_Params().cuda(), 600)
+    offsets = es.offsets(11)
+    losses = _losses(1200, seed=1)
+    grads = es.update(losses, offsets, chunk=256)
+    # eggroll.py:151-165 literally, over the device slices (fp32 torch matmuls, CHUNK = 256)
+    fitness = losses[1::2] - losses[0::2]
+    fitness = fitness / (fitness.std() + 1e-8)
+    weight = torch.zeros(600, device='cuda').index_add_(0, torch.arange(len(fitness), device='cuda') % 600, fitness)
+    gradients = {n: torch.zeros_like(p) for n, p in es.params.items()}
+    for start in range(0, 600, 256):
+        directions = torch.arange(start, min(600, start + 256), device='cuda')
+        w = weight[directions]
+        for name, n in es.noise(offsets, directions).items():
+            if isinstance(n, tuple):
+                gradients[name] -= (w[:, None] * n[0]).t() @ n[1]
+            else:
+                gradients[name] -= w @ n
+    ref = _oracle(es, losses, offsets)
+    for name in es.params:
+        got = grads[name].cpu().numpy()
+        torch_ref = (gradients[name] / len(fitness)).cpu().numpy()
+        print(name, _rel(got, ref[name]), _rel(got, torch_ref), flush=True)
+        assert got.shape == tuple(es.params[name].shape)
+        assert _rel(got, ref[name]) <= TOL
+        assert _rel(got, torch_ref) <= TOL
+
+
+def test_update_is_deterministic_and_linear_in_fitness():
+    from noise_amd.eggroll import Eggroll
+    es = Eggroll(_Params().cuda(), 64)
+    offsets = es.offsets(0)
+    losses = _losses(128, seed=2)
+    g1 = es.update(losses, offsets)
+    g2 = es.update(losses, offsets)
+    # shifting every loss leaves the antithetic differences (and so the update) unchanged: the losses lie in
+    # [8, 16), where adding 0.5 is exact in fp32
+    g3 = es.update(losses + 0.5, offsets)
+    for n in g1:
+        assert torch.equal(g1[n], g2[n])
+        assert torch.equal(g3[n], g1[n])
+
+
+def test_step_applies_the_update_with_the_optimizer():
+    from noise_amd.eggroll import Eggroll
+    from noise_amd.model import make_model
+    model = make_model('cpu', 0).cuda()
+    es = Eggroll(model, 8)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randint(0, 4096, (1, 2048), generator=g).cuda()
+    y = torch.randint(0, 4096, (1, 2048), generator=g).cuda()
+    before = {n: p.detach().clone() for n, p in es.params.items()}
+    opt = torch.optim.SGD(model.parameters(), lr=0.1)
+    mean = es.step(x, y, opt, 0)
+    after = {n: p.detach().clone() for n, p in es.params.items()}
+    # replay from the old parameters: the same losses and offsets give the same gradients, and SGD moved
+    # each parameter by -lr * grad
+    for n, p in es.params.items():
+        p.data.copy_(before[n])
+    losses = es.population(0, x, y)
+    assert abs(losses.mean().item() - mean) < 1e-6
+    grads = es.update(losses, es.offsets(0))
+    for n in es.params:
+        assert not torch.equal(after[n], before[n]), n
+        assert torch.allclose(after[n], before[n] - 0.1 * grads[n], rtol=0, atol=1e-6), n
+
+
+def test_materialised_buffer_gives_the_same_gradients():
+    # reading the materialised draw (noise_normal_fill) instead of regenerating it changes nothing: the
+    # tables hold the same values, so the GEMMs produce the same bits
+    from noise_amd.eggroll import Eggroll
+    es = Eggroll(_Params().cuda(), 600)
+    offsets = es.offsets(5)
+    losses = _losses(1200, seed=3)
+    g_regen = es.update(losses, offsets, chunk=256, materialise=False)
+    g_buf = es.update(losses, offsets, chunk=256, materialise=True)
+    for n in g_regen:
+        print(n, float((g_regen[n] - g_buf[n]).abs().max()), flush=True)
+        assert torch.equal(g_regen[n], g_buf[n]), n
