@@ -125,13 +125,21 @@ __global__ __launch_bounds__(256) void update_tables_from_buffer_kernel(UpdateSe
     while (p + 1 < s.n && s.row_start[p + 1] <= r0) ++p;
     const int rl0 = r0 - s.row_start[p];  // the 256 rows lie in one parameter (its row count is a multiple of 256)
     const int64_t k0 = (int64_t)blockIdx.y * kTabK;
-    for (int k = 0; k < kTabK; ++k) {
-        float v = 0.0f;
-        if (k0 + k < n) {
-            const int64_t L = s.offsets[p][d0 + k0 + k] + rl0 + tid;
-            v = (L >= 0 && L < numel) ? buf[L] : __builtin_nanf("");
+    const int kv = n - k0 < kTabK ? (int)(n - k0) : kTabK;  // valid directions of this block (>= 1)
+    const int64_t *off = s.offsets[p] + d0 + k0;
+    // 16 loads in flight per thread: addresses clamped into the buffer, out-of-range elements set after
+    for (int kb = 0; kb < kTabK; kb += 16) {
+        float v[16];
+        bool ok[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+            const int64_t L = (kb + e < kv ? off[kb + e] : 0) + rl0 + tid;
+            ok[e] = L >= 0 && L < numel;
+            v[e] = buf[L < 0 ? 0 : (L < numel ? L : numel - 1)];
         }
-        sm[k * kTabPad + tid] = v;
+#pragma unroll
+        for (int e = 0; e < 16; ++e)
+            sm[(kb + e) * kTabPad + tid] = kb + e < kv ? (ok[e] ? v[e] : __builtin_nanf("")) : 0.0f;
     }
     __syncthreads();
     const int c = tid & 7;  // columns 8c .. 8c + 7 of the block's 64
