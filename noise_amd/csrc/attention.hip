@@ -404,16 +404,24 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
         for (int qb = 0; qb < QB; ++qb) {
             const int q = q0w + 32 * qb + j;
             if (edge) {
-                // key of register r in block kb: k0 + 32 kb + 16 (r / 8) + 8 hf + r % 8; visible iff
-                // 0 <= q - key <= W, one unsigned compare
-                const int d0 = q - k0 - 8 * hf;
+                // key of register r in block kb: k0 + 8 hf + c with c = 32 kb + 16 (r / 8) + r % 8 (0 .. 63,
+                // an inline constant); visible iff c <= d0 (causal) and c >= d0 - W (window), d0 = q - k0 - 8 hf.
+                // Each bound is applied only in tiles that reach it (wave-uniform): one compare per score.
+                int d0 = q - k0 - 8 * hf, dw = d0 - W;
+                // (pinned here: compares hoisted above the products would each hold a 64-bit lane mask)
+                asm volatile("" : "+v"(d0), "+v"(dw));
+                const bool causal_edge = k0 + kBKV - 1 > wq_lo, window_edge = k0 < wq_hi - W;
+                auto mask = [&](auto visible) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
+                    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int r = 0; r < 16; ++r) {
-                        const unsigned dq = (unsigned)(d0 - (32 * kb + 16 * (r >> 3) + (r & 7)));
-                        sc[kb][qb][r] = dq <= (unsigned)W ? sc[kb][qb][r] : -__builtin_inff();
-                    }
+                        for (int r = 0; r < 16; ++r) {
+                            const int c = 32 * kb + 16 * (r >> 3) + (r & 7);
+                            sc[kb][qb][r] = visible(c) ? sc[kb][qb][r] : -__builtin_inff();
+                        }
+                };
+                if (causal_edge) mask([&](int c) { return c <= d0; });
+                if (window_edge) mask([&](int c) { return c >= dw; });
             }
             float mb;
             if constexpr (BOUNDED) {
