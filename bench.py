@@ -106,7 +106,8 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update'), default='population')
+    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update', 'head-error'),
+                    default='population')
     ap.add_argument('--pairs', type=int, default=None,
                     help='update workload: antithetic pairs (default 512; the reference trains with 131072)')
     ap.add_argument('--update-chunk', type=int, default=8192, help='update workload: directions per GEMM pass')
@@ -134,6 +135,8 @@ def main():
 
     if args.workload == 'update':
         return bench_update(args)
+    if args.workload == 'head-error':
+        return bench_head_error(args)
     import torch
     from noise_amd import eggroll as eg
     from noise_amd.model import make_model, window_sizes
@@ -278,6 +281,36 @@ def bench_update(args):
         executed_mfma=dict(tflops=round(executed / dt / 1e12, 1), frac=round(executed / dt / BF16_PEAK, 4)),
         grad_finite=bool(all(torch.isfinite(t).all().item() for t in grads.values())),
     )), flush=True)
+
+
+def bench_head_error(args):
+    """DUST.head_error (run.py:380-389) on the cached logits of one DUST batch: 8 sequences x 2048 tokens x
+    4096 bf16 logits -> fp32 coordinate differences. HBM-bound: 8 KiB read + 16 KiB written per token."""
+    import torch
+    from noise_amd.dust import head_error
+    dev = torch.device('cuda', 0)
+    g = torch.Generator().manual_seed(0)
+    logits = (torch.randn(8, 2048, 4096, generator=g) * 5).to(torch.bfloat16).to(dev)
+    y = torch.randint(0, 4096, (8, 2048), generator=g).to(dev)
+    for _ in range(args.warmup):
+        head_error(logits, y, 4096)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        out = head_error(logits, y, 4096)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    traffic = 8 * 2048 * 4096 * (2 + 4)
+    print(json.dumps(dict(
+        metric='DUST head error (coordinate differences) throughput, tokens/s on 1 GPU', value=round(8 * 2048 / ms * 1e3),
+        unit='tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=round(ms, 4),
+        higher_is_better=True, scaling='weak', vs_baseline=None, dtype='fp32 (bf16 logits in)', data='synthetic',
+        config=dict(workload='DUST head_error over cached bf16 logits [8, 2048, 4096]'),
+        roofline=dict(bound='hbm', achieved=round(traffic / ms / 1e6, 1), peak=8000.0, unit='GB/s',
+                      frac=round(traffic / ms / 1e6 / 8000.0, 4), traffic=None),
+        finite=bool(torch.isfinite(out).all().item()))), flush=True)
 
 
 if __name__ == '__main__':

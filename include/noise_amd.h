@@ -223,6 +223,17 @@ int noise_lowrank_embed(float *out, const float *w, int64_t vocab, int64_t width
 int noise_rank1_expand(const noise_population_t *pop, const float *base, int64_t width, const float *dots,
                        const noise_rank1_t *r1, void *y, int y_fp32, noise_stream_t stream);
 
+/* ---- DUST --------------------------------------------------------------------------------------------- */
+
+/* DUST.head_error (run.py:380-389) over coordinate_differences (run.py:121-137): for each row (token) r and
+ * logit j < vocab, out[r][j] = (loss(raw_j + sigma) - loss(raw_j - sigma)) / (2 sigma) with loss the
+ * token's soft-capped (15 tanh(v / 15)) cross-entropy against targets[r], in the reference's closed form
+ * log1p(softmax(z)_j expm1(z' - z_j)) - [j = target] (z' - z_j); rows with targets[r] < 0 and columns
+ * vocab .. out_width are 0. raw: bf16 (raw_bf16) or fp32 [rows][raw_stride]; out fp32 [rows][out_stride]. */
+int noise_coordinate_differences(const void *raw, int raw_bf16, int64_t rows, int64_t vocab, int64_t raw_stride,
+                                 const int64_t *targets, float sigma, float *out, int64_t out_width,
+                                 int64_t out_stride, noise_stream_t stream);
+
 /* ---- EGGROLL update reassembly (eggroll.py:151-163) ---------------------------------------------------- */
 
 /* Fitness weights (eggroll.py:151-154): f_i = losses[2i+1] - losses[2i] (i < members/2),

@@ -37,6 +37,7 @@ SIGNATURES = {
     'noise_split3': [_p, _i64, _i64, _i32, _i32, _p, _p],
     'noise_lowrank_embed': [_p, _p, _i64, _i64, _p, _p, _p, _p],
     'noise_rank1_expand': [_p, _p, _i64, _p, _p, _p, _i32, _p],
+    'noise_coordinate_differences': [_p, _i32, _i64, _i64, _i64, _p, _f32, _p, _i64, _i64, _p],
     'noise_update_weights': [_p, _i64, _i64, _p, _p],
     'noise_update_workspace_bytes': [_p, _i32, _i64, _i64],
     'noise_update_gradients': [_p, _i32, _i64, _p, _f32, _i64, _i64, _u64, _u64, _i64, _p, _p, _i64, _p],

@@ -1,0 +1,92 @@
+// DUST's head error (run.py:380-389 head_error over run.py:121-137 coordinate_differences): for every token
+// and every logit j, the central difference of the token's soft-capped cross-entropy along its own raw logit,
+//   (loss(raw_j + sigma) - loss(raw_j - sigma)) / (2 sigma),
+// in the reference's closed form: moving one logit changes the partition function by one term, so with
+// z = cap(raw), cap(v) = 15 tanh(v / 15), w = softmax(z) and z' the capped moved logit,
+//   loss(z_j -> z') - loss(z) = log1p(w_j expm1(z' - z_j)) - [j = target] (z' - z_j).
+// Zero for ignored tokens (target < 0) and for the padding columns vocab .. out_width.
+//
+// One wave per token row: pass 1 sums exp(z - 15) over the row (z <= 15, so no running maximum is needed and
+// nothing overflows), pass 2 re-reads the row (<= 16 KiB, from the cache) and writes the differences. fp32 throughout with the device library's tanhf /
+// expm1f / log1pf, as the reference's fp32 torch ops.
+#include "common.hpp"
+
+namespace noise {
+namespace {
+
+constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
+
+__device__ inline float load_logit(const void *raw, int bf16, int64_t i) {
+    return bf16 ? (float)static_cast<const __bf16 *>(raw)[i] : static_cast<const float *>(raw)[i];
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// The moved logits through tanh's addition theorem: with t = tanh(raw / 15) and c = tanh(sigma / 15),
+// cap(raw +- sigma) - cap(raw) = +-15 c (1 - t)(1 + t) / (1 +- c t), free of the cancellation of subtracting
+// two capped values (and one tanh per logit instead of three).
+__global__ __launch_bounds__(64 * kRowsPerBlock) void coordinate_differences_kernel(
+    const void *__restrict__ raw, int raw_bf16, int64_t rows, int64_t vocab, int64_t raw_stride,
+    const int64_t *__restrict__ targets, float sigma, float *__restrict__ out, int64_t out_width,
+    int64_t out_stride) {
+    const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    float *orow = out + row * out_stride;
+    const int64_t y = targets[row];
+    if (y < 0) {
+        for (int64_t j = lane; j < out_width; j += 64) orow[j] = 0.0f;
+        return;
+    }
+    const int64_t base = row * raw_stride;
+    const float c = tanhf(sigma * (1.0f / 15.0f)), inv_2s = 1.0f / (2.0f * sigma);
+    float s = 0.0f;
+    for (int64_t j = lane; j < vocab; j += 64)
+        s += __expf(15.0f * tanhf(load_logit(raw, raw_bf16, base + j) * (1.0f / 15.0f)) - 15.0f);
+    const float inv_z = 1.0f / wave_sum(s);
+    for (int64_t j = lane; j < out_width; j += 64) {
+        float d = 0.0f;
+        if (j < vocab) {
+            const float t = tanhf(load_logit(raw, raw_bf16, base + j) * (1.0f / 15.0f));
+            const float w = __expf(15.0f * t - 15.0f) * inv_z, omt2 = (1.0f - t) * (1.0f + t);
+            const float du = 15.0f * c * omt2 / (1.0f + c * t), dd = -15.0f * c * omt2 / (1.0f - c * t);
+            // log1p(a) - log1p(b) = log1p((a - b) / (1 + b)); a - b = w (expm1(du) - expm1(dd)) adds two
+            // terms of opposite sign (du > 0 > dd), so nothing cancels
+            const float eu = expm1f(du), ed = expm1f(dd);
+            d = log1pf(w * (eu - ed) / (1.0f + w * ed));
+            if (j == y) d -= du - dd;
+            d *= inv_2s;
+        }
+        orow[j] = d;
+    }
+}
+
+}  // namespace
+}  // namespace noise
+
+using namespace noise;
+
+extern "C" int noise_coordinate_differences(const void *raw, int raw_bf16, int64_t rows, int64_t vocab,
+                                            int64_t raw_stride, const int64_t *targets, float sigma, float *out,
+                                            int64_t out_width, int64_t out_stride, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(rows >= 0 && vocab >= 1 && out_width >= vocab && raw_stride >= vocab && out_stride >= out_width,
+                    "noise_coordinate_differences: need rows >= 0, 1 <= vocab <= out_width <= out_stride, "
+                    "raw_stride >= vocab");
+    NOISE_CHECK_ARG(sigma > 0.0f, "noise_coordinate_differences: sigma must be positive");
+    if (rows == 0) return NOISE_OK;
+    NOISE_CHECK_ARG(raw != nullptr && targets != nullptr && out != nullptr,
+                    "noise_coordinate_differences: raw, targets and out must be non-NULL");
+    NOISE_CHECK_ARG(aligned(raw, raw_bf16 ? 2 : 4) && aligned(targets, 8) && aligned(out, 4),
+                    "noise_coordinate_differences: misaligned pointer");
+    const int64_t blocks = (rows + kRowsPerBlock - 1) / kRowsPerBlock;
+    NOISE_CHECK_ARG(blocks < (1ll << 31), "noise_coordinate_differences: too many rows");
+    hipLaunchKernelGGL(coordinate_differences_kernel, dim3((unsigned)blocks), dim3(64 * kRowsPerBlock), 0,
+                       (hipStream_t)stream, raw, raw_bf16, rows, vocab, raw_stride, targets, sigma, out, out_width,
+                       out_stride);
+    return launch_status("noise_coordinate_differences");
+}

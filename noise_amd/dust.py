@@ -1,6 +1,8 @@
 """DUST pieces on the population-forward path (train/val/run.py):
 
   head_loss(x, weight, targets, vocab)      run.py:89-94, the fp32 head of rerun (run.py:273-278)
+  coordinate_differences(raw, y, sigma)     run.py:121-137
+  head_error(logits, y, vocab, sigma)       run.py:380-389
   hadamard(d, device, dtype)                run.py:143-152
   OrthogonalDraws                           run.py:218-238 (signs, orthogonal_noise)
 """
@@ -47,3 +49,28 @@ def head_loss(x, weight, targets, vocab):
     _lib.call('noise_pop_head_ce', ctypes.byref(pop), _lib.View(x3.data_ptr(), 0, 3 * d), w3.data_ptr(), 3 * d, vocab,
               ctypes.byref(none), None, tg.data_ptr(), 0, loss.data_ptr(), stream)
     return loss[:rows]
+
+
+def coordinate_differences(raw, y, sigma):
+    """run.py:121-137: per token and logit, (loss(raw_j + sigma) - loss(raw_j - sigma)) / (2 sigma) of the
+    soft-capped cross-entropy, in closed form; zero at ignored tokens (y < 0). raw [..., V] bf16 or fp32
+    (unit inner stride), y [...] int64 -> fp32 [..., V]."""
+    return head_error(raw, y, raw.shape[-1], sigma)
+
+
+def head_error(logits, y, vocab, sigma=0.1):
+    """DUST.head_error (run.py:380-389): coordinate differences of the first `vocab` logits, the padding
+    columns zero. logits [..., Vpad] bf16 or fp32 (unit inner stride), y [...] -> fp32 [..., Vpad]."""
+    if logits.dtype not in (F32, BF16) or logits.stride(-1) != 1:
+        raise ValueError('logits must be bf16 or fp32 with unit inner stride')
+    width = logits.shape[-1]
+    raw = logits.reshape(-1, width)
+    if raw.data_ptr() != logits.data_ptr():
+        raw = raw.contiguous()
+    rows = raw.shape[0]
+    tg = y.reshape(rows).to(device=logits.device, dtype=torch.int64).contiguous()
+    out = torch.empty(*logits.shape[:-1], width, dtype=F32, device=logits.device)
+    _lib.call('noise_coordinate_differences', raw.data_ptr(), 1 if raw.dtype == BF16 else 0, rows, vocab,
+              raw.stride(0), tg.data_ptr(), float(sigma), out.data_ptr(), width, width,
+              _lib.stream_ptr(logits.device))
+    return out

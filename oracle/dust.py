@@ -1,0 +1,31 @@
+"""ORACLE (test infrastructure only): DUST's head error on the CPU.
+
+Restates train/val/run.py:121-137 (coordinate_differences) and run.py:380-389 (head_error) in float64
+numpy: z = 15 tanh(raw / 15), the moved logits z' = cap(raw +- sigma), w = softmax(z), and
+    change_j = log1p(w_j expm1(up_j - z_j)) - log1p(w_j expm1(down_j - z_j)) - [j = y] (up_j - down_j)
+divided by 2 sigma, zero where y < 0.
+"""
+import numpy as np
+
+
+def softcap(v):
+    return 15.0 * np.tanh(v / 15.0)
+
+
+def coordinate_differences(raw, y, sigma):
+    raw = np.asarray(raw, dtype=np.float64)
+    y = np.asarray(y, dtype=np.int64)
+    z, up, down = softcap(raw), softcap(raw + sigma), softcap(raw - sigma)
+    e = np.exp(z - z.max(-1, keepdims=True))
+    w = e / e.sum(-1, keepdims=True)
+    change = np.log1p(w * np.expm1(up - z)) - np.log1p(w * np.expm1(down - z))
+    t = np.clip(y, 0, None)[..., None]
+    np.put_along_axis(change, t, np.take_along_axis(change, t, -1) - np.take_along_axis(up - down, t, -1), -1)
+    return change / (2.0 * sigma) * (y >= 0)[..., None]
+
+
+def head_error(logits, y, vocab, sigma=0.1):
+    logits = np.asarray(logits, dtype=np.float64)
+    out = np.zeros(logits.shape, dtype=np.float64)
+    out[..., :vocab] = coordinate_differences(logits[..., :vocab], y, sigma)
+    return out
