@@ -106,7 +106,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update', 'head-error'),
+    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update', 'head-error', 'dust-block'),
                     default='population')
     ap.add_argument('--pairs', type=int, default=None,
                     help='update workload: antithetic pairs (default 512; the reference trains with 131072)')
@@ -137,6 +137,8 @@ def main():
         return bench_update(args)
     if args.workload == 'head-error':
         return bench_head_error(args)
+    if args.workload == 'dust-block':
+        return bench_dust_block(args)
     import torch
     from noise_amd import eggroll as eg
     from noise_amd.model import make_model, window_sizes
@@ -310,6 +312,48 @@ def bench_head_error(args):
         config=dict(workload='DUST head_error over cached bf16 logits [8, 2048, 4096]'),
         roofline=dict(bound='hbm', achieved=round(traffic / ms / 1e6, 1), peak=8000.0, unit='GB/s',
                       frac=round(traffic / ms / 1e6 / 8000.0, 4), traffic=None),
+        finite=bool(torch.isfinite(out).all().item()))), flush=True)
+
+
+def bench_dust_block(args):
+    """DUST's block_forward (run.py:102-117) as rerun calls it: block 1 (value embeddings, window 1024) of the
+    fixed model over 128 sequences (16 draws x 8 sequences) x 2048 tokens with bf16 jitter at mlp.c_fc."""
+    import torch
+    from noise_amd.dust import block_forward
+    from noise_amd.model import make_model, rotary_tables, window_sizes
+    dev = torch.device('cuda', 0)
+    P = {k: v.to(dev) for k, v in make_model('cpu', 0).state_dict().items()}
+    pre = 'transformer.h.1.'
+    w = dict(q=P[pre + 'attn.c_q.weight'], k=P[pre + 'attn.c_k.weight'], v=P[pre + 'attn.c_v.weight'],
+             gate=P[pre + 'attn.ve_gate.weight'], proj=P[pre + 'attn.c_proj.weight'], fc=P[pre + 'mlp.c_fc.weight'],
+             out=P[pre + 'mlp.c_proj.weight'])
+    S, T = 128, 2048
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(S, T, 512, generator=g).to(dev)
+    ve = torch.randn(S, T, 512, generator=g).bfloat16().to(dev)
+    fc = (0.1 * (torch.randint(0, 2, (S, T, 2048), generator=g) * 2 - 1)).bfloat16().to(dev)
+    cos, sin = (t.to(dev) for t in rotary_tables(T))
+    win = window_sizes(8)[1]
+    for _ in range(args.warmup):
+        block_forward(x, w, ve, cos, sin, win, fc=fc)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        out = block_forward(x, w, ve, cos, sin, win, fc=fc)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    gemm = 2 * (512 * 1536 + 512 * 512 + 2 * 512 * 2048)
+    attn = 4 * 64 * 8 * visible_pairs(T, win) / T
+    flops = (gemm + attn) * S * T
+    print(json.dumps(dict(
+        metric='DUST block_forward throughput (one block, jitter at mlp.c_fc), sequence-tokens/s on 1 GPU',
+        value=round(S * T / ms * 1e3), unit='tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 3), higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
+        data='synthetic', config=dict(workload=f'block 1 of the fixed 37.7M GPT over {S} x {T} tokens, window {win}'),
+        roofline=dict(bound='mfma', achieved=round(flops / ms / 1e9, 1), peak=BF16_PEAK / 1e12, unit='TFLOP/s',
+                      frac=round(flops / ms / 1e9 / (BF16_PEAK / 1e12), 4), traffic=None),
         finite=bool(torch.isfinite(out).all().item()))), flush=True)
 
 

@@ -234,6 +234,21 @@ int noise_coordinate_differences(const void *raw, int raw_bf16, int64_t rows, in
                                  const int64_t *targets, float sigma, float *out, int64_t out_width,
                                  int64_t out_stride, noise_stream_t stream);
 
+/* DUST's block_forward (run.py:102-117) over `sequences` rows of `tokens` (a multiple of 256) tokens: the fixed
+ * model's block (utils/model.py:103-110) on x fp32 [sequences][tokens][512] -> x_out fp32 (same layout), with
+ * the weights unperturbed and optional jitter, bf16 [sequences][tokens][width] or NULL, added where the
+ * reference adds it: jit_o to the attention output, jit_attn to attn.c_proj's product, jit_fc to mlp.c_fc's
+ * product (before ReLU^2, width 2048), jit_mlp to mlp.c_proj's product. w = {c_q, c_k, c_v (bf16 [512][512]),
+ * ve_gate (fp32 [8][32], NULL without value embeddings), c_proj (bf16 [512][512]), c_fc (bf16 [2048][512]),
+ * mlp.c_proj (bf16 [512][2048])}; ve: the value embedding rows bf16 [sequences][tokens][512] or NULL;
+ * rope_cos / rope_sin: bf16 [tokens][32]; window: the block's attention window. The workspace (256 B
+ * aligned) holds the intermediates; its size comes from noise_dust_block_workspace_bytes. */
+int64_t noise_dust_block_workspace_bytes(int64_t sequences, int64_t tokens, int with_ve);
+int noise_dust_block(const float *x, float *x_out, int64_t sequences, int64_t tokens, const void *const w[7],
+                     const void *ve, const void *rope_cos, const void *rope_sin, int64_t window, const void *jit_o,
+                     const void *jit_attn, const void *jit_fc, const void *jit_mlp, void *workspace,
+                     int64_t workspace_bytes, noise_stream_t stream);
+
 /* ---- EGGROLL update reassembly (eggroll.py:151-163) ---------------------------------------------------- */
 
 /* Fitness weights (eggroll.py:151-154): f_i = losses[2i+1] - losses[2i] (i < members/2),

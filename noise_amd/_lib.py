@@ -38,11 +38,14 @@ SIGNATURES = {
     'noise_lowrank_embed': [_p, _p, _i64, _i64, _p, _p, _p, _p],
     'noise_rank1_expand': [_p, _p, _i64, _p, _p, _p, _i32, _p],
     'noise_coordinate_differences': [_p, _i32, _i64, _i64, _i64, _p, _f32, _p, _i64, _i64, _p],
+    'noise_dust_block_workspace_bytes': [_i64, _i64, _i32],
+    'noise_dust_block': [_p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p],
     'noise_update_weights': [_p, _i64, _i64, _p, _p],
     'noise_update_workspace_bytes': [_p, _i32, _i64, _i64],
     'noise_update_gradients': [_p, _i32, _i64, _p, _f32, _i64, _i64, _u64, _u64, _i64, _p, _p, _i64, _p],
 }
-_RESTYPES = {'noise_last_error': ctypes.c_char_p, 'noise_update_workspace_bytes': ctypes.c_int64}
+_RESTYPES = {'noise_last_error': ctypes.c_char_p, 'noise_update_workspace_bytes': ctypes.c_int64,
+             'noise_dust_block_workspace_bytes': ctypes.c_int64}
 
 # noise_attention_fwd flags (include/noise_amd.h)
 ATTN_V_TRANSPOSED = 1

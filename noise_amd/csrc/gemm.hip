@@ -64,7 +64,8 @@ struct QkvArgs {
     Rank1 r1[3];
     const float *dots;        // [rows][3]: x . b_q, x . b_k, x . b_v
     const __bf16 *cos_t, *sin_t;  // [T][32] bf16 (model.py:177-183's tables)
-    const float *ve;          // [V][512] fp32 or NULL
+    const float *ve;          // [V][512] fp32 or NULL; member m reads rows ve + m * ve_m
+    int64_t ve_m;             // 0 (one table for all members) or the member stride of per-member rows
     const int64_t *idx;       // [T]
     const float *gates;       // [rows][8] value-embedding gates (noise_pop_gate)
     Rank1 ve_r1;              // value-embedding noise (a [dirs][V], b [dirs][512]) or a == NULL
@@ -144,7 +145,7 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     M::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds, acc, tid,
            wn0, wm0);
 
-    const float sgn = p.pop.sign[m];
+    const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;  // unperturbed calls may pass no signs
     const float *arow = vec + wn0;  // zeros when unperturbed
     __bf16 *outm = p.out[mat];
     __bf16 *stg = lds + wave * kWaveStg;
@@ -178,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
                 // the gates 2 sigmoid(x[:32] . Wg[head] (+ rank-1)) come precomputed (noise_pop_gate)
                 const int64_t tok = tb ? tokv[1] : tokv[0];
                 const float gate = tb ? (hd ? gt[1][1] : gt[1][0]) : (hd ? gt[0][1] : gt[0][0]);
-                const float *ver = p.ve + tok * 512 + (head0 + hd) * 64;
+                const float *ver = p.ve + m * p.ve_m + tok * 512 + (head0 + hd) * 64;
                 // lowrank_embed of the value table (eggroll.py:61-63): + sign * a_ve[tok] * b_ve[:]
                 const float ves = sgn * (tb ? vesc[1] : vesc[0]);     // 0 without value-table noise
                 const float *veb = vec + 256 + wn0 + hd * 64;           // zeros without value-table noise
@@ -285,11 +286,14 @@ struct ResidArgs {
     int64_t nb_stride[3];
     int nnext;
     float *ndots;             // [rows][nnext]
+    const __bf16 *jit;        // DUST jitter added to the product (run.py:115-117), [m][T][512] bf16, or NULL
+    int64_t jit_m, jit_t;
 };
 
-// MIX: apply the next block's mixing (x0 read); NNEXT: number of next-matrix dots (0..3). Both fixed at
-// compile time so the epilogue's loads carry no per-group branches and can be issued in batches.
-template <int KD, bool MIX, int NNEXT>
+// MIX: apply the next block's mixing (x0 read); NNEXT: number of next-matrix dots (0..3); JIT: add a
+// per-token jitter to the product. All fixed at compile time so the epilogue's loads carry no per-group
+// branches and can be issued in batches.
+template <int KD, bool MIX, int NNEXT, bool JIT = false>
 __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     using M = Mma<8, 512, 128, 32, 3>;
     // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
@@ -321,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
         else if (v == 0)
             st4(vec + 256 * h + 4 * lane, float4{0.f, 0.f, 0.f, 0.f});  // no perturbation: a = 0
     }
-    const float sgn = p.pop.sign[m];
+    const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;  // unperturbed calls may pass no signs
     float dsum[2] = {0.f, 0.f};
     if (p.r1.a) {
 #pragma unroll
@@ -350,16 +354,19 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
         const float corr = sgn * (tb ? dsum[1] : dsum[0]);  // dsum = 0 without perturbation
         const float *xr = p.xres + m * p.xr_m + (int64_t)t * p.xr_t + wn0;
         const float *x0r = MIX ? p.x0 + m * p.x0_m + (int64_t)t * p.x0_t + wn0 : nullptr;
+        const __bf16 *jr = JIT ? p.jit + m * p.jit_m + (int64_t)t * p.jit_t + wn0 : nullptr;
         float ssq = 0.f;
         // one feature block (4 groups of 4) at a time: its residual (and x0) loads are issued, then used
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb) {
             float4 xv[4], zv[4];
+            bf16x4 jv[4];
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int f0 = 32 * fb + 8 * g + 4 * hf;
                 xv[g] = ld4(xr + f0);
                 if constexpr (MIX) zv[g] = ld4(x0r + f0);
+                if constexpr (JIT) jv[g] = *reinterpret_cast<const bf16x4 *>(jr + f0);
             }
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
@@ -367,7 +374,9 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
                 const float4 a4 = ld4(vec + wn0 + f0);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float y = f4get(xv[g], e) + (acc[fb][tb][4 * g + e] + corr * f4get(a4, e));
+                    float prod = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
+                    if constexpr (JIT) prod += (float)jv[g][e];
+                    float y = f4get(xv[g], e) + prod;
                     if constexpr (MIX) y = rl * y + ml * f4get(zv[g], e);
                     acc[fb][tb][4 * g + e] = y;
                     ssq += y * y;
@@ -468,8 +477,10 @@ struct FcArgs {
     const float *nb;          // next b rows [dirs][2048] or NULL
     int64_t nb_stride;
     float *pdots;             // [rows][16]
+    const __bf16 *jit;        // DUST jitter on the hidden pre-activation (run.py:116), [rows][2048] bf16, or NULL
 };
 
+template <bool JIT = false>
 __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     using M = Mma<8, 256, 256, 64, 2>;
     constexpr int kMain = cmax(M::LDS_BYTES, 8 * 64 * kStg * 2);  // K loop, then per-wave act staging
@@ -509,7 +520,7 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     M::run(p.w + (int64_t)n0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds, acc, tid, wn0,
            wm0);
 
-    const float sgn = p.pop.sign[m];
+    const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;  // unperturbed calls may pass no signs
     const int nf0 = n0 + wn0;
     const float *arow = vec + wn0, *brow = vec + 256 + wn0;  // zeros when absent
     __bf16 *stg = lds + wave * 64 * kStg;
@@ -518,6 +529,7 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
         const float corr = sgn * dt[tb];  // dt = 0 without perturbation
+        const __bf16 *jr = JIT ? p.jit + row * 2048 + nf0 : nullptr;
         float pd = 0.f;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
@@ -525,10 +537,13 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
             for (int g = 0; g < 4; ++g) {
                 const int f = 32 * fb + 8 * g + 4 * hf;
                 const float4 a4 = ld4(arow + f), b4 = ld4(brow + f);
+                bf16x4 jv;
+                if constexpr (JIT) jv = *reinterpret_cast<const bf16x4 *>(jr + f);
                 bf16x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     float y = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
+                    if constexpr (JIT) y += (float)jv[e];
                     y = y > 0.f ? y * y : 0.f;
                     o[e] = (__bf16)y;
                     pd += (float)o[e] * f4get(b4, e);
@@ -775,8 +790,8 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
     NOISE_CHECK_ARG(aligned(rope_cos, 16) && aligned(rope_sin, 16), "%s: rotary tables must be 16 B aligned", fn);
     for (int i = 0; i < 3; ++i) {
         NOISE_CHECK_ARG(w[i] && out[i] && aligned(w[i], 16) && aligned(out[i], 8), "%s: weight/output %d NULL or misaligned", fn, i);
-        NOISE_CHECK_ARG(!r1 || !r1[i].a || (dots && aligned(r1[i].a, 16) && r1[i].a_stride % 4 == 0),
-                        "%s: perturbed matrix %d needs dots and 16 B aligned a rows", fn, i);
+        NOISE_CHECK_ARG(!r1 || !r1[i].a || (dots && pop->sign && aligned(r1[i].a, 16) && r1[i].a_stride % 4 == 0),
+                        "%s: perturbed matrix %d needs dots, sign and 16 B aligned a rows", fn, i);
     }
     NOISE_CHECK_ARG(!ve || (idx && gates), "%s: value embeddings need idx and gates", fn);
     QkvArgs a;
@@ -787,10 +802,10 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
         a.r1[i] = make_r1(r1 ? &r1[i] : nullptr);
         a.out[i] = (__bf16 *)out[i];
     }
-    a.dots = dots; a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin; a.ve = ve; a.idx = idx;
+    a.dots = dots; a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin; a.ve = ve; a.ve_m = 0; a.idx = idx;
     a.gates = gates;
     a.ve_r1 = make_r1(ve ? ve_noise : nullptr);
-    NOISE_CHECK_ARG(!a.ve_r1.a || (aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
+    NOISE_CHECK_ARG(!a.ve_r1.a || (pop->sign && aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
                     "%s: value-embedding noise b rows must be 16 B aligned", fn);
     dim3 grid((unsigned)(6 * pop->members * (pop->tokens / 256)));
     hipLaunchKernelGGL(qkv_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
@@ -813,8 +828,9 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     NOISE_CHECK_ARG(!mix || (x0.ptr && aligned(x0.ptr, 16) && x0.sm % 4 == 0 && x0.st % 4 == 0), "%s: mix needs x0", fn);
     NOISE_CHECK_ARG(hout && aligned(hout, 8), "%s: hout NULL or misaligned", fn);
     NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || (next && next_dots)), "%s: bad next-dot request", fn);
-    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && dots_count >= 1 && aligned(r1->a, 16) && r1->a_stride % 4 == 0),
-                    "%s: perturbation needs dots and 16 B aligned a rows", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && pop->sign && dots_count >= 1 && aligned(r1->a, 16) && r1->a_stride % 4 == 0),
+                    "%s: perturbation needs dots, sign and 16 B aligned a rows", fn);
+    NOISE_CHECK_ARG(!(eps_r || eps_x) || pop->sign, "%s: mixing-scalar noise needs sign", fn);
     ResidArgs a;
     a.pop = make_pop(pop);
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
@@ -827,6 +843,7 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     a.x0 = (const float *)x0.ptr; a.x0_m = x0.sm; a.x0_t = x0.st;
     a.hout = (__bf16 *)hout; a.split3 = split3;
     a.nnext = (int)nnext; a.ndots = next_dots;
+    a.jit = nullptr; a.jit_m = 0; a.jit_t = 0;
     for (int k = 0; k < 3; ++k) {
         a.nb[k] = (k < nnext) ? next[k].b : nullptr;
         a.nb_stride[k] = (k < nnext) ? next[k].b_stride : 0;
@@ -850,7 +867,7 @@ extern "C" int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const
     NOISE_TRY(check_pop(pop, 256, fn));
     NOISE_TRY(check_view(x, fn, "x"));
     NOISE_CHECK_ARG(w && aligned(w, 16) && act && aligned(act, 8), "%s: w/act NULL or misaligned", fn);
-    NOISE_CHECK_ARG(!r1 || !r1->a || dots, "%s: perturbation needs dots", fn);
+    NOISE_CHECK_ARG(!r1 || !r1->a || (dots && pop->sign), "%s: perturbation needs dots and sign", fn);
     NOISE_CHECK_ARG(!next || !next->b || partial_dots, "%s: next b needs partial_dots", fn);
     NOISE_CHECK_ARG(!r1 || !r1->a || (aligned(r1->a, 16) && r1->a_stride % 4 == 0),
                     "%s: a rows must be 16 B aligned (stride a multiple of 4)", fn);
@@ -866,8 +883,9 @@ extern "C" int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const
     a.nb = (next && next->b) ? next->b : nullptr;
     a.nb_stride = (next && next->b) ? next->b_stride : 0;
     a.pdots = a.nb ? partial_dots : nullptr;
+    a.jit = nullptr;
     dim3 grid((unsigned)(8 * pop->members * (pop->tokens / 256)));
-    hipLaunchKernelGGL(fc_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    hipLaunchKernelGGL(fc_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 
@@ -913,4 +931,198 @@ extern "C" int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, 
     dim3 grid((unsigned)(pop->members * (pop->tokens / 256)));
     hipLaunchKernelGGL(head_ce_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
+}
+
+// ------------------------------------------------------------------------------------------------
+// DUST's block_forward (run.py:102-117): one unperturbed block over N sequences with optional per-token
+// jitter at the attention output (o), the two residual writers' products (attn, mlp) and the MLP hidden
+// pre-activation (fc). The same kernels as the population forward, with the rank-1 terms off:
+//   h = norm(x) -> q, k, v (+ gated value embedding, rotary, q/k norm) -> attention (+ o) ->
+//   x_mid = x + (y Wproj^T + attn), h2 = norm(x_mid) -> act = relu(h2 Wfc^T + fc)^2 ->
+//   x_out = x_mid + (act Wout^T + mlp)
+// ------------------------------------------------------------------------------------------------
+namespace noise {
+namespace {
+
+__global__ __launch_bounds__(256) void rmsnorm_bf16_kernel(const float *__restrict__ x, int64_t rows,
+                                                           __bf16 *__restrict__ h) {
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float *xr = x + row * 512 + 8 * lane;
+    const float4 a = ld4(xr), b = ld4(xr + 4);
+    float ss = a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w + b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+    const float r = rsqrtf(ss * (1.0f / 512.0f) + kEps);
+    bf16x8 v;
+    v[0] = (__bf16)(a.x * r); v[1] = (__bf16)(a.y * r); v[2] = (__bf16)(a.z * r); v[3] = (__bf16)(a.w * r);
+    v[4] = (__bf16)(b.x * r); v[5] = (__bf16)(b.y * r); v[6] = (__bf16)(b.z * r); v[7] = (__bf16)(b.w * r);
+    *reinterpret_cast<bf16x8 *>(h + row * 512 + 8 * lane) = v;
+}
+
+// y = bf16(y + o), 8 elements per thread
+__global__ __launch_bounds__(256) void add_bf16_kernel(__bf16 *__restrict__ y, const __bf16 *__restrict__ o,
+                                                       int64_t n8) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    bf16x8 a = reinterpret_cast<const bf16x8 *>(y)[i];
+    const bf16x8 b = reinterpret_cast<const bf16x8 *>(o)[i];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = (__bf16)((float)a[e] + (float)b[e]);
+    reinterpret_cast<bf16x8 *>(y)[i] = a;
+}
+
+// value-embedding rows bf16 -> fp32 (the qkv epilogue's table format), and the identity token map
+__global__ __launch_bounds__(256) void ve_rows_kernel(const __bf16 *__restrict__ ve, int64_t n8, float *__restrict__ out,
+                                                      int64_t *__restrict__ iota, int64_t T) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < T) iota[i] = i;
+    if (i >= n8) return;
+    const bf16x8 a = reinterpret_cast<const bf16x8 *>(ve)[i];
+    float4 lo, hi;
+    lo.x = (float)a[0]; lo.y = (float)a[1]; lo.z = (float)a[2]; lo.w = (float)a[3];
+    hi.x = (float)a[4]; hi.y = (float)a[5]; hi.z = (float)a[6]; hi.w = (float)a[7];
+    st4(out + 8 * i, lo);
+    st4(out + 8 * i + 4, hi);
+}
+
+struct DustLayout {
+    int64_t h, vef, gates, q, k, v, y, xmid, h2, act, hs, iota, total;
+};
+
+DustLayout dust_layout(int64_t rows, int64_t T, bool ve) {
+    DustLayout L;
+    int64_t off = 0;
+    auto take = [&](int64_t bytes) {
+        const int64_t o = off;
+        off += (bytes + 255) / 256 * 256;
+        return o;
+    };
+    L.h = take(rows * 512 * 2);
+    L.vef = ve ? take(rows * 512 * 4) : -1;
+    L.gates = ve ? take(rows * 8 * 4) : -1;
+    L.q = take(rows * 512 * 2);
+    L.k = take(rows * 512 * 2);
+    L.v = take(rows * 512 * 2);
+    L.y = take(rows * 512 * 2);
+    L.xmid = take(rows * 512 * 4);
+    L.h2 = take(rows * 512 * 2);
+    L.act = take(rows * 2048 * 2);
+    L.hs = take(rows * 512 * 2);
+    L.iota = ve ? take(T * 8) : -1;
+    L.total = off;
+    return L;
+}
+
+}  // namespace
+}  // namespace noise
+
+extern "C" int64_t noise_dust_block_workspace_bytes(int64_t sequences, int64_t tokens, int with_ve) {
+    if (sequences < 1 || tokens < 1) return -1;
+    return dust_layout(sequences * tokens, tokens, with_ve != 0).total;
+}
+
+extern "C" int noise_dust_block(const float *x, float *x_out, int64_t sequences, int64_t tokens,
+                                const void *const w[7], const void *ve, const void *rope_cos, const void *rope_sin,
+                                int64_t window, const void *jit_o, const void *jit_attn, const void *jit_fc,
+                                const void *jit_mlp, void *workspace, int64_t workspace_bytes,
+                                noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_dust_block";
+    NOISE_CHECK_ARG(sequences >= 1 && tokens >= 256 && tokens % 256 == 0 && sequences * tokens < (1ll << 31),
+                    "%s: tokens must be a positive multiple of 256 and sequences * tokens < 2^31", fn);
+    NOISE_CHECK_ARG(x && x_out && aligned(x, 16) && aligned(x_out, 16), "%s: x / x_out NULL or misaligned", fn);
+    NOISE_CHECK_ARG(w != nullptr, "%s: weights NULL", fn);
+    for (int i = 0; i < 7; ++i)
+        NOISE_CHECK_ARG(i == 3 ? (!ve || w[3] != nullptr) : (w[i] && aligned(w[i], 16)),
+                        "%s: weight %d NULL or misaligned (the gate may be NULL only without value embeddings)", fn, i);
+    NOISE_CHECK_ARG(!ve || aligned(ve, 16), "%s: value embeddings misaligned", fn);
+    NOISE_CHECK_ARG(rope_cos && rope_sin && aligned(rope_cos, 16) && aligned(rope_sin, 16), "%s: rotary tables", fn);
+    const void *jit[4] = {jit_o, jit_attn, jit_fc, jit_mlp};
+    for (int i = 0; i < 4; ++i)
+        NOISE_CHECK_ARG(!jit[i] || aligned(jit[i], 16), "%s: jitter %d misaligned", fn, i);
+    const int64_t rows = sequences * tokens;
+    const DustLayout L = dust_layout(rows, tokens, ve != nullptr);
+    NOISE_CHECK_ARG(workspace && aligned(workspace, 256) && workspace_bytes >= L.total,
+                    "%s: workspace must be 256 B aligned and hold %lld bytes (noise_dust_block_workspace_bytes)", fn,
+                    (long long)L.total);
+    char *ws = static_cast<char *>(workspace);
+    hipStream_t s = (hipStream_t)stream;
+    __bf16 *h = (__bf16 *)(ws + L.h), *q = (__bf16 *)(ws + L.q), *k = (__bf16 *)(ws + L.k), *v = (__bf16 *)(ws + L.v);
+    __bf16 *y = (__bf16 *)(ws + L.y), *h2 = (__bf16 *)(ws + L.h2), *act = (__bf16 *)(ws + L.act);
+    __bf16 *hs = (__bf16 *)(ws + L.hs);
+    float *xmid = (float *)(ws + L.xmid);
+    noise_population_t pop{sequences, tokens, nullptr, 1};
+
+    hipLaunchKernelGGL(rmsnorm_bf16_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, s, x, rows, h);
+    NOISE_TRY(launch_status(fn));
+    float *vef = nullptr, *gates = nullptr;
+    int64_t *iota = nullptr;
+    if (ve) {
+        vef = (float *)(ws + L.vef);
+        gates = (float *)(ws + L.gates);
+        iota = (int64_t *)(ws + L.iota);
+        const int64_t n8 = rows * 512 / 8, work = n8 > tokens ? n8 : tokens;
+        hipLaunchKernelGGL(ve_rows_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, s,
+                           (const __bf16 *)ve, n8, vef, iota, tokens);
+        NOISE_TRY(launch_status(fn));
+        NOISE_TRY(noise_pop_gate(&pop, noise_view_t{h, tokens * 512, 512}, (const float *)w[3], nullptr, gates, stream));
+    }
+    {
+        QkvArgs a{};
+        a.pop = make_pop(&pop);
+        a.x = h; a.xs_m = tokens * 512; a.xs_t = 512;
+        for (int i = 0; i < 3; ++i) a.w[i] = (const __bf16 *)w[i];
+        a.out[0] = q; a.out[1] = k; a.out[2] = v;
+        a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin;
+        a.ve = vef; a.ve_m = tokens * 512; a.idx = iota; a.gates = gates;
+        hipLaunchKernelGGL(qkv_kernel, dim3((unsigned)(6 * sequences * (tokens / 256))), dim3(kThreads), 0, s, a);
+        NOISE_TRY(launch_status(fn));
+    }
+    // q, k: [N][8][T][64]; v transposed [N][8][64][T]; y token-major [N][T][512]
+    NOISE_TRY(noise_attention_fwd(q, k, v, y, sequences, 8, tokens, 64, 8 * tokens * 64, tokens * 64, 64,
+                                  8 * tokens * 64, tokens * 64, 64, 8 * 64 * tokens, 64 * tokens, tokens,
+                                  NOISE_ATTN_V_TRANSPOSED | NOISE_ATTN_QK_NORMED, tokens * 512, 64, 512, window,
+                                  0.125f, nullptr, 0, 1, nullptr, stream));
+    if (jit_o) {
+        const int64_t n8 = rows * 512 / 8;
+        hipLaunchKernelGGL(add_bf16_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, s, y,
+                           (const __bf16 *)jit_o, n8);
+        NOISE_TRY(launch_status(fn));
+    }
+    auto resid = [&](const __bf16 *xin, int K, const void *wt, const float *xres, float *xo, __bf16 *hout,
+                     const void *jt) {
+        ResidArgs a{};
+        a.pop = make_pop(&pop);
+        a.x = xin; a.xs_m = tokens * K; a.xs_t = K;
+        a.w = (const __bf16 *)wt; a.K = K;
+        a.xres = xres; a.xr_m = tokens * 512; a.xr_t = 512;
+        a.xout = xo; a.hout = hout;
+        a.jit = (const __bf16 *)jt; a.jit_m = tokens * 512; a.jit_t = 512;
+        const dim3 grid((unsigned)(sequences * (tokens / 128)));
+        if (K == 512) {
+            if (jt) hipLaunchKernelGGL((resid_kernel<512, false, 0, true>), grid, dim3(kThreads), 0, s, a);
+            else hipLaunchKernelGGL((resid_kernel<512, false, 0>), grid, dim3(kThreads), 0, s, a);
+        } else {
+            if (jt) hipLaunchKernelGGL((resid_kernel<2048, false, 0, true>), grid, dim3(kThreads), 0, s, a);
+            else hipLaunchKernelGGL((resid_kernel<2048, false, 0>), grid, dim3(kThreads), 0, s, a);
+        }
+        return launch_status(fn);
+    };
+    NOISE_TRY(resid(y, 512, w[4], x, xmid, h2, jit_attn));
+    {
+        FcArgs a{};
+        a.pop = make_pop(&pop);
+        a.x = h2; a.xs_m = tokens * 512; a.xs_t = 512;
+        a.w = (const __bf16 *)w[5];
+        a.act = act;
+        a.jit = (const __bf16 *)jit_fc;
+        const dim3 grid((unsigned)(8 * sequences * (tokens / 256)));
+        if (jit_fc) hipLaunchKernelGGL(fc_kernel<true>, grid, dim3(kThreads), 0, s, a);
+        else hipLaunchKernelGGL(fc_kernel<false>, grid, dim3(kThreads), 0, s, a);
+        NOISE_TRY(launch_status(fn));
+    }
+    NOISE_TRY(resid(act, 2048, w[6], xmid, x_out, hs, jit_mlp));
+    return NOISE_OK;
 }

@@ -1,6 +1,7 @@
 """DUST pieces on the population-forward path (train/val/run.py):
 
   head_loss(x, weight, targets, vocab)      run.py:89-94, the fp32 head of rerun (run.py:273-278)
+  block_forward(x, w, ve, cos, sin, window, o, attn, fc, mlp)   run.py:102-117
   coordinate_differences(raw, y, sigma)     run.py:121-137
   head_error(logits, y, vocab, sigma)       run.py:380-389
   hadamard(d, device, dtype)                run.py:143-152
@@ -73,4 +74,43 @@ def head_error(logits, y, vocab, sigma=0.1):
     _lib.call('noise_coordinate_differences', raw.data_ptr(), 1 if raw.dtype == BF16 else 0, rows, vocab,
               raw.stride(0), tg.data_ptr(), float(sigma), out.data_ptr(), width, width,
               _lib.stream_ptr(logits.device))
+    return out
+
+
+def _bf16_weight(t):
+    """bf16 contiguous copy of a weight (the reference's autocast casts it at every call too)."""
+    return t.detach().to(BF16).contiguous()
+
+
+def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=None):
+    """run.py:102-117: Block.forward on x [B, T, 512] with optional jitter at o (attention output), attn
+    (attn.c_proj product), fc (mlp.c_fc product, before ReLU^2) or mlp (mlp.c_proj product), each
+    [B, T, width]. w: the reference's dict q, k, v, gate (None without value embeddings), proj, fc, out.
+    ve: [B, T, 512] value-embedding rows or None. cos, sin: the model's rotary tables (bf16, T x 32 values).
+    Returns x_out fp32 [B, T, 512]. One HIP chain (noise_dust_block): bf16 products with fp32 accumulation,
+    bf16 attention, fp32 residual stream, as the reference's autocast."""
+    dev = x.device
+    B, T, C = x.shape
+    if C != 512 or T % 256:
+        raise ValueError('block_forward: width 512 and a multiple of 256 tokens are supported')
+    xs = x.to(F32).contiguous()
+    out = torch.empty(B, T, C, dtype=F32, device=dev)
+    gate = w.get('gate')
+    ws = [_bf16_weight(w['q']), _bf16_weight(w['k']), _bf16_weight(w['v']),
+          None if gate is None else gate.detach().to(F32).contiguous(),
+          _bf16_weight(w['proj']), _bf16_weight(w['fc']), _bf16_weight(w['out'])]
+    wp = (ctypes.c_void_p * 7)(*[None if t is None else t.data_ptr() for t in ws])
+    if ve is not None:
+        if gate is None:
+            raise ValueError('block_forward: value embeddings need the ve_gate weight')
+        ve = ve.reshape(B, T, C).to(BF16).contiguous()
+    cs = cos.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous()
+    sn = sin.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous()
+    jit = []
+    for t, width in ((o, C), (attn, C), (fc, 4 * C), (mlp, C)):
+        jit.append(None if t is None else t.reshape(B, T, width).to(BF16).contiguous())
+    need = _lib.lib().noise_dust_block_workspace_bytes(B, T, 1 if ve is not None else 0)
+    work = torch.empty(need, dtype=torch.uint8, device=dev)
+    _lib.call('noise_dust_block', xs.data_ptr(), out.data_ptr(), B, T, wp, _lib.ptr(ve), cs.data_ptr(), sn.data_ptr(),
+              int(window), *[_lib.ptr(t) for t in jit], work.data_ptr(), need, _lib.stream_ptr(dev))
     return out

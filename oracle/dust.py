@@ -29,3 +29,26 @@ def head_error(logits, y, vocab, sigma=0.1):
     out = np.zeros(logits.shape, dtype=np.float64)
     out[..., :vocab] = coordinate_differences(logits[..., :vocab], y, sigma)
     return out
+
+
+def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=None):
+    """run.py:102-117 in the dtype of x (fp32 or fp64 torch, CPU): Block.forward with the jitter added at o
+    (attention output), attn (c_proj product), fc (c_fc product, before ReLU^2) and mlp (mlp.c_proj product).
+    w: q, k, v, gate (or None), proj, fc, out; cos, sin [T, 32]."""
+    import torch
+    import torch.nn.functional as F
+    from .model import norm, apply_rotary_emb, attention, N_HEAD, HEAD_DIM
+    add = lambda t, j: t if j is None else t + j.to(t.dtype)
+    B, T, C = x.shape
+    dt = x.dtype
+    W = {k: (None if v is None else v.to(dt)) for k, v in w.items()}
+    h = norm(x)
+    q, k, v = ((h @ W[n].t()).view(B, T, N_HEAD, HEAD_DIM) for n in ('q', 'k', 'v'))
+    if ve is not None:
+        gate = 2 * torch.sigmoid(h[..., :W['gate'].shape[1]] @ W['gate'].t())
+        v = v + gate.unsqueeze(-1) * ve.to(dt).view(B, T, N_HEAD, HEAD_DIM)
+    q, k = norm(apply_rotary_emb(q, cos.to(dt), sin.to(dt))), norm(apply_rotary_emb(k, cos.to(dt), sin.to(dt)))
+    y = add(attention(q, k, v, window).to(dt).reshape(B, T, C), o)
+    x = x + add(y @ W['proj'].t(), attn)
+    hidden = add(norm(x) @ W['fc'].t(), fc)
+    return x + add(F.relu(hidden).square() @ W['out'].t(), mlp)

@@ -62,3 +62,65 @@ def test_coordinate_differences_invalid_arguments():
     assert 'out_width' in L.noise_last_error().decode()
     assert L.noise_coordinate_differences(16, 1, 4, 4096, 4096, 16, 0.0, 16, 4096, 4096, None) == -1
     assert 'sigma' in L.noise_last_error().decode()
+
+
+# ---- block_forward (run.py:102-117): the oracle pinned against the reference's Block and by the algebra
+# of where each jitter enters
+
+def _block_setup(layer, T=256, B=2):
+    import torch
+    from noise_amd.model import make_model
+    from oracle.model import rotary_tables
+    P = {k: v.float() for k, v in make_model('cpu', 0).state_dict().items()}
+    pre = f'transformer.h.{layer}.'
+    w = dict(q=P[pre + 'attn.c_q.weight'], k=P[pre + 'attn.c_k.weight'], v=P[pre + 'attn.c_v.weight'],
+             gate=P.get(pre + 'attn.ve_gate.weight'), proj=P[pre + 'attn.c_proj.weight'],
+             fc=P[pre + 'mlp.c_fc.weight'], out=P[pre + 'mlp.c_proj.weight'])
+    # random residual-writer and gate weights: the pins below then do not depend on the init's values
+    g = torch.Generator().manual_seed(layer)
+    w['proj'] = torch.randn(512, 512, generator=g) * 0.02
+    w['out'] = torch.randn(512, 2048, generator=g) * 0.02
+    x = torch.randn(B, T, 512, generator=g)
+    ve = torch.randn(B, T, 512, generator=g) if w['gate'] is not None else None
+    if w['gate'] is not None:
+        w['gate'] = torch.randn(8, 32, generator=g) * 0.3
+    cos, sin = rotary_tables(T)
+    return P, w, x, ve, cos, sin, g
+
+
+def test_block_forward_without_jitter_is_the_models_block():
+    import torch
+    from oracle.model import _block
+    for layer in (0, 1):
+        P, w, x, ve, cos, sin, _ = _block_setup(layer)
+        pre = f'transformer.h.{layer}.'
+        P = dict(P)
+        P[pre + 'attn.c_proj.weight'], P[pre + 'mlp.c_proj.weight'] = w['proj'], w['out']
+        if ve is not None:
+            P[pre + 'attn.ve_gate.weight'] = w['gate']
+        ref = _block(P, layer, x, ve, cos, sin, 128)
+        got = odust.block_forward(x, w, ve, cos, sin, 128)
+        assert torch.allclose(got, ref, rtol=0, atol=1e-5)
+
+
+def test_block_forward_jitter_placement():
+    import torch
+    P, w, x, ve, cos, sin, g = _block_setup(1)
+    base = odust.block_forward(x, w, ve, cos, sin, 128)
+    j = torch.randn(x.shape, generator=g) * 0.1
+    # mlp: added to the block's last product, so to the output
+    assert torch.allclose(odust.block_forward(x, w, ve, cos, sin, 128, mlp=j), base + j, rtol=0, atol=1e-5)
+    # o: added before c_proj, so o = j Wproj^-T is attn = j
+    o = torch.linalg.solve(w['proj'].double(), j.double().reshape(-1, 512).t()).t().reshape(x.shape).float()
+    a1 = odust.block_forward(x, w, ve, cos, sin, 128, attn=j)
+    a2 = odust.block_forward(x, w, ve, cos, sin, 128, o=o)
+    assert torch.allclose(a1, a2, rtol=0, atol=2e-4)
+    assert not torch.allclose(a1, base + j, rtol=0, atol=1e-3)  # the MLP sees the shifted residual
+    # fc: added to the c_fc product, so fc = norm(x_mid) D^T is c_fc's weight + D
+    w0 = dict(w, out=torch.zeros_like(w['out']))
+    x_mid = odust.block_forward(x, w0, ve, cos, sin, 128)
+    D = torch.randn(2048, 512, generator=g) * 0.01
+    from oracle.model import norm
+    f1 = odust.block_forward(x, w, ve, cos, sin, 128, fc=norm(x_mid) @ D.t())
+    f2 = odust.block_forward(x, dict(w, fc=w['fc'] + D), ve, cos, sin, 128)
+    assert torch.allclose(f1, f2, rtol=0, atol=1e-4)

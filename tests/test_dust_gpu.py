@@ -39,3 +39,81 @@ def test_coordinate_differences_sum_rule():
     assert float(got.sum(-1).abs().max()) < 1e-4
     ref = odust.coordinate_differences(raw.numpy(), y.numpy(), 0.01)
     assert float(np.abs(got.numpy() - ref).max()) <= ATOL
+
+
+def _block_case(layer, seed, B=2, T=2048):
+    from noise_amd.model import make_model, window_sizes
+    from oracle.model import rotary_tables
+    P = {k: v.float() for k, v in make_model('cpu', 0).state_dict().items()}
+    pre = f'transformer.h.{layer}.'
+    g = torch.Generator().manual_seed(seed)
+    w = dict(q=P[pre + 'attn.c_q.weight'], k=P[pre + 'attn.c_k.weight'], v=P[pre + 'attn.c_v.weight'],
+             gate=P.get(pre + 'attn.ve_gate.weight'), proj=torch.randn(512, 512, generator=g) * 0.03,
+             fc=P[pre + 'mlp.c_fc.weight'], out=torch.randn(512, 2048, generator=g) * 0.02)
+    x = torch.randn(B, T, 512, generator=g)
+    ve = None
+    if w['gate'] is not None:
+        w['gate'] = torch.randn(8, 32, generator=g) * 0.3
+        ve = torch.randn(B, T, 512, generator=g).bfloat16()
+    cos, sin = rotary_tables(T)
+    return P, w, x, ve, cos, sin, window_sizes()[layer], g
+
+
+@pytest.mark.parametrize('layer,site', [(0, None), (1, None), (1, 'o'), (3, 'attn'), (5, 'fc'), (7, 'mlp')])
+def test_block_forward_matches_oracle(layer, site):
+    """run.py:102-117 on the device vs the fp32 oracle at T = 2048 (the layer's real window): the block's
+    increment x_out - x within 2e-2 relative (bf16 products and attention), and the fp32 head's per-sequence
+    mean loss on x_out within 1e-3."""
+    from noise_amd.dust import block_forward, head_loss
+    from oracle.model import head_loss as o_head_loss
+    P, w, x, ve, cos, sin, window, g = _block_case(layer, 10 + layer)
+    jit = {}
+    if site:
+        width = 2048 if site == 'fc' else 512
+        jit[site] = (0.1 * (torch.randint(0, 2, (2, 2048, width), generator=g) * 2 - 1)).bfloat16()
+    dev = {k: (None if v is None else v.cuda()) for k, v in w.items()}
+    got = block_forward(x.cuda(), dev, None if ve is None else ve.cuda(), cos.bfloat16().cuda(), sin.bfloat16().cuda(),
+                        window, **{k: v.cuda() for k, v in jit.items()}).cpu()
+    ref = odust.block_forward(x, w, None if ve is None else ve.float(), cos, sin, window,
+                              **{k: v.float() for k, v in jit.items()})
+    d_got, d_ref = got - x, ref - x
+    rel = float((d_got - d_ref).norm() / d_ref.norm())
+    y = torch.randint(0, 4096, (2, 2048), generator=g)
+    head = P['lm_head.weight'] * 30
+    l_got = head_loss(got.cuda(), head.cuda(), y.cuda(), 4096).view(2, 2048).mean(-1).cpu()
+    l_ref = o_head_loss(ref, head, y, 4096).view(2, 2048).mean(-1)
+    err = float((l_got - l_ref).abs().max())
+    print(f'layer {layer} site {site}: increment rel {rel:.2e}, mean-loss err {err:.2e}', flush=True)
+    assert rel <= 2e-2
+    assert err <= 1e-3
+    if site:
+        # the jitter's own effect (jittered minus clean) against the oracle's: a difference of two runs whose
+        # bf16 activations round independently (2^-9 of |y| ~ 1 against a 0.1 jitter), so 5e-2
+        clean = block_forward(x.cuda(), dev, None if ve is None else ve.cuda(), cos.bfloat16().cuda(),
+                              sin.bfloat16().cuda(), window).cpu()
+        ref_clean = odust.block_forward(x, w, None if ve is None else ve.float(), cos, sin, window)
+        eff, ref_eff = got - clean, ref - ref_clean
+        rel_eff = float((eff - ref_eff).norm() / ref_eff.norm())
+        print(f'    jitter effect rel {rel_eff:.2e} (|effect| {float(ref_eff.norm()):.3e})', flush=True)
+        assert rel_eff <= 5e-2
+
+
+def test_block_forward_chain_is_a_rerun():
+    """Two blocks chained from a cached block input with the mixing scalars between them (the loop of
+    run.py:256-272) stay within the same bars as one block."""
+    from noise_amd.dust import block_forward
+    P, w1, x, ve, cos, sin, win1, g = _block_case(1, 21)
+    _, w2, _, _, _, _, win2, _ = _block_case(2, 22)
+    x0 = torch.randn(x.shape, generator=g)
+    lr, lx = 0.9, 0.1
+    dev = lambda w: {k: (None if v is None else v.cuda()) for k, v in w.items()}
+    cb, sb = cos.bfloat16().cuda(), sin.bfloat16().cuda()
+    a = block_forward(x.cuda(), dev(w1), ve.cuda(), cb, sb, win1)
+    a = lr * a + lx * x0.cuda()
+    a = block_forward(a, dev(w2), None, cb, sb, win2).cpu()
+    r = odust.block_forward(x, w1, ve.float(), cos, sin, win1)
+    r = lr * r + lx * x0
+    r = odust.block_forward(r, w2, None, cos, sin, win2)
+    rel = float(((a - x) - (r - x)).norm() / (r - x).norm())
+    print('chain rel', rel, flush=True)
+    assert rel <= 2e-2
