@@ -234,6 +234,13 @@ int noise_coordinate_differences(const void *raw, int raw_bf16, int64_t rows, in
                                  const int64_t *targets, float sigma, float *out, int64_t out_width,
                                  int64_t out_stride, noise_stream_t stream);
 
+/* DUST.direct_errors' estimate update (run.py:351-355) for one site and chunk of n draws:
+ * errors[r][j] += scale * e[r][j], e = einsum('nbt,nbtd->btd', reward.to(bf16), a) with rows r = (b, t):
+ * reward fp32 [n][rows], a bf16 [n][rows][d] (the site's draws), fp32 sums rounded to bf16 as the
+ * reference's bf16 einsum; errors fp32 [rows][d]; the reference's scale is -1 / sigma. d a multiple of 8. */
+int noise_draw_errors(const float *reward, const void *a, int64_t n, int64_t rows, int64_t d, float scale,
+                      float *errors, noise_stream_t stream);
+
 /* DUST's block_forward (run.py:102-117) over `sequences` rows of `tokens` (a multiple of 256) tokens: the fixed
  * model's block (utils/model.py:103-110) on x fp32 [sequences][tokens][512] -> x_out fp32 (same layout), with
  * the weights unperturbed and optional jitter, bf16 [sequences][tokens][width] or NULL, added where the

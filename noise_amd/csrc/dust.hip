@@ -10,6 +10,7 @@
 // nothing overflows), pass 2 re-reads the row (<= 16 KiB, from the cache) and writes the differences. fp32 throughout with the device library's tanhf /
 // expm1f / log1pf, as the reference's fp32 torch ops.
 #include "common.hpp"
+#include "mfma.hpp"
 
 namespace noise {
 namespace {
@@ -65,10 +66,52 @@ __global__ __launch_bounds__(64 * kRowsPerBlock) void coordinate_differences_ker
     }
 }
 
+// DUST.direct_errors' estimate update (run.py:351-355): errors[r][j] += scale * e[r][j] with
+//   e = einsum('nbt,nbtd->btd', reward.to(bf16), a)   (bf16 operands, fp32 sums, a bf16 result)
+// over the n draws of a chunk, rows r = (b, t). One thread per 8 consecutive coordinates of a row.
+__global__ __launch_bounds__(256) void draw_errors_kernel(const float *__restrict__ reward, const __bf16 *__restrict__ a,
+                                                          int64_t n, int64_t rows, int64_t d, float scale,
+                                                          float *__restrict__ errors) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;  // over rows * d / 8
+    const int64_t per_row = d / 8;
+    if (i >= rows * per_row) return;
+    const int64_t r = i / per_row, j = (i - r * per_row) * 8;
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int64_t q = 0; q < n; ++q) {
+        const float w = (float)(__bf16)reward[q * rows + r];
+        const bf16x8 v = *reinterpret_cast<const bf16x8 *>(a + (q * rows + r) * d + j);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] += w * (float)v[e];
+    }
+    float *out = errors + r * d + j;
+    float4 o0 = *reinterpret_cast<const float4 *>(out), o1 = *reinterpret_cast<const float4 *>(out + 4);
+    o0.x += scale * (float)(__bf16)acc[0]; o0.y += scale * (float)(__bf16)acc[1];
+    o0.z += scale * (float)(__bf16)acc[2]; o0.w += scale * (float)(__bf16)acc[3];
+    o1.x += scale * (float)(__bf16)acc[4]; o1.y += scale * (float)(__bf16)acc[5];
+    o1.z += scale * (float)(__bf16)acc[6]; o1.w += scale * (float)(__bf16)acc[7];
+    *reinterpret_cast<float4 *>(out) = o0;
+    *reinterpret_cast<float4 *>(out + 4) = o1;
+}
+
 }  // namespace
 }  // namespace noise
 
 using namespace noise;
+
+extern "C" int noise_draw_errors(const float *reward, const void *a, int64_t n, int64_t rows, int64_t d, float scale,
+                                 float *errors, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(n >= 1 && rows >= 0 && d >= 8 && d % 8 == 0,
+                    "noise_draw_errors: need n >= 1, rows >= 0 and d a positive multiple of 8");
+    if (rows == 0) return NOISE_OK;
+    NOISE_CHECK_ARG(reward && a && errors && aligned(reward, 4) && aligned(a, 16) && aligned(errors, 16),
+                    "noise_draw_errors: reward, a and errors must be non-NULL and aligned (a and errors 16 B)");
+    const int64_t work = rows * (d / 8);
+    NOISE_CHECK_ARG((work + 255) / 256 < (1ll << 31), "noise_draw_errors: too many rows");
+    hipLaunchKernelGGL(draw_errors_kernel, dim3((unsigned)((work + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       reward, (const __bf16 *)a, n, rows, d, scale, errors);
+    return launch_status("noise_draw_errors");
+}
 
 extern "C" int noise_coordinate_differences(const void *raw, int raw_bf16, int64_t rows, int64_t vocab,
                                             int64_t raw_stride, const int64_t *targets, float sigma, float *out,

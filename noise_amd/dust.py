@@ -2,6 +2,7 @@
 
   head_loss(x, weight, targets, vocab)      run.py:89-94, the fp32 head of rerun (run.py:273-278)
   block_forward(x, w, ve, cos, sin, window, o, attn, fc, mlp)   run.py:102-117
+  draw_errors(errors, reward, a, sigma)     run.py:351-355 (direct_errors' estimate update)
   coordinate_differences(raw, y, sigma)     run.py:121-137
   head_error(logits, y, vocab, sigma)       run.py:380-389
   hadamard(d, device, dtype)                run.py:143-152
@@ -114,3 +115,18 @@ def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=No
     _lib.call('noise_dust_block', xs.data_ptr(), out.data_ptr(), B, T, wp, _lib.ptr(ve), cs.data_ptr(), sn.data_ptr(),
               int(window), *[_lib.ptr(t) for t in jit], work.data_ptr(), need, _lib.stream_ptr(dev))
     return out
+
+
+def draw_errors(errors, reward, a, sigma):
+    """run.py:351-355 in place: errors -= einsum('nbt,nbtd->btd', reward.to(bf16), a).float() / sigma.
+    errors fp32 [b, t, d] (contiguous), reward [n, b, t], a bf16 [n * b, t, d] or [n, b, t, d]."""
+    n = reward.shape[0]
+    rows = errors.numel() // errors.shape[-1]
+    d = errors.shape[-1]
+    if errors.dtype != F32 or not errors.is_contiguous():
+        raise ValueError('errors must be a contiguous fp32 tensor')
+    r = reward.to(device=errors.device, dtype=F32).reshape(n, rows).contiguous()
+    av = a.to(BF16).reshape(n, rows, d).contiguous()
+    _lib.call('noise_draw_errors', r.data_ptr(), av.data_ptr(), n, rows, d, -1.0 / float(sigma), errors.data_ptr(),
+              _lib.stream_ptr(errors.device))
+    return errors

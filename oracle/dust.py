@@ -52,3 +52,13 @@ def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=No
     x = x + add(y @ W['proj'].t(), attn)
     hidden = add(norm(x) @ W['fc'].t(), fc)
     return x + add(F.relu(hidden).square() @ W['out'].t(), mlp)
+
+
+def draw_errors(errors, reward, a, sigma):
+    """run.py:351-355: errors - einsum('nbt,nbtd->btd', bf16(reward), a) rounded to bf16, / sigma (float64
+    sums; bf16 rounding of the reward and of the einsum's result as the reference's bf16 einsum)."""
+    import torch
+    bf = lambda v: torch.as_tensor(np.asarray(v, dtype=np.float32)).bfloat16().double().numpy()
+    n = reward.shape[0]
+    e = np.einsum('nbt,nbtd->btd', bf(reward), np.asarray(a, dtype=np.float64).reshape(n, *errors.shape))
+    return np.asarray(errors, dtype=np.float64) - bf(e) / sigma

@@ -117,3 +117,20 @@ def test_block_forward_chain_is_a_rerun():
     rel = float(((a - x) - (r - x)).norm() / (r - x).norm())
     print('chain rel', rel, flush=True)
     assert rel <= 2e-2
+
+
+@pytest.mark.parametrize('d', [512, 2048])
+def test_draw_errors_matches_oracle(d):
+    """run.py:351-355: one chunk's estimate update against the float64 einsum of the oracle; both round the
+    reward and the einsum's result to bf16, so entries agree to one bf16 step of the result."""
+    from noise_amd.dust import draw_errors
+    g = torch.Generator().manual_seed(d)
+    n, b, t, sigma = 16, 8, 256, 0.1
+    reward = torch.randn(n, b, t, generator=g) * 0.01
+    a = (torch.randint(0, 2, (n * b, t, d), generator=g) * 2 - 1).bfloat16()
+    errors = torch.randn(b, t, d, generator=g)
+    got = draw_errors(errors.clone().cuda(), reward.cuda(), a.cuda(), sigma).cpu().double().numpy()
+    ref = odust.draw_errors(errors.numpy(), reward.numpy(), a.float().numpy(), sigma)
+    step = np.abs(ref - errors.double().numpy()) * 2 ** -7 + 1e-6
+    print('max abs err', float(np.abs(got - ref).max()), flush=True)
+    assert np.all(np.abs(got - ref) <= step)
