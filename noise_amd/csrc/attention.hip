@@ -13,8 +13,9 @@
 //  - attention_fwd_kernel (any layout and length): 4 waves of 64 queries, K / V tiles register-staged
 //    into double-buffered LDS (rows padded to 144 B), running-max softmax.
 //  - attention_vt_kernel (transposed V, length a multiple of 256; the population path): 8 waves of 32
-//    queries (four waves per SIMD), K / V^T copied global -> LDS into a three-stage swizzled ring, and
-//    an optional fixed-shift softmax for RMS-normed q, k (described at the kernel).
+//    queries (four waves per SIMD) in two groups half a tile apart, K / V^T copied global -> LDS into a
+//    four-stage swizzled ring, and an optional fixed-shift softmax for RMS-normed q, k (described at the
+//    kernel).
 // Key tiles outside a wave's band are skipped; masking runs only on band-edge tiles. All query tiles of
 // one head run on one XCD (workgroups are dispatched round-robin over the 8 XCDs), heaviest tile first,
 // so that head's K/V stay in that XCD's L2.
@@ -266,8 +267,8 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
 
 
 // ------------------------------------------------------------------------------------------------
-// Transposed-V kernel (the population layout; seq a multiple of 64). K and V^T tiles are copied
-// global -> LDS directly (global_load_lds_dwordx4) into a ring of three stages, rows of 128 B with the
+// Transposed-V kernel (the population layout; seq a multiple of 256). K and V^T tiles are copied
+// global -> LDS directly (global_load_lds_dwordx4) into a ring of four stages, rows of 128 B with the
 // 16 B chunks XOR-swizzled by row pair (conflict-free fragment reads). The K rows of each 32-key block
 // are read in the order sigma (bits 2 and 3 of the key index swapped), which makes register r of a
 // lane's S^T block hold key 16 (r / 8) + 8 hf + (r % 8): the 8 scores P^T needs as one B fragment of
@@ -278,19 +279,21 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
 // shift-invariant; fp32 and bf16 keep full relative precision down to 2^-126).
 // ------------------------------------------------------------------------------------------------
 constexpr int kStage = 2 * 64 * 128;  // K [64 keys][64 d] then V^T [64 d][64 keys], 128 B rows
-// Queries per workgroup of the transposed-V kernel and its ring depth (128 queries and 4 stages were measured
-// slower on MI355X).
-constexpr int kVtQT = 256;
-constexpr int kVtNS = 3;
+constexpr int kVtQT = 256;  // queries per workgroup of the transposed-V kernel
 
 __device__ __forceinline__ int key_sigma(int i) { return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1); }
 
-// QT queries per workgroup in waves of 32 (~128 VGPRs: four waves per SIMD), NS-stage K / V^T ring.
-template <bool BOUNDED, int QT, int NS>
-__global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_vt_kernel(AttnArgs a) {
-    constexpr int QB = 1, NW = QT / 32, QW = 32, CPW = 16 / NW;  // waves, queries per wave, copies per wave
-    static_assert(NW * QW == QT && NW % 2 == 0 && 16 % NW == 0, "whole tile; copy parity follows the wave parity");
-    static_assert(NS >= 2 && NS <= 4, "ring depth");
+// 256 queries per workgroup in 8 waves of 32 (~120 VGPRs: four waves per SIMD with two workgroups per CU).
+// Ping-pong: waves 0-3 (A) and 4-7 (B, one of each per SIMD) run the same tile sequence half a phase apart, so one wave's softmax (VALU) overlaps the other's products (MFMA) instead
+// of every wave of the workgroup switching between them together after each barrier. Per barrier interval
+// A does S = K Q^T, softmax, O += V^T P^T of tile t; B does the softmax and O of tile t - 1, then S of tile t.
+// Both groups pass the same barriers (one per tile), placed at different points of their loops. A alone
+// copies the K / V^T tiles (4 copies per wave per tile) into a 4-slot ring; after barrier t + 1 it refills
+// the slot of tile t - 1, which B finished reading before that barrier.
+template <bool BOUNDED>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_vt_kernel(AttnArgs a) {
+    constexpr int QT = kVtQT, NS = 4;
+    constexpr int QB = 1, NW = QT / 32, QW = 32, CPW = 4;  // waves, queries per wave, copies per A wave
     __shared__ __attribute__((aligned(16))) char lds[NS * kStage];
 
     int wg = blockIdx.x;
@@ -318,18 +321,22 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     for (int qb = 0; qb < QB; ++qb)
 #pragma unroll
         for (int s = 0; s < 4; ++s) qf[qb][s] = load_bf16x8(Qb + (int64_t)(q0w + 32 * qb + j) * a.qs_t + 16 * s + 8 * hf);
+    // the query fragments land before any tile copy is issued: the compiler's own wait for them inside the
+    // tile loop would otherwise be a vmcnt that also drains the copies in flight
+    vm_wait<0>();
 
-    // copies: per stage 16 of 1 KB (8 rows); wave w issues copies c = NW i + w, rows 8 (c % 8) .. of K (c < 8)
+    // copies: per stage 16 of 1 KB (8 rows); A wave w issues copies c = 4 i + w, rows 8 (c % 8) .. of K (c < 8)
     // or V^T. Row R's slot P holds chunk P ^ ((R >> 1) & 7); for this lane R = 8 c' + lane / 8, so the chunk
     // it fetches is (lane % 8) ^ (4 (c' & 1) + lane / 16), the same for all of a wave's copies (c' & 1 = w & 1).
     const int chunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
+    const bool group_a = wave < 4;
     const unsigned koff = (unsigned)((lane >> 3) * a.ks_t * 2 + chunk * 16);
     const unsigned voff = (unsigned)((lane >> 3) * a.vs_x * 2 + chunk * 16);
     const unsigned lb = lds_addr(lds);
     auto issue = [&](int k0, unsigned st) {  // st: LDS byte address of the stage
 #pragma unroll
         for (int i = 0; i < CPW; ++i) {
-            const int c = NW * i + wave;
+            const int c = 4 * i + wave;  // A waves only: copy c's row parity is the wave's
             if (c < 8)
                 lds_dma16_at(Kb + (int64_t)(k0 + 8 * c) * a.ks_t, koff, st + c * 1024);
             else
@@ -363,24 +370,13 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
     const int wq_lo = q0w, wq_hi = q0w + QW - 1;
     const float c2 = a.scale_log2, shift = a.shift;
 
-    // tiles 0 .. NS-2 in flight; iteration it waits for tile it, then refills the slot of tile it - 1
-#pragma unroll
-    for (int t = 0; t < NS - 1; ++t)
-        if (t < nt) issue((kv_first + t) * kBKV, lb + t * kStage);
-
-#pragma unroll 1
-    for (int it = 0; it < nt; ++it) {
-        // tile it landed: at most min(NS - 2, nt - 1 - it) later tiles in flight
-        vm_wait_groups<CPW, NS - 2>(nt - 1 - it < NS - 2 ? nt - 1 - it : NS - 2);
-        __syncthreads();  // ... for every wave; tile it - 1 fully read
-        if (it + NS - 1 < nt) issue((kv_first + it + NS - 1) * kBKV, lb + ((it + NS - 1) % NS) * kStage);
-        const char *st = lds + (it % NS) * kStage;
-        const int k0 = (kv_first + it) * kBKV;
-        const bool active = k0 <= wq_hi && k0 + kBKV - 1 >= wq_lo - W;
-        if (!active) continue;
-        const bool edge = (k0 + kBKV - 1 > wq_lo) || (k0 < wq_hi - W);
-
-        f32x16 sc[2][QB];
+    f32x16 sc[2][QB];
+    bf16x8 pf[QB][4];
+    auto tile_k0 = [&](int t) { return (kv_first + t) * kBKV; };
+    auto active = [&](int t) { return tile_k0(t) <= wq_hi && tile_k0(t) + kBKV - 1 >= wq_lo - W; };
+    // S = K Q^T of tile t (slot t % NS)
+    auto qk = [&](int t) {
+        const char *st = lds + (t % NS) * kStage;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -394,8 +390,11 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
                 for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = mfma32x32x16(ka, qf[qb][s], sc[kb][qb]);
             }
         }
-
-        bf16x8 pf[QB][4];
+    };
+    // masked softmax weights of tile t into pf (and l, m, o for the running maximum)
+    auto softmax = [&](int t) {
+        const int k0 = tile_k0(t);
+        const bool edge = (k0 + kBKV - 1 > wq_lo) || (k0 < wq_hi - W);
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
             const int q = q0w + 32 * qb + j;
@@ -455,6 +454,10 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
                 pf[qb][s] = v;
             }
         }
+    };
+    // O += V^T P^T of tile t
+    auto pv = [&](int t) {
+        const char *st = lds + (t % NS) * kStage;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -463,6 +466,46 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) o[db][qb] = mfma32x32x16(va, pf[qb][s], o[db][qb]);
             }
+        }
+    };
+
+    if (group_a) {
+        // tiles 0 .. 2 in flight; tile 0 landed when min(2, nt - 1) later tiles may still be
+#pragma unroll
+        for (int t = 0; t < 3; ++t)
+            if (t < nt) issue(tile_k0(t), lb + t * kStage);
+        vm_wait_groups<CPW, 2>(nt - 1 < 2 ? nt - 1 : 2);
+    }
+    __syncthreads();  // barrier 0: tile 0 landed
+    if (group_a) {
+#pragma unroll 1
+        for (int t = 0; t < nt; ++t) {
+            if (active(t)) {
+                qk(t);
+                softmax(t);
+                pv(t);
+            }
+            if (t + 1 < nt) {
+                // tile t + 1 landed: tiles after it issued so far: min(t + 2, nt - 1) - (t + 1)
+                vm_wait_groups<CPW, 1>(nt - 2 - t < 1 ? nt - 2 - t : 1);
+                __syncthreads();  // barrier t + 1
+                if (t + 3 < nt) issue(tile_k0(t + 3), lb + ((t + 3) % NS) * kStage);
+            }
+        }
+    } else {
+        if (active(0)) qk(0);
+#pragma unroll 1
+        for (int t = 1; t < nt; ++t) {
+            __syncthreads();  // barrier t: tile t landed
+            if (active(t - 1)) {
+                softmax(t - 1);
+                pv(t - 1);
+            }
+            if (active(t)) qk(t);
+        }
+        if (active(nt - 1)) {
+            softmax(nt - 1);
+            pv(nt - 1);
         }
     }
 
@@ -494,6 +537,7 @@ __global__ __launch_bounds__(QT * 2) __attribute__((amdgpu_waves_per_eu(4, 4))) 
         }
     }
 }
+
 
 
 }  // namespace
@@ -552,11 +596,9 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     dim3 grid((unsigned)(bh * qtiles));
     if (vt_path) {
         if (flags & NOISE_ATTN_QK_NORMED)
-            hipLaunchKernelGGL((attention_vt_kernel<true, kVtQT, kVtNS>), grid, dim3(kVtQT * 2), 0,
-                               (hipStream_t)stream, a);
+            hipLaunchKernelGGL(attention_vt_kernel<true>, grid, dim3(512), 0, (hipStream_t)stream, a);
         else
-            hipLaunchKernelGGL((attention_vt_kernel<false, kVtQT, kVtNS>), grid, dim3(kVtQT * 2), 0,
-                               (hipStream_t)stream, a);
+            hipLaunchKernelGGL(attention_vt_kernel<false>, grid, dim3(512), 0, (hipStream_t)stream, a);
     } else if (v_transposed)
         hipLaunchKernelGGL(attention_fwd_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
     else
