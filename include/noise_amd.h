@@ -131,11 +131,21 @@ typedef struct {
     int64_t a_stride, b_stride;
 } noise_rank1_t;
 
+/* Rounding of the forward between its stored tensors (noise_population_t.rounding):
+ * FUSED  the training scripts' compiled population forward (eggroll.py:66-103 under torch.compile): elementwise
+ *        chains in fp32, the residual stream fp32, bf16 only where a tensor is materialised in bf16;
+ * EAGER  the scorer's eager autocast forward (utils/eval.py:43-46 over utils/model.py:193-209 with the bf16
+ *        embeddings of model.py:170-174): every elementwise op's result rounded to bf16, so the residual
+ *        stream is bf16-valued. Unperturbed calls only (no rank-1 terms, lambda noise or next-matrix dots). */
+#define NOISE_ROUNDING_FUSED 0
+#define NOISE_ROUNDING_EAGER 1
+
 /* Shared member bookkeeping of one population call. */
 typedef struct {
     int64_t members, tokens;
     const float *sign;   /* [members] +-sigma (or any per-member scale) */
     int64_t dir_div;     /* member m uses noise row m / dir_div */
+    int64_t rounding;    /* NOISE_ROUNDING_FUSED (0) or NOISE_ROUNDING_EAGER */
 } noise_population_t;
 
 /* Block entry (eggroll.py:74-79 for block 0; model.py:196-199): e = wte[idx[t]] (+ sign * a[idx[t]] * b,
@@ -161,14 +171,15 @@ int noise_pop_gate(const noise_population_t *pop, noise_view_t x, const float *g
 
 /* Q, K, V of one block for every member (eggroll.py:81-90): x (= norm of the block input, bf16) times
  * c_q, c_k, c_v (w[0..2], bf16 [512][512]) + sign * dots[row*3 + i] * a_i; on V, + gates[row*8 + h] *
- * (ve[idx[t], :] + lowrank_embed noise of the value table, ve_noise a [dirs][V], b [dirs][512], or NULL)
- * when ve (fp32 [V][512]) is not NULL; rotary (rope_cos/rope_sin: model.py:177-183's bf16 tables,
+ * (ve[idx[m * idx_sm + t], :] + lowrank_embed noise of the value table, ve_noise a [dirs][V], b [dirs][512],
+ * or NULL) when ve (fp32 [V][512]) is not NULL; idx_sm = 0 when every member reads the same sequence (the
+ * population), else the member stride of per-member token ids (>= tokens: scoring distinct sequences); rotary (rope_cos/rope_sin: model.py:177-183's bf16 tables,
  * [tokens][32] bf16, 16 B aligned) then per-head RMSNorm on Q and K. Outputs bf16: Q, K
  * [members][8][tokens][64]; V transposed [members][8][64][tokens]. */
 int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3], const noise_rank1_t r1[3],
                   const float *dots, const void *rope_cos, const void *rope_sin, const float *ve,
-                  const int64_t *idx, const float *gates, const noise_rank1_t *ve_noise, void *const out[3],
-                  noise_stream_t stream);
+                  const int64_t *idx, int64_t idx_sm, const float *gates, const noise_rank1_t *ve_noise,
+                  void *const out[3], noise_stream_t stream);
 
 /* Residual writer (eggroll.py:92 attn.c_proj and :93 mlp.c_proj): y = xres + x w^T + sign * (sum of
  * dots_count dots at dots[row*dots_stride]) * a; if mix: y = rl*y + ml*x0 (the next block's mixing,

@@ -26,7 +26,7 @@ SIGNATURES = {
                             _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _p, _p],
     'noise_pop_embed': [_p, _i32, _p, _p, _p, _f32, _f32, _p, _p, _i64, _p, _p, _p, _p],
     'noise_member_dots': [_p, 'View', _i64, _p, _i64, _p, _p],
-    'noise_pop_qkv': [_p, 'View', _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    'noise_pop_qkv': [_p, 'View', _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p],
     'noise_pop_gate': [_p, 'View', _p, _p, _p, _p],
     'noise_pop_residual': [_p, 'View', _p, _i64, _p, _p, _i64, _i64, 'View', _p, _i32, _f32, _f32, _p, _p,
                            _i64, 'View', _p, _i32, _p, _i64, _p, _p],
@@ -48,6 +48,10 @@ SIGNATURES = {
 _RESTYPES = {'noise_last_error': ctypes.c_char_p, 'noise_update_workspace_bytes': ctypes.c_int64,
              'noise_dust_block_workspace_bytes': ctypes.c_int64}
 
+# noise_population_t.rounding (include/noise_amd.h)
+ROUNDING_FUSED = 0
+ROUNDING_EAGER = 1
+
 # noise_attention_fwd flags (include/noise_amd.h)
 ATTN_V_TRANSPOSED = 1
 ATTN_QK_NORMED = 2
@@ -65,9 +69,9 @@ class Rank1(ctypes.Structure):
 
 
 class Population(ctypes.Structure):
-    """noise_population_t."""
+    """noise_population_t (rounding: ROUNDING_FUSED, the default, or ROUNDING_EAGER)."""
     _fields_ = [('members', ctypes.c_int64), ('tokens', ctypes.c_int64), ('sign', ctypes.c_void_p),
-                ('dir_div', ctypes.c_int64)]
+                ('dir_div', ctypes.c_int64), ('rounding', ctypes.c_int64)]
 
 
 class UpdateParam(ctypes.Structure):

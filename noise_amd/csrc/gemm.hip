@@ -66,7 +66,8 @@ struct QkvArgs {
     const __bf16 *cos_t, *sin_t;  // [T][32] bf16 (model.py:177-183's tables)
     const float *ve;          // [V][512] fp32 or NULL; member m reads rows ve + m * ve_m
     int64_t ve_m;             // 0 (one table for all members) or the member stride of per-member rows
-    const int64_t *idx;       // [T]
+    const int64_t *idx;       // token ids: member m, token t at idx[m * idx_m + t]
+    int64_t idx_m;            // 0 (one sequence for all members) or the member stride of per-member tokens
     const float *gates;       // [rows][8] value-embedding gates (noise_pop_gate)
     Rank1 ve_r1;              // value-embedding noise (a [dirs][V], b [dirs][512]) or a == NULL
     __bf16 *out[3];           // q, k: [m][8][T][64]; v transposed: [m][8][64][T]
@@ -76,6 +77,9 @@ struct QkvArgs {
 // XOR-swizzled by (token / 4) mod 4, so the 8 B reads of 16 consecutive tokens hit distinct banks
 __device__ __forceinline__ int rope_off(int row, int chunk) { return row * 64 + ((chunk ^ ((row >> 2) & 3)) << 4); }
 
+// EAGER: the eager autocast forward's roundings (every elementwise op's result rounded to bf16; unperturbed
+// calls only): q, k, v rounded as linear outputs, v + bf16(gate * ve), rotary products and sums rounded.
+template <bool EAGER = false>
 __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     using M = Mma<8, 256, 256, 32, 3>;
     // LDS: the K loop's stages, reused after it as per-wave, per-head staging ([64][72] bf16: Q, K as
@@ -134,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
         const int64_t row = (int64_t)m * T + t;
         if (a0) dt[tb] = p.dots[row * 3 + mat];
         if (ve_on) {
-            tokv[tb] = p.idx[t];
+            tokv[tb] = p.idx[m * p.idx_m + t];
             gt[tb][0] = p.gates[row * 8 + head0];
             gt[tb][1] = p.gates[row * 8 + head0 + 1];
             if (p.ve_r1.a) vesc[tb] = p.ve_r1.a[dir * p.ve_r1.a_stride + tokv[tb]];
@@ -174,6 +178,13 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
                         for (int e = 0; e < 4; ++e) v[half][4 * g + e] += corr * f4get(a4, e);
                     }
             }
+            if constexpr (EAGER) {
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    v[0][r] = bfr(v[0][r]);
+                    v[1][r] = bfr(v[1][r]);
+                }
+            }
             if (ve_on) {
                 // v += gate[row, head] * (ve[idx[t], head*64 + d] (+ lowrank_embed term))   (eggroll.py:85-89);
                 // the gates 2 sigmoid(x[:32] . Wg[head] (+ rank-1)) come precomputed (noise_pop_gate)
@@ -191,7 +202,12 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
                     const int half = q >> 2, g = q & 3;
                     const float4 b4 = ld4(veb + 32 * half + 8 * g + 4 * hf);
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) v[half][4 * g + e] += gate * (f4get(e4[q], e) + ves * f4get(b4, e));
+                    for (int e = 0; e < 4; ++e) {
+                        if constexpr (EAGER)
+                            v[half][4 * g + e] = bfr(v[half][4 * g + e] + bfr(gate * f4get(e4[q], e)));
+                        else
+                            v[half][4 * g + e] += gate * (f4get(e4[q], e) + ves * f4get(b4, e));
+                    }
                 }
             }
             if (mat < 2) {
@@ -207,8 +223,8 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
                         const int r = 4 * g + e;
                         const float c = (float)c4[e], sn = (float)s4[e];
                         const float x1 = v[0][r], x2 = v[1][r];
-                        const float o1 = x1 * c + x2 * sn;
-                        const float o2 = x1 * -sn + x2 * c;
+                        const float o1 = EAGER ? bfr(bfr(x1 * c) + bfr(x2 * sn)) : x1 * c + x2 * sn;
+                        const float o2 = EAGER ? bfr(bfr(x1 * -sn) + bfr(x2 * c)) : x1 * -sn + x2 * c;
                         v[0][r] = o1;
                         v[1][r] = o2;
                         ss += o1 * o1 + o2 * o2;
@@ -293,7 +309,9 @@ struct ResidArgs {
 // MIX: apply the next block's mixing (x0 read); NNEXT: number of next-matrix dots (0..3); JIT: add a
 // per-token jitter to the product. All fixed at compile time so the epilogue's loads carry no per-group
 // branches and can be issued in batches.
-template <int KD, bool MIX, int NNEXT, bool JIT = false>
+// EAGER: the eager forward's roundings (unperturbed, no next dots): y = bf16(xres + bf16(x W^T)) and the
+// mix bf16(bf16(rl * y) + bf16(ml * x0)), so the residual stream stays bf16-valued.
+template <int KD, bool MIX, int NNEXT, bool JIT = false, bool EAGER = false>
 __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     using M = Mma<8, 512, 128, 32, 3>;
     // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
@@ -339,6 +357,11 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
         if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
         if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
     }
+    if constexpr (EAGER) {
+        // eager autocast multiplies a bf16 tensor by the 0-dim fp32 lambdas in bf16: they enter rounded
+        rl = bfr(rl);
+        ml = bfr(ml);
+    }
 
     f32x16 acc[4][2];
     M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, wm0);
@@ -376,8 +399,14 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
                 for (int e = 0; e < 4; ++e) {
                     float prod = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
                     if constexpr (JIT) prod += (float)jv[g][e];
-                    float y = f4get(xv[g], e) + prod;
-                    if constexpr (MIX) y = rl * y + ml * f4get(zv[g], e);
+                    float y;
+                    if constexpr (EAGER) {
+                        y = bfr(f4get(xv[g], e) + bfr(prod));
+                        if constexpr (MIX) y = bfr(bfr(rl * y) + bfr(ml * f4get(zv[g], e)));
+                    } else {
+                        y = f4get(xv[g], e) + prod;
+                        if constexpr (MIX) y = rl * y + ml * f4get(zv[g], e);
+                    }
                     acc[fb][tb][4 * g + e] = y;
                     ssq += y * y;
                 }
@@ -480,7 +509,8 @@ struct FcArgs {
     const __bf16 *jit;        // DUST jitter on the hidden pre-activation (run.py:116), [rows][2048] bf16, or NULL
 };
 
-template <bool JIT = false>
+// EAGER: relu(bf16(x W^T)) squared and rounded (the eager forward; unperturbed calls only)
+template <bool JIT = false, bool EAGER = false>
 __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     using M = Mma<8, 256, 256, 64, 2>;
     constexpr int kMain = cmax(M::LDS_BYTES, 8 * 64 * kStg * 2);  // K loop, then per-wave act staging
@@ -544,6 +574,7 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
                 for (int e = 0; e < 4; ++e) {
                     float y = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
                     if constexpr (JIT) y += (float)jv[e];
+                    if constexpr (EAGER) y = bfr(y);
                     y = y > 0.f ? y * y : 0.f;
                     o[e] = (__bf16)y;
                     pd += (float)o[e] * f4get(b4, e);
@@ -644,6 +675,8 @@ struct HeadArgs {
     float *loss;              // [m][T] per-token CE (0 where target < 0)
 };
 
+// EAGER: logits rounded to bf16 before the soft cap (the autocast head's bf16 output; unperturbed calls only)
+template <bool EAGER = false>
 __global__ __launch_bounds__(kThreads) void head_ce_kernel(HeadArgs p) {
     using M = Mma<8, 256, 256, 64, 2>;
     __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
@@ -680,7 +713,8 @@ __global__ __launch_bounds__(kThreads) void head_ce_kernel(HeadArgs p) {
                 for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const float l = acc[fb][tb][4 * g + e] + corr[tb] * f4get(a4, e);
+                        const float l = EAGER ? bfr(acc[fb][tb][4 * g + e])
+                                              : acc[fb][tb][4 * g + e] + corr[tb] * f4get(a4, e);
                         const float u = exp2_fast(l * k1) + 1.0f;
                         const float ru = __builtin_amdgcn_rcpf(u);
                         sum[tb] += exp2_fast(k2 * ru);
@@ -739,8 +773,12 @@ int check_pop(const noise_population_t *pp, int tile, const char *fn) {
     NOISE_CHECK_ARG(pp->tokens % tile == 0, "%s: tokens (%lld) must be a multiple of %d", fn, (long long)pp->tokens, tile);
     NOISE_CHECK_ARG(pp->dir_div >= 1, "%s: dir_div must be >= 1", fn);
     NOISE_CHECK_ARG(pp->members * pp->tokens < (1ll << 31), "%s: members * tokens must stay below 2^31", fn);
+    NOISE_CHECK_ARG(pp->rounding == NOISE_ROUNDING_FUSED || pp->rounding == NOISE_ROUNDING_EAGER,
+                    "%s: unknown rounding mode %lld", fn, (long long)pp->rounding);
     return NOISE_OK;
 }
+
+bool eager(const noise_population_t *pp) { return pp->rounding == NOISE_ROUNDING_EAGER; }
 
 int check_view(const noise_view_t &v, const char *fn, const char *name) {
     NOISE_CHECK_ARG(v.ptr != nullptr, "%s: %s is NULL", fn, name);
@@ -760,8 +798,13 @@ void launch_resid_mix(const ResidArgs &a, dim3 grid, hipStream_t s) {
 }
 
 template <int KD>
-void launch_resid(const ResidArgs &a, dim3 grid, hipStream_t s) {
-    if (a.mix)
+void launch_resid(const ResidArgs &a, dim3 grid, hipStream_t s, bool eager) {
+    if (eager) {
+        if (a.mix)
+            hipLaunchKernelGGL((resid_kernel<KD, true, 0, false, true>), grid, dim3(kThreads), 0, s, a);
+        else
+            hipLaunchKernelGGL((resid_kernel<KD, false, 0, false, true>), grid, dim3(kThreads), 0, s, a);
+    } else if (a.mix)
         launch_resid_mix<KD, true>(a, grid, s);
     else
         launch_resid_mix<KD, false>(a, grid, s);
@@ -780,8 +823,8 @@ using namespace noise;
 
 extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3],
                              const noise_rank1_t r1[3], const float *dots, const void *rope_cos, const void *rope_sin,
-                             const float *ve, const int64_t *idx, const float *gates, const noise_rank1_t *ve_noise,
-                             void *const out[3], noise_stream_t stream) {
+                             const float *ve, const int64_t *idx, int64_t idx_sm, const float *gates,
+                             const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream) {
     clear_error();
     const char *fn = "noise_pop_qkv";
     NOISE_TRY(check_pop(pop, 256, fn));
@@ -794,6 +837,9 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
                         "%s: perturbed matrix %d needs dots, sign and 16 B aligned a rows", fn, i);
     }
     NOISE_CHECK_ARG(!ve || (idx && gates), "%s: value embeddings need idx and gates", fn);
+    NOISE_CHECK_ARG(idx_sm == 0 || idx_sm >= pop->tokens, "%s: idx_sm must be 0 or >= tokens", fn);
+    NOISE_CHECK_ARG(!eager(pop) || ((!r1 || (!r1[0].a && !r1[1].a && !r1[2].a)) && (!ve_noise || !ve_noise->a)),
+                    "%s: eager rounding is for unperturbed calls", fn);
     QkvArgs a;
     a.pop = make_pop(pop);
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
@@ -803,12 +849,16 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
         a.out[i] = (__bf16 *)out[i];
     }
     a.dots = dots; a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin; a.ve = ve; a.ve_m = 0; a.idx = idx;
+    a.idx_m = idx_sm;
     a.gates = gates;
     a.ve_r1 = make_r1(ve ? ve_noise : nullptr);
     NOISE_CHECK_ARG(!a.ve_r1.a || (pop->sign && aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
                     "%s: value-embedding noise b rows must be 16 B aligned", fn);
     dim3 grid((unsigned)(6 * pop->members * (pop->tokens / 256)));
-    hipLaunchKernelGGL(qkv_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    if (eager(pop))
+        hipLaunchKernelGGL(qkv_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(qkv_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 
@@ -831,6 +881,8 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     NOISE_CHECK_ARG(!r1 || !r1->a || (dots && pop->sign && dots_count >= 1 && aligned(r1->a, 16) && r1->a_stride % 4 == 0),
                     "%s: perturbation needs dots, sign and 16 B aligned a rows", fn);
     NOISE_CHECK_ARG(!(eps_r || eps_x) || pop->sign, "%s: mixing-scalar noise needs sign", fn);
+    NOISE_CHECK_ARG(!eager(pop) || ((!r1 || !r1->a) && !eps_r && !eps_x && nnext == 0 && !split3),
+                    "%s: eager rounding is for unperturbed calls with a bf16 head input", fn);
     ResidArgs a;
     a.pop = make_pop(pop);
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
@@ -853,9 +905,9 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     }
     dim3 grid((unsigned)(pop->members * (pop->tokens / 128)));
     if (K == 512)
-        launch_resid<512>(a, grid, (hipStream_t)stream);
+        launch_resid<512>(a, grid, (hipStream_t)stream, eager(pop));
     else
-        launch_resid<2048>(a, grid, (hipStream_t)stream);
+        launch_resid<2048>(a, grid, (hipStream_t)stream, eager(pop));
     return launch_status(fn);
 }
 
@@ -885,7 +937,12 @@ extern "C" int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const
     a.pdots = a.nb ? partial_dots : nullptr;
     a.jit = nullptr;
     dim3 grid((unsigned)(8 * pop->members * (pop->tokens / 256)));
-    hipLaunchKernelGGL(fc_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    if (eager(pop)) {
+        NOISE_CHECK_ARG((!r1 || !r1->a) && !a.nb, "%s: eager rounding is for unperturbed calls", fn);
+        hipLaunchKernelGGL((fc_kernel<false, true>), grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    } else {
+        hipLaunchKernelGGL(fc_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    }
     return launch_status(fn);
 }
 
@@ -922,6 +979,7 @@ extern "C" int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, 
     NOISE_CHECK_ARG(K > 0 && K % 64 == 0 && vocab > 0 && vocab % 256 == 0, "%s: K multiple of 64, vocab of 256", fn);
     NOISE_CHECK_ARG(w && aligned(w, 16) && targets && token_loss, "%s: NULL w/targets/loss", fn);
     NOISE_CHECK_ARG(!r1 || !r1->a || (dots && pop->sign), "%s: perturbation needs dots and sign", fn);
+    NOISE_CHECK_ARG(!eager(pop) || ((!r1 || !r1->a) && K == 512), "%s: eager rounding is for the unperturbed bf16 head", fn);
     HeadArgs a;
     a.pop = make_pop(pop);
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
@@ -929,7 +987,10 @@ extern "C" int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, 
     a.r1 = make_r1(r1);
     a.dots = dots; a.targets = targets; a.targets_sm = targets_sm; a.loss = token_loss;
     dim3 grid((unsigned)(pop->members * (pop->tokens / 256)));
-    hipLaunchKernelGGL(head_ce_kernel, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    if (eager(pop))
+        hipLaunchKernelGGL(head_ce_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    else
+        hipLaunchKernelGGL(head_ce_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
 
@@ -1076,8 +1137,9 @@ extern "C" int noise_dust_block(const float *x, float *x_out, int64_t sequences,
         for (int i = 0; i < 3; ++i) a.w[i] = (const __bf16 *)w[i];
         a.out[0] = q; a.out[1] = k; a.out[2] = v;
         a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin;
-        a.ve = vef; a.ve_m = tokens * 512; a.idx = iota; a.gates = gates;
-        hipLaunchKernelGGL(qkv_kernel, dim3((unsigned)(6 * sequences * (tokens / 256))), dim3(kThreads), 0, s, a);
+        a.ve = vef; a.ve_m = tokens * 512; a.idx = iota; a.idx_m = 0; a.gates = gates;
+        hipLaunchKernelGGL(qkv_kernel<false>, dim3((unsigned)(6 * sequences * (tokens / 256))), dim3(kThreads), 0, s,
+                           a);
         NOISE_TRY(launch_status(fn));
     }
     // q, k: [N][8][T][64]; v transposed [N][8][64][T]; y token-major [N][T][512]

@@ -27,6 +27,9 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// x rounded to the nearest bf16 (ties to even), as a float
+__device__ __forceinline__ float bfr(float x) { return (float)(__bf16)x; }
+
 __device__ __forceinline__ bf16x8 load_bf16x8(const __bf16 *p) { return *reinterpret_cast<const bf16x8 *>(p); }
 
 __device__ __forceinline__ bf16x4 load_bf16x4(const __bf16 *p) { return *reinterpret_cast<const bf16x4 *>(p); }

@@ -27,9 +27,10 @@ __device__ __forceinline__ void st8(float *p, const float (&v)[8]) {
 // Embedding entry of population_loss (eggroll.py:74-79 for block 0, model.py:196-199):
 //   e = W[idx[t]] (+ sign * a[dir, idx[t]] * b[dir, :])      lowrank_embed, eggroll.py:61-63
 //   x0 = norm(e); x = rl * x0 + ml * x0 (block 0's mix); h = bf16(norm(x))
+// eager: x0, the two products and their sum each rounded to bf16 (the eager autocast forward's bf16 stream).
 // rows = (member or shared, token); grid = rows / 4 workgroups of 4 waves.
 struct EmbedArgs {
-    int rows, tokens, per_member, dir_div;
+    int rows, tokens, per_member, dir_div, eager;
     const float *wte;
     const int64_t *idx;
     const float *sign;
@@ -67,12 +68,22 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs p) {
     float rl = p.lam_r, ml = p.lam_x;
     if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
     if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
+    if (p.eager) {
+        // eager autocast multiplies a bf16 tensor by the 0-dim fp32 lambdas in bf16: they enter rounded
+        rl = bfr(rl);
+        ml = bfr(ml);
+    }
     float x0[8], x[8];
     ss = 0.f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         x0[i] = e[i] * r;
-        x[i] = rl * x0[i] + ml * x0[i];
+        if (p.eager) {
+            x0[i] = bfr(x0[i]);
+            x[i] = bfr(bfr(rl * x0[i]) + bfr(ml * x0[i]));
+        } else {
+            x[i] = rl * x0[i] + ml * x0[i];
+        }
         ss += x[i] * x[i];
     }
     r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
@@ -188,6 +199,9 @@ extern "C" int noise_pop_embed(const noise_population_t *pop, int per_member, co
     NOISE_CHECK_ARG(aligned(wte, 16) && aligned(x0, 16) && aligned(xin, 16) && aligned(h, 16), "%s: 16 B alignment", fn);
     const bool noisy = (emb_noise && emb_noise->a) || eps_r || eps_x;
     NOISE_CHECK_ARG(!noisy || (per_member && pop->sign), "%s: per-member noise needs per_member = 1 and sign", fn);
+    NOISE_CHECK_ARG(pop->rounding == NOISE_ROUNDING_FUSED || pop->rounding == NOISE_ROUNDING_EAGER,
+                    "%s: unknown rounding mode", fn);
+    NOISE_CHECK_ARG(pop->rounding == NOISE_ROUNDING_FUSED || !noisy, "%s: eager rounding is for unperturbed calls", fn);
     EmbedArgs a;
     a.tokens = (int)pop->tokens;
     a.per_member = per_member;
@@ -200,6 +214,7 @@ extern "C" int noise_pop_embed(const noise_population_t *pop, int per_member, co
     a.eb_stride = a.ea ? emb_noise->b_stride : 0;
     a.lam_r = lam_r; a.lam_x = lam_x; a.eps_r = eps_r; a.eps_x = eps_x; a.eps_stride = eps_stride;
     a.x0 = x0; a.xin = xin; a.h = (__bf16 *)h;
+    a.eager = pop->rounding == NOISE_ROUNDING_EAGER;
     hipLaunchKernelGGL(embed_kernel, dim3(rows_grid(a.rows)), dim3(256), 0, (hipStream_t)stream, a);
     return launch_status(fn);
 }
@@ -341,7 +356,8 @@ namespace {
 // (x[:32] . b_g) * a_g[h] for lowrank ve_gate)), one thread per row.
 __global__ __launch_bounds__(256) void gate_kernel(int members, int tokens, int dir_div, const __bf16 *x, int64_t xs_m,
                                                    int64_t xs_t, const float *wg, const float *sign, const float *ga,
-                                                   const float *gb, int64_t ga_stride, int64_t gb_stride, float *out) {
+                                                   const float *gb, int64_t ga_stride, int64_t gb_stride, float *out,
+                                                   int eager) {
     const int64_t row = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (row >= (int64_t)members * tokens) return;
     const int m = (int)(row / tokens), t = (int)(row - (int64_t)m * tokens);
@@ -366,7 +382,8 @@ __global__ __launch_bounds__(256) void gate_kernel(int members, int tokens, int 
 #pragma unroll
         for (int c = 0; c < 32; ++c) z += xf[c] * wg[h * 32 + c];
         if (ga) z += dg * ga[dir * ga_stride + h];
-        out[row * 8 + h] = 2.0f / (1.0f + __expf(-z));
+        // eager: bf16 linear output, bf16 sigmoid, times 2 (exact)
+        out[row * 8 + h] = eager ? 2.0f * bfr(1.0f / (1.0f + __expf(-bfr(z)))) : 2.0f / (1.0f + __expf(-z));
     }
 }
 
@@ -382,10 +399,13 @@ extern "C" int noise_pop_gate(const noise_population_t *pop, noise_view_t x, con
     NOISE_CHECK_ARG(gate_w && gates, "%s: NULL gate weights or output", fn);
     const bool noisy = gate_noise && gate_noise->a;
     NOISE_CHECK_ARG(!noisy || (pop->sign && gate_noise->b), "%s: gate noise needs sign and b", fn);
+    NOISE_CHECK_ARG(pop->rounding == NOISE_ROUNDING_FUSED || (pop->rounding == NOISE_ROUNDING_EAGER && !noisy),
+                    "%s: unknown rounding mode, or eager rounding with gate noise", fn);
     const int64_t rows = pop->members * pop->tokens;
     hipLaunchKernelGGL(gate_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                        (int)pop->members, (int)pop->tokens, (int)pop->dir_div, (const __bf16 *)x.ptr, x.sm, x.st, gate_w,
                        pop->sign, noisy ? gate_noise->a : nullptr, noisy ? gate_noise->b : nullptr,
-                       noisy ? gate_noise->a_stride : 0, noisy ? gate_noise->b_stride : 0, gates);
+                       noisy ? gate_noise->a_stride : 0, noisy ? gate_noise->b_stride : 0, gates,
+                       (int)(pop->rounding == NOISE_ROUNDING_EAGER));
     return launch_status(fn);
 }

@@ -119,7 +119,8 @@ class Weights:
                        o=bf(pre + 'attn.c_proj.weight'), fc=bf(pre + 'mlp.c_fc.weight'),
                        mp=bf(pre + 'mlp.c_proj.weight'))
             if has_ve(i, n_layer):
-                blk['gate'] = g(pre + 'attn.ve_gate.weight').to(F32).contiguous()
+                # the gate's product runs under autocast: its weights enter rounded to bf16
+                blk['gate'] = bf(pre + 'attn.ve_gate.weight').to(F32).contiguous()
                 blk['ve'] = g(f'value_embeds.{i}.weight').to(F32).contiguous()
             self.blocks.append(blk)
         self.windows = window_sizes(n_layer)
@@ -159,22 +160,36 @@ def _zero_b(dev, width):
     return _lib.Rank1(None, z.data_ptr(), 0, 0)
 
 
-def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffers=None):
+def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffers=None, per_token=False,
+                       rounding=_lib.ROUNDING_FUSED):
     """Per-member mean cross-entropy [m] of the perturbed models (eggroll.py:66-103 semantics).
 
     W: Weights. noise: name -> (a [dirs, out], b [dirs, in]) fp32 row views for matrices and embeddings,
     or eps [dirs, L] for 'resid_lambdas' / 'x0_lambdas'; absent names are unperturbed. sign: [m] fp32
     (+-sigma). Member m uses noise row m // dir_div. idx, targets: [T] int64 token ids shared by all
-    members. rope: (cos, sin) bf16 [T][32] rotary tables on the device (default: rotary_tables(T))."""
+    members, or [m, T] with one sequence per member (scoring distinct sequences, utils/eval.py:43-46; the
+    embedding and mixing scalars unperturbed). rope: (cos, sin) bf16 [T][32] rotary tables on the device
+    (default: rotary_tables(T)). per_token: return the [m, T] per-token losses (0 at targets < 0) instead
+    of the member means (a view of the buffers' storage). rounding: ROUNDING_FUSED (the compiled training
+    forward) or ROUNDING_EAGER (the scorer's eager autocast forward, bf16 residual stream; noise must be
+    empty)."""
     dev = W.device
-    m, T = sign.shape[0], idx.shape[0]
+    m, T = sign.shape[0], idx.shape[-1]
     if T % 256:
         raise ValueError(f'sequence length must be a multiple of 256, got {T}')
+    rows_in = idx.dim() == 2
+    if idx.dim() not in (1, 2) or (rows_in and idx.shape[0] != m) or targets.shape != idx.shape:
+        raise ValueError(f'idx and targets must both be [T] or [members, T]; got {tuple(idx.shape)}, '
+                         f'{tuple(targets.shape)} for {m} members')
     sign = sign.to(device=dev, dtype=F32).contiguous()
     idx = idx.to(device=dev, dtype=torch.int64).contiguous()
     targets = targets.to(device=dev, dtype=torch.int64).contiguous()
     stream = _lib.stream_ptr(dev)
-    pop = _lib.Population(m, T, sign.data_ptr(), dir_div)
+    if rounding not in (_lib.ROUNDING_FUSED, _lib.ROUNDING_EAGER):
+        raise ValueError(f'unknown rounding mode {rounding}')
+    if rounding == _lib.ROUNDING_EAGER and (noise or W.fp32_head):
+        raise ValueError('eager rounding is the unperturbed bf16 forward: no noise, no fp32 head')
+    pop = _lib.Population(m, T, sign.data_ptr(), dir_div, rounding)
     popp = ctypes.byref(pop)
     if rope is None:
         cos, sin = rotary_tables(T)
@@ -189,16 +204,22 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
 
     eps_r, eps_x = nz('resid_lambdas'), nz('x0_lambdas')
     emb = nz('transformer.wte.weight')
-    per_member = emb is not None or eps_r is not None or eps_x is not None
+    noisy_entry = emb is not None or eps_r is not None or eps_x is not None
+    if rows_in and noisy_entry:
+        raise ValueError('per-member token rows need the embedding and mixing scalars unperturbed')
+    per_member = noisy_entry or rows_in
     B = buffers if buffers is not None else _Buffers(m, T, dev, W.fp32_head, per_member)
-    # block 0 entry: embedding, norm, mix, norm (shared by every member when nothing there is perturbed)
+    # block 0 entry: embedding, norm, mix, norm (shared by every member when nothing there is perturbed;
+    # per-member token rows go through as one sequence of m * T tokens: the entry is token-local)
     emb_r1 = _rank1(emb)
-    _call('noise_pop_embed', popp, 1 if per_member else 0, W.wte.data_ptr(), idx.data_ptr(),
+    embed_pop = _lib.Population(1, m * T, None, 1, rounding) if rows_in else pop
+    _call('noise_pop_embed', ctypes.byref(embed_pop), 1 if noisy_entry else 0, W.wte.data_ptr(), idx.data_ptr(),
               ctypes.byref(emb_r1), W.resid_lambdas[0], W.x0_lambdas[0],
               None if eps_r is None else eps_r.data_ptr(), None if eps_x is None else eps_x.data_ptr(),
               0 if eps_r is None and eps_x is None else (eps_r if eps_r is not None else eps_x).stride(0),
               B.x0.data_ptr(), B.xin0.data_ptr(), B.h0.data_ptr(), stream)
     sm_e = T * E if per_member else 0
+    idx_sm = T if rows_in else 0
     eps_ptr = lambda e, i: None if e is None else e[:, i].data_ptr()
     eps_stride = (eps_r if eps_r is not None else eps_x).stride(0) if (eps_r is not None or eps_x is not None) else 0
 
@@ -230,7 +251,7 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
             _call('noise_pop_gate', popp, x_in, blk['gate'].data_ptr(), ctypes.byref(gate_r1), B.gates.data_ptr(),
                   stream)
         _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
-              sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(),
+              sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(), idx_sm,
               B.gates.data_ptr() if 've' in blk else None, ctypes.byref(ve_r1), qkv_out, stream)
         # attention; its epilogue also forms y . b_o per head for c_proj's rank-1 term
         no = nz(pre + 'attn.c_proj.weight')
@@ -285,7 +306,9 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     else:
         hx, hw, K = _view(B.h, T * E, E), W.lm_head, E
     _call('noise_pop_head_ce', popp, hx, hw.data_ptr(), K, VOCAB, ctypes.byref(head_r1), B.d_head.data_ptr(),
-              targets.data_ptr(), 0, B.loss_tok.data_ptr(), stream)
+              targets.data_ptr(), idx_sm, B.loss_tok.data_ptr(), stream)
+    if per_token:
+        return B.loss_tok.view(m, T)
     out = torch.empty(m, dtype=F32, device=dev)
     _call('noise_member_mean', B.loss_tok.data_ptr(), m, T, out.data_ptr(), stream)
     return out

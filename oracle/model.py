@@ -5,6 +5,8 @@ Follows, in plain fp32 torch CPU ops (no autocast, no flex_attention):
   utils/model.py:46-58   norm (rms_norm, eps = finfo(fp32).eps), has_ve, apply_rotary_emb
   utils/model.py:177-191 rotary tables (fp32 freqs -> cos/sin rounded to bf16), window sizes
   utils/model.py:193-209 GPT.forward (mix scalars, blocks, final norm, head, softcap 15, cross-entropy)
+  utils/eval.py:43-46    the scorer's forward: GPT.forward run eagerly under bf16 autocast with the bf16
+                         embeddings of model.py:170-174 (gpt_forward_eager: every op's result rounded)
   utils/model.py:81-120  CausalSelfAttention / MLP / Block forward
   train/val/eggroll.py:56-103 lowrank, lowrank_embed, population_loss
   train/val/run.py:89-94  head_loss (final norm, fp32 head, softcap, per-token CE)
@@ -104,6 +106,52 @@ def gpt_forward(P, idx, targets=None, reduction='mean'):
         x = _block(P, i, x, ve, cos, sin, windows[i])
     x = norm(x)
     logits = (x @ P['lm_head.weight'].t())[..., :VOCAB].float()
+    if targets is None:
+        return SOFTCAP * torch.tanh(logits / SOFTCAP)
+    return softcap_ce(logits, targets, reduction)
+
+
+def bf16(t):
+    """t rounded to the nearest bf16 (ties to even), as fp32."""
+    return t.bfloat16().float()
+
+
+def gpt_forward_eager(P, idx, targets=None, reduction='mean'):
+    """The scorer's forward (eval.py:43-46 over model.py:193-209, 81-120): eager, under bf16 autocast, with
+    the token and value embeddings stored in bf16. Every op's result is rounded to bf16 as eager autocast
+    does: linear outputs (weights cast to bf16, fp32 sums), rms_norm of a bf16 input (fp32 inside), each
+    product and sum of the mix (model.py:197, the fp32 lambdas entering as bf16), the rotary products and sums (model.py:55-58), the value
+    gate's sigmoid and products (model.py:90-92), attention's output (fp32 inside), the residual adds
+    (model.py:119-120) and ReLU's square (model.py:107). The logits leave the head as bf16 and are capped
+    and scored in fp32 (model.py:203-209). Computation in fp32 with explicit rounding."""
+    B, T = idx.shape
+    cos, sin = rotary_tables(T)
+    c, s = cos[None, :, None, :], sin[None, :, None, :]
+    windows = window_sizes()
+    lin = lambda x, name: bf16(x @ bf16(P[name]).t())
+
+    def rotary(u):
+        u1, u2 = u[..., :HEAD_DIM // 2], u[..., HEAD_DIM // 2:]
+        return torch.cat([bf16(bf16(u1 * c) + bf16(u2 * s)), bf16(bf16(u1 * -s) + bf16(u2 * c))], 3)
+
+    x = x0 = bf16(norm(bf16(P['transformer.wte.weight'])[idx]))
+    for i in range(N_LAYER):
+        pre = f'transformer.h.{i}.'
+        # a 0-dim fp32 tensor times a bf16 tensor computes in bf16: the scalar is rounded first
+        rl, ml = bf16(P['resid_lambdas'][i]), bf16(P['x0_lambdas'][i])
+        x = bf16(bf16(rl * x) + bf16(ml * x0))
+        h = bf16(norm(x))
+        q, k, v = (lin(h, pre + f'attn.c_{n}.weight').view(B, T, N_HEAD, HEAD_DIM) for n in 'qkv')
+        if has_ve(i):
+            ve = bf16(P[f'value_embeds.{i}.weight'])[idx].view(B, T, N_HEAD, HEAD_DIM)
+            gate = bf16(2 * bf16(torch.sigmoid(lin(h[..., :32], pre + 'attn.ve_gate.weight'))))
+            v = bf16(v + bf16(gate.unsqueeze(-1) * ve))
+        q, k = bf16(norm(rotary(q))), bf16(norm(rotary(k)))
+        y = bf16(attention(q, k, v, windows[i])).reshape(B, T, N_EMBD)
+        x = bf16(x + lin(y, pre + 'attn.c_proj.weight'))
+        hidden = lin(bf16(norm(x)), pre + 'mlp.c_fc.weight')
+        x = bf16(x + lin(bf16(F.relu(hidden).square()), pre + 'mlp.c_proj.weight'))
+    logits = lin(bf16(norm(x)), 'lm_head.weight')[..., :VOCAB]
     if targets is None:
         return SOFTCAP * torch.tanh(logits / SOFTCAP)
     return softcap_ce(logits, targets, reduction)
