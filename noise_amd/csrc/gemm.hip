@@ -313,14 +313,20 @@ struct ResidArgs {
 // mix bf16(bf16(rl * y) + bf16(ml * x0)), so the residual stream stays bf16-valued.
 template <int KD, bool MIX, int NNEXT, bool JIT = false, bool EAGER = false>
 __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
-    using M = Mma<8, 512, 128, 32, 3>;
-    // LDS after the K loop: per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the
-    // hi/lo rows of the split3 output), then the per-token statistics [128 tokens][4 feature waves][4];
-    // above both, the a vector and up to three next b vectors (512 floats each), copied before the K loop.
+    using M = Mma<8, 512, 128, 64, 2>;
+    static_assert(KD % 128 == 0, "an even number of K stages: the last one runs in slot 1");
+    // LDS: the K loop's two stages of 80 KiB fill all 160 KiB. During the last stage (slot 1) slot 0 is free
+    // and takes the a vector and up to three next b vectors (512 floats each, at 72 KiB). After the loop:
+    // per-wave staging of 17 KiB (fp32 [32 tokens][136], or bf16 [64][136] for the hi/lo rows of the split3
+    // output) for waves 0-3 below the vectors and waves 4-7 above them, then the per-token statistics
+    // [128 tokens][4 feature waves][4].
     constexpr int kStgF = 136;
-    constexpr int kEpi = 8 * 32 * kStgF * 4 + 128 * 4 * 4 * 4;
-    constexpr int kMain = cmax(M::LDS_BYTES, kEpi);
-    constexpr int kLds = kMain + 4 * 512 * 4;
+    constexpr int kStgBytes = 32 * kStgF * 4;
+    constexpr int kVecOff = 72 * 1024, kVecBytes = 4 * 512 * 4;
+    constexpr int kRedOff = kVecOff + kVecBytes + 4 * kStgBytes;
+    constexpr int kLds = M::LDS_BYTES;
+    static_assert(4 * kStgBytes <= kVecOff && kVecOff + kVecBytes <= M::STAGE, "vectors within free slot 0");
+    static_assert(kRedOff + 128 * 4 * 4 * 4 <= kLds, "epilogue layout fits");
     static_assert(32 * kStgF * 4 >= 64 * kStg * 2, "bf16 split3 staging must fit the wave's region");
     __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
@@ -330,11 +336,12 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     const int wn0 = M::wn0(wave), wm0 = M::wm0(wave), wq = wave % 4;
     const int dir = m / p.pop.dir_div;
 
-    // epilogue inputs fetched ahead of the K loop: the per-feature vectors by direct copy into LDS (wave
-    // 2v + h copies half h of vector v; the K loop's waits and barriers cover them), the per-token rank-1
-    // dot sums and the mixing scalars into registers
-    float *vec = reinterpret_cast<float *>(reinterpret_cast<char *>(lds) + kMain);
-    {
+    // epilogue inputs: the per-feature vectors by direct copy into LDS during the last K stage (wave
+    // 2v + h copies half h of vector v; the K loop waits for them before its final barrier), the per-token
+    // rank-1 dot sums and the mixing scalars into registers ahead of the K loop
+    char *ldsb = reinterpret_cast<char *>(lds);
+    float *vec = reinterpret_cast<float *>(ldsb + kVecOff);
+    auto copy_vectors = [&]() {
         const int v = wave >> 1, h = wave & 1;
         const float *src = v == 0 ? (p.r1.a ? p.r1.a + dir * p.r1.a_stride : nullptr)
                                   : (v - 1 < NNEXT ? p.nb[v - 1] + dir * p.nb_stride[v - 1] : nullptr);
@@ -342,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
             lds_dma16(src + 256 * h, lane * 16, vec + 512 * v + 256 * h);
         else if (v == 0)
             st4(vec + 256 * h + 4 * lane, float4{0.f, 0.f, 0.f, 0.f});  // no perturbation: a = 0
-    }
+    };
     const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;  // unperturbed calls may pass no signs
     float dsum[2] = {0.f, 0.f};
     if (p.r1.a) {
@@ -364,11 +371,11 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
     }
 
     f32x16 acc[4][2];
-    M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, wm0);
+    M::run(p.w, KD, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, KD, lds, acc, tid, wn0, wm0, copy_vectors);
 
-    float *stgf = reinterpret_cast<float *>(lds) + wave * 32 * kStgF;
+    float *stgf = reinterpret_cast<float *>(ldsb + (wave < 4 ? wave * kStgBytes : kVecOff + kVecBytes + (wave - 4) * kStgBytes));
     __bf16 *stgb = reinterpret_cast<__bf16 *>(stgf);
-    float *red = reinterpret_cast<float *>(lds) + 8 * 32 * kStgF;
+    float *red = reinterpret_cast<float *>(ldsb + kRedOff);
 
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {

@@ -21,7 +21,14 @@ __device__ __forceinline__ float f4get(const float4 &v, int e) { return e == 0 ?
 // k-step are read while the current step's MFMAs run; the wait for stage ks + 1 and the workgroup
 // barrier sit just before the read that crosses into it, and the stage just finished is refilled with
 // stage ks + NS right after that barrier. Ends with a barrier: the LDS may be reused at once.
+// Optional tail (callers with K >= 2 BK): called once by every wave right after the barrier that precedes
+// the last stage, when every slot but the last stage's ((K / BK - 1) % NS) is free for good; it may issue
+// copies into those slots (the loop then waits for all of a wave's copies before its final barrier).
 // ------------------------------------------------------------------------------------------------
+struct NoTail {
+    __device__ void operator()() const {}
+};
+
 template <int NW, int BN, int BM, int BK, int NS>
 struct Mma {
     static constexpr int WN = BN / 128;
@@ -46,8 +53,10 @@ struct Mma {
 
     // W: BN rows of stride ldw; X: BM rows of stride ldx (elements, multiples of 8; 16 B aligned bases);
     // K a multiple of BK
+    template <class Tail = NoTail>
     __device__ static void run(const __bf16 *W, int64_t ldw, const __bf16 *X, int64_t ldx, int K, void *lds_v,
-                               f32x16 (&acc)[4][2], int tid, int wn, int wm) {
+                               f32x16 (&acc)[4][2], int tid, int wn, int wm, Tail tail = Tail{}) {
+        constexpr bool kTail = !__is_same(Tail, NoTail);
         char *lds = static_cast<char *>(lds_v);
         const int lane = tid & 63, j = lane & 31, hf = lane >> 5;
         const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: copy targets stay scalar
@@ -110,6 +119,9 @@ struct Mma {
                     __syncthreads();
                     // every wave has read its last fragments of stage ks: its buffer takes stage ks + NS
                     if (ks + NS < nk) issue(ks + NS);
+                    if constexpr (kTail) {
+                        if (ks + 2 == nk) tail();
+                    }
                     fetch(cur ^ 1, lds + ((ks + 1) % NS) * STAGE, 0);
                 }
 #pragma unroll
@@ -118,6 +130,7 @@ struct Mma {
                     for (int tb = 0; tb < 2; ++tb) acc[fb][tb] = mfma32x32x16(fa[cur][fb], fx[cur][tb], acc[fb][tb]);
             }
         }
+        if constexpr (kTail) vm_wait<0>();  // the tail's copies
         __syncthreads();
     }
 };
