@@ -81,15 +81,18 @@ __device__ __forceinline__ int rope_off(int row, int chunk) { return row * 64 + 
 // calls only): q, k, v rounded as linear outputs, v + bf16(gate * ve), rotary products and sums rounded.
 template <bool EAGER = false>
 __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
-    using M = Mma<8, 256, 256, 32, 3>;
-    // LDS: the K loop's stages, reused after it as per-wave, per-head staging ([64][72] bf16: Q, K as
-    // tokens x dims, V^T as dims x tokens); above them the tile's rotary rows (cos then sin) and the a and
-    // value-embedding b vectors, all copied before the K loop
+    using M = Mma<8, 256, 256, 64, 2>;
+    // LDS: the K loop's two stages of 64 KiB. During the last stage (slot 1) slot 0 takes the tile's rotary
+    // rows (cos then sin, 32 KiB) and the a and value-embedding b vectors (2 KiB); after the loop, per-wave,
+    // per-head staging ([64][72] bf16: Q, K as tokens x dims, V^T as dims x tokens) follows them.
     constexpr int kStgH = 72;
     constexpr int kWaveStg = 64 * kStgH;
-    constexpr int kMain = cmax(M::LDS_BYTES, 8 * kWaveStg * 2);
     constexpr int kRope = 2 * 256 * 64;
-    constexpr int kLds = kMain + kRope + 2 * 256 * 4;
+    constexpr int kVec = 2 * 256 * 4;
+    constexpr int kStgOff = kRope + kVec;
+    static_assert(kStgOff <= M::STAGE, "rotary rows and vectors within free slot 0");
+    static_assert(kStgOff + 8 * kWaveStg * 2 <= M::LDS_BYTES, "staging within the stages");
+    constexpr int kLds = M::LDS_BYTES;
     __shared__ __attribute__((aligned(16))) __bf16 lds[kLds / 2];
     const int T = p.pop.tokens;
     const int tiles_t = T / 256;
@@ -104,32 +107,34 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
     const int head0 = (nl0 + wn0) / 64;
     const bool ve_on = mat == 2 && p.ve;
 
-    // epilogue inputs fetched ahead of the K loop (its waits and barriers cover the copies): rotary rows and
-    // per-feature vectors by direct copy into LDS, per-token scalars into registers
-    char *rope = reinterpret_cast<char *>(lds) + kMain;
+    // epilogue inputs: rotary rows and per-feature vectors by direct copy into LDS during the last K stage
+    // (the K loop waits for them before its final barrier), per-token scalars into registers ahead of it
+    char *rope = reinterpret_cast<char *>(lds);
     float *vec = reinterpret_cast<float *>(rope + kRope);
-    if (mat < 2) {
-        // 32 copies of 16 rows (1 KiB): copy i covers rows 16 (i % 16) .. of table i / 16; lane l fetches
-        // row 16 (i % 16) + l / 4, chunk (l % 4) ^ (l / 16) (the row's swizzle, rows 16 apart share it)
-        const int chunk = (lane & 3) ^ (lane >> 4);
-        const unsigned off = (unsigned)((lane >> 2) * 64 + chunk * 16);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int i = 8 * k + wave;
-            const __bf16 *tab = i < 16 ? p.cos_t : p.sin_t;
-            lds_dma16(tab + (int64_t)(t0 + 16 * (i & 15)) * 32, off, rope + i * 1024);
-        }
-    }
     const float *a0 = r1.a ? r1.a + dir * r1.a_stride + nl0 : nullptr;
     const float *vb0 = ve_on && p.ve_r1.a ? p.ve_r1.b + dir * p.ve_r1.b_stride + nl0 : nullptr;
-    // (an absent vector reads as zeros, so the epilogue needs no branches)
-    if (wave < 2) {
-        const float *src = wave == 0 ? a0 : vb0;
-        if (src)
-            lds_dma16(src, lane * 16, vec + 256 * wave);
-        else
-            st4(vec + 256 * wave + 4 * lane, float4{0.f, 0.f, 0.f, 0.f});
-    }
+    auto copy_inputs = [&]() {
+        if (mat < 2) {
+            // 32 copies of 16 rows (1 KiB): copy i covers rows 16 (i % 16) .. of table i / 16; lane l fetches
+            // row 16 (i % 16) + l / 4, chunk (l % 4) ^ (l / 16) (the row's swizzle, rows 16 apart share it)
+            const int chunk = (lane & 3) ^ (lane >> 4);
+            const unsigned off = (unsigned)((lane >> 2) * 64 + chunk * 16);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int i = 8 * k + wave;
+                const __bf16 *tab = i < 16 ? p.cos_t : p.sin_t;
+                lds_dma16(tab + (int64_t)(t0 + 16 * (i & 15)) * 32, off, rope + i * 1024);
+            }
+        }
+        // (an absent vector reads as zeros, so the epilogue needs no branches)
+        if (wave < 2) {
+            const float *src = wave == 0 ? a0 : vb0;
+            if (src)
+                lds_dma16(src, lane * 16, vec + 256 * wave);
+            else
+                st4(vec + 256 * wave + 4 * lane, float4{0.f, 0.f, 0.f, 0.f});
+        }
+    };
     float dt[2] = {0.f, 0.f}, gt[2][2] = {{0.f, 0.f}, {0.f, 0.f}}, vesc[2] = {0.f, 0.f};
     int64_t tokv[2] = {0, 0};
 #pragma unroll
@@ -147,12 +152,12 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
 
     f32x16 acc[4][2];
     M::run(p.w[mat] + (int64_t)nl0 * 512, 512, p.x + m * p.xs_m + (int64_t)t0 * p.xs_t, p.xs_t, 512, lds, acc, tid,
-           wn0, wm0);
+           wn0, wm0, copy_inputs);
 
     const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;  // unperturbed calls may pass no signs
     const float *arow = vec + wn0;  // zeros when unperturbed
     __bf16 *outm = p.out[mat];
-    __bf16 *stg = lds + wave * kWaveStg;
+    __bf16 *stg = lds + kStgOff / 2 + wave * kWaveStg;
 
     // one head at a time: its two token blocks (32 accumulators each, copied out with static indices so
     // the body is compiled once and only one block's values are live), staged, then stored
