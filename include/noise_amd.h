@@ -181,6 +181,16 @@ int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *con
                   const int64_t *idx, int64_t idx_sm, const float *gates, const noise_rank1_t *ve_noise,
                   void *const out[3], noise_stream_t stream);
 
+/* noise_pop_qkv for an input every member shares (block 0 of the population when the embedding and the
+ * mixing scalars are unperturbed; no value embeddings): base = x [c_q; c_k; c_v]^T, fp32 [tokens][1536],
+ * computed once by the caller (noise_pop_linear with one member), then per member base + sign * dots[row*3 +
+ * i] * a_i, rotary and per-head RMSNorm on Q and K. Same outputs as noise_pop_qkv (16 B aligned); tokens a
+ * multiple of 64; fused rounding only. No counterpart in the reference beyond eggroll.py:81-90 itself: the
+ * shared product is this library's restructuring of the same arithmetic. */
+int noise_pop_qkv_shared(const noise_population_t *pop, const float *base, const noise_rank1_t r1[3],
+                         const float *dots, const void *rope_cos, const void *rope_sin, void *const out[3],
+                         noise_stream_t stream);
+
 /* Residual writer (eggroll.py:92 attn.c_proj and :93 mlp.c_proj): y = xres + x w^T + sign * (sum of
  * dots_count dots at dots[row*dots_stride]) * a; if mix: y = rl*y + ml*x0 (the next block's mixing,
  * eggroll.py:79, lambdas + sign * eps); xout = y (fp32, may be NULL); hout = bf16(norm(y)) [m][T][512]

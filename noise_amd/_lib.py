@@ -28,6 +28,7 @@ SIGNATURES = {
     'noise_member_dots': [_p, 'View', _i64, _p, _i64, _p, _p],
     'noise_pop_qkv': [_p, 'View', _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p],
     'noise_pop_gate': [_p, 'View', _p, _p, _p, _p],
+    'noise_pop_qkv_shared': [_p, _p, _p, _p, _p, _p, _p, _p],
     'noise_pop_residual': [_p, 'View', _p, _i64, _p, _p, _i64, _i64, 'View', _p, _i32, _f32, _f32, _p, _p,
                            _i64, 'View', _p, _i32, _p, _i64, _p, _p],
     'noise_pop_fc': [_p, 'View', _p, _p, _p, _p, _p, _p, _p],

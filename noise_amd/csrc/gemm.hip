@@ -277,6 +277,99 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
 }
 
 // ------------------------------------------------------------------------------------------------
+// Q, K, V of a block whose input every member shares (block 0 of the population when the embedding and
+// mixing scalars are unperturbed): the product base = x [c_q; c_k; c_v]^T is the same for all members
+// (fp32 [T][1536], computed once), so each member's Q, K, V are base + sign * dot * a (eggroll.py:58) then
+// rotary and per-head RMSNorm on Q and K (eggroll.py:90, model.py:55-58, 46-47), as qkv_kernel's epilogue
+// computes them (no value embedding). An HBM-write stream instead of a per-member GEMM.
+// Workgroup = (64-token tile, head, member), members fastest so a tile's base rows stay in L2; 256
+// threads: token tl = tid / 4, part = tid % 4 holds dims 8 part .. +8 of both rotary halves.
+// ------------------------------------------------------------------------------------------------
+struct QkvSharedArgs {
+    Pop pop;
+    const float *base;                // [T][1536]
+    Rank1 r1[3];
+    const float *dots;                // [rows][3]
+    const __bf16 *cos_t, *sin_t;      // [T][32]
+    __bf16 *out[3];                   // q, k: [m][8][T][64]; v transposed: [m][8][64][T]
+};
+
+__global__ __launch_bounds__(256) void qkv_shared_kernel(QkvSharedArgs p) {
+    __shared__ __attribute__((aligned(16))) __bf16 vt[64][72];  // V^T tile [dim][token]
+    const int M = p.pop.members, T = p.pop.tokens;
+    const int m = blockIdx.x % M, th = blockIdx.x / M, h = th % 8, t0 = (th / 8) * 64;
+    const int tid = threadIdx.x, tl = tid >> 2, part = tid & 3, t = t0 + tl;
+    const int64_t row = (int64_t)m * T + t;
+    const int dir = m / p.pop.dir_div;
+    const float sgn = p.pop.sign ? p.pop.sign[m] : 0.f;
+    const float *brow = p.base + (int64_t)t * 1536 + h * 64;
+    const int64_t hrow = ((int64_t)m * 8 + h) * T + t;  // row of Q, K [m][h][t]
+#pragma unroll
+    for (int mat = 0; mat < 3; ++mat) {
+        // dims d = 8 part + i (first half) and 32 + 8 part + i (second half), i < 8
+        float x1[8], x2[8];
+        const float *b = brow + mat * 512 + 8 * part;
+        const float4 u0 = ld4(b), u1 = ld4(b + 4), w0 = ld4(b + 32), w1 = ld4(b + 36);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            x1[e] = f4get(u0, e); x1[4 + e] = f4get(u1, e);
+            x2[e] = f4get(w0, e); x2[4 + e] = f4get(w1, e);
+        }
+        const Rank1 r = p.r1[mat];
+        if (r.a) {
+            const float corr = sgn * p.dots[row * 3 + mat];
+            const float *a = r.a + dir * r.a_stride + h * 64 + 8 * part;
+            const float4 a0 = ld4(a), a1 = ld4(a + 4), c0 = ld4(a + 32), c1 = ld4(a + 36);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                x1[e] += corr * f4get(a0, e); x1[4 + e] += corr * f4get(a1, e);
+                x2[e] += corr * f4get(c0, e); x2[4 + e] += corr * f4get(c1, e);
+            }
+        }
+        if (mat < 2) {
+            const bf16x8 c8 = load_bf16x8(p.cos_t + (int64_t)t * 32 + 8 * part);
+            const bf16x8 s8 = load_bf16x8(p.sin_t + (int64_t)t * 32 + 8 * part);
+            float ss = 0.f;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float c = (float)c8[i], sn = (float)s8[i];
+                const float o1 = x1[i] * c + x2[i] * sn;
+                const float o2 = x1[i] * -sn + x2[i] * c;
+                x1[i] = o1;
+                x2[i] = o2;
+                ss += o1 * o1 + o2 * o2;
+            }
+            ss += __shfl_xor(ss, 1, 64);
+            ss += __shfl_xor(ss, 2, 64);
+            const float rstd = rsqrtf(ss * (1.0f / 64.0f) + kEps);
+            bf16x8 lo, hi;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                lo[i] = (__bf16)(x1[i] * rstd);
+                hi[i] = (__bf16)(x2[i] * rstd);
+            }
+            __bf16 *o = p.out[mat] + hrow * 64;
+            store_bf16x8(o + 8 * part, lo);
+            store_bf16x8(o + 32 + 8 * part, hi);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                vt[8 * part + i][tl] = (__bf16)x1[i];
+                vt[32 + 8 * part + i][tl] = (__bf16)x2[i];
+            }
+        }
+    }
+    __syncthreads();
+    // V^T rows [m][h][d][t0 .. t0 + 64): 64 rows of 128 B, 8 chunks of 16 B each
+    __bf16 *ov = p.out[2] + ((int64_t)m * 8 + h) * 64 * T + t0;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int c = it * 256 + tid, d = c >> 3, ch = c & 7;
+        store_bf16x8(ov + (int64_t)d * T + ch * 8, load_bf16x8(&vt[d][ch * 8]));
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // Residual writers (attn.c_proj, mlp.c_proj; N = 512, whole rows per workgroup):
 //   y = xres + (x W^T + sign * dot * a)        [+ mix: y = rl * y + ml * x0 for the next block]
 //   write y (fp32) if xout; h = RMSNorm(y) as bf16 (or its [hi | lo | hi] bf16 split for the fp32 head);
@@ -871,6 +964,35 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
         hipLaunchKernelGGL(qkv_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     else
         hipLaunchKernelGGL(qkv_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    return launch_status(fn);
+}
+
+extern "C" int noise_pop_qkv_shared(const noise_population_t *pop, const float *base, const noise_rank1_t r1[3],
+                                    const float *dots, const void *rope_cos, const void *rope_sin, void *const out[3],
+                                    noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_qkv_shared";
+    NOISE_TRY(check_pop(pop, 64, fn));
+    NOISE_CHECK_ARG(!eager(pop), "%s: eager rounding has per-member inputs; use noise_pop_qkv", fn);
+    NOISE_CHECK_ARG(base && aligned(base, 16), "%s: base must be a 16 B aligned [tokens][1536] fp32 array", fn);
+    NOISE_CHECK_ARG(out && rope_cos && rope_sin && aligned(rope_cos, 16) && aligned(rope_sin, 16),
+                    "%s: NULL output, or rotary tables not 16 B aligned", fn);
+    NOISE_CHECK_ARG(pop->members * 8 * (pop->tokens / 64) < (1ll << 31), "%s: too many workgroups", fn);
+    QkvSharedArgs a;
+    a.pop = make_pop(pop);
+    a.base = base;
+    for (int i = 0; i < 3; ++i) {
+        NOISE_CHECK_ARG(out[i] && aligned(out[i], 16), "%s: output %d NULL or not 16 B aligned", fn, i);
+        NOISE_CHECK_ARG(!r1 || !r1[i].a || (dots && pop->sign && aligned(r1[i].a, 16) && r1[i].a_stride % 4 == 0),
+                        "%s: perturbed matrix %d needs dots, sign and 16 B aligned a rows", fn, i);
+        a.r1[i] = make_r1(r1 ? &r1[i] : nullptr);
+        a.out[i] = (__bf16 *)out[i];
+    }
+    a.dots = dots;
+    a.cos_t = (const __bf16 *)rope_cos;
+    a.sin_t = (const __bf16 *)rope_sin;
+    hipLaunchKernelGGL(qkv_shared_kernel, dim3((unsigned)(pop->members * 8 * (pop->tokens / 64))), dim3(256), 0,
+                       (hipStream_t)stream, a);
     return launch_status(fn);
 }
 

@@ -139,6 +139,8 @@ class _Buffers:
         self.y = torch.empty(m, T, N_EMBD, dtype=BF16, device=dev)
         self.act = torch.empty(m, T, 4 * N_EMBD, dtype=BF16, device=dev)
         self.h3 = torch.empty(m, T, 3 * N_EMBD, dtype=BF16, device=dev) if fp32_head else None
+        # block 0's shared q/k/v product when every member reads the same block input
+        self.qkv_base = None if per_member else torch.empty(T, 3 * N_EMBD, dtype=F32, device=dev)
         self.d_qkv = torch.empty(rows, 3, dtype=F32, device=dev)
         self.d_attn = torch.empty(rows, N_HEAD, dtype=F32, device=dev)
         self.d_fc = torch.empty(rows, dtype=F32, device=dev)
@@ -250,9 +252,19 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
             gate_r1 = _rank1(nz(pre + 'attn.ve_gate.weight'))
             _call('noise_pop_gate', popp, x_in, blk['gate'].data_ptr(), ctypes.byref(gate_r1), B.gates.data_ptr(),
                   stream)
-        _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
-              sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(), idx_sm,
-              B.gates.data_ptr() if 've' in blk else None, ctypes.byref(ve_r1), qkv_out, stream)
+        if i == 0 and B.qkv_base is not None and 've' not in blk and rounding == _lib.ROUNDING_FUSED:
+            # every member reads the same block input: its product with c_q, c_k, c_v is computed once and
+            # each member adds its rank-1 terms before rotary and norm
+            one = _lib.Population(1, T, None, 1, _lib.ROUNDING_FUSED)
+            for j in range(3):
+                _call('noise_pop_linear', ctypes.byref(one), x_in, ws[j], E, E, None, None,
+                      B.qkv_base.data_ptr() + 4 * E * j, 1, T * 3 * E, 3 * E, stream)
+            _call('noise_pop_qkv_shared', popp, B.qkv_base.data_ptr(), _rank1_array(nq), B.d_qkv.data_ptr(),
+                  cos_t.data_ptr(), sin_t.data_ptr(), qkv_out, stream)
+        else:
+            _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
+                  sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(), idx_sm,
+                  B.gates.data_ptr() if 've' in blk else None, ctypes.byref(ve_r1), qkv_out, stream)
         # attention; its epilogue also forms y . b_o per head for c_proj's rank-1 term
         no = nz(pre + 'attn.c_proj.weight')
         q4, k4 = (B.qkv[j].transpose(1, 2) for j in range(2))  # [m, T, H, D] views of [m, H, T, D]
