@@ -680,10 +680,12 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
                     float y = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
                     if constexpr (JIT) y += (float)jv[e];
                     if constexpr (EAGER) y = bfr(y);
-                    y = y > 0.f ? y * y : 0.f;
-                    o[e] = (__bf16)y;
-                    pd += (float)o[e] * f4get(b4, e);
+                    y = fmaxf(y, 0.f);
+                    o[e] = (__bf16)(y * y);
                 }
+                // act . b with both in bf16, as the reference's autocast x @ b (eggroll.py:58) multiplies them
+                pd = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{o[0], o[1]}, bf16x2{(__bf16)b4.x, (__bf16)b4.y}, pd, false);
+                pd = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{o[2], o[3]}, bf16x2{(__bf16)b4.z, (__bf16)b4.w}, pd, false);
                 store_bf16x4(stg + (32 * tb + j) * kStg + f, o);
             }
         if (p.pdots) {
