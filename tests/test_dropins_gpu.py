@@ -121,3 +121,51 @@ def test_custom_ops_compile_without_graph_breaks():
     q, k, v = (torch.randn(1, 256, 8, 64, generator=g).bfloat16().to(DEV) for _ in range(3))
     compiled = torch.compile(f, fullgraph=True, backend='aot_eager')
     assert torch.equal(compiled(q, k, v), f(q, k, v))
+
+
+def test_config3_antithetic_linear_full_size():
+    """The antithetic perturbed linear at full size: X bf16 [2048, 512] ~ N(0, 1) and W bf16 [2048 out,
+    512 in] ~ N(0, 0.02^2) from one CPU generator seeded 0 (X drawn first); 256 pairs (512 members),
+    sigma = 1e-3; a [2048], b [512] per pair sliced from the seed-0 noise buffer at offsets drawn by
+    torch.randint(0, 2^28 - 2560) on a cuda generator seeded 0 (eggroll.py:117-128 for one parameter of
+    this shape). Output [512, 2048, 2048] fp32 (8.6 GB).
+
+    Size-independent checks: the slices are bit-exact against torch's own device draws; every pair's sum
+    y+ + y- equals 2 x W^T (the rank-1 terms cancel; vs an fp32 product of the same bf16 operands, to
+    1e-5 of its scale, measured 5e-7); every pair's difference (y+ - y-) / 2 equals sigma (x b) a^T (to
+    1e-4 of its scale, measured 1.2e-6); four members checked whole against the fp32 formula."""
+    from noise_amd.eggroll import lowrank
+    from noise_amd.noise import DeviceGenerator
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(2048, 512, generator=g).bfloat16()
+    W = (torch.randn(2048, 512, generator=g) * 0.02).bfloat16()
+    pairs, sigma, NOISE = 256, 1e-3, 2 ** 28
+    offs = torch.randint(0, NOISE - 2560, (pairs,), device=DEV, generator=torch.Generator(DEV).manual_seed(0))
+    rows = DeviceGenerator(0, DEV).take(NOISE).gather(offs, 2560)
+    a, b = rows[:, :2048], rows[:, 2048:]
+    ref_buffer = torch.randn(NOISE, device=DEV, generator=torch.Generator(DEV).manual_seed(0))
+    ref_rows = ref_buffer[offs[:, None] + torch.arange(2560, device=DEV)]
+    assert torch.equal(bits(rows), bits(ref_rows))
+    del ref_buffer, ref_rows
+    print('config 3: 512 members x 2048 tokens x 2048 features', flush=True)
+    sign = torch.tensor([sigma, -sigma], device=DEV).repeat(pairs)
+    xd = X.to(DEV)
+    y = lowrank(xd[None].expand(2 * pairs, 2048, 512), W.to(DEV), a, b, sign, dir_div=2)
+    assert y.shape == (512, 2048, 2048) and torch.isfinite(y).all()
+    base = xd.float() @ W.to(DEV).float().t()
+    scale = base.abs().max()
+    xb = xd.float() @ b.t()                       # [2048 tokens, 256 pairs]
+    worst_sum = worst_diff = 0.0
+    for i in range(pairs):
+        s = (y[2 * i] + y[2 * i + 1]) * 0.5
+        worst_sum = max(worst_sum, ((s - base).abs().max() / scale).item())
+        d = (y[2 * i] - y[2 * i + 1]) * 0.5
+        r1 = sigma * xb[:, i, None] * a[i][None, :]
+        worst_diff = max(worst_diff, ((d - r1).abs().max() / r1.abs().max()).item())
+    print(f'config 3: worst pair-sum error {worst_sum:.2e}, worst rank-1 error {worst_diff:.2e}', flush=True)
+    assert worst_sum <= 1e-5
+    assert worst_diff <= 1e-4
+    for mbr in (0, 1, 255, 511):
+        i = mbr // 2
+        ref = base + sign[mbr] * xb[:, i, None] * a[i][None, :]
+        assert ((y[mbr] - ref).abs().max() / scale).item() <= 1e-4, mbr
