@@ -184,3 +184,68 @@ def test_matches_reference_population_fixture(params):
     W = Weights({k: v.to(DEV) for k, v in P.items()})
     got = population_forward(W, noise, sign.to(DEV), idx[:-1].to(DEV), idx[1:].to(DEV), dir_div=2).cpu()
     check(got, torch.from_numpy(fx['pop_losses']))
+
+
+def _config4_tables(model, pairs):
+    """Step-0 noise of the metric's workload (eggroll.py:117-128): per-direction (a, b) rows of the 48
+    block matrices for directions 0 .. pairs-1 (member m uses row m // 2)."""
+    from noise_amd.eggroll import Eggroll
+    es = Eggroll(model, pairs)
+    offsets = es.offsets(0)
+    directions = torch.arange(pairs, device=DEV)
+    tables = {}
+    for n in BLOCK_MATRICES:
+        p = es.params[n]
+        rows = es.buffer.gather(offsets[n], sum(p.shape), rows=directions)
+        tables[n] = tuple(rows.split(list(p.shape), dim=1))
+    return tables
+
+
+@pytest.mark.parametrize('head_scale', [1.0, 30.0])
+def test_config4_full_population(params, head_scale):
+    """The metric's workload at full size: 1024 members (512 antithetic pairs, sigma 0.002, step-0 noise
+    of the seed-0 buffer on the 48 block matrices) x 2048 Zipf(1.1) tokens, seed-0 init (and the same with
+    the head x30, where the blocks move the loss). Members 0-3 and 1020-1023 within 1e-3 of the fp32
+    oracle; the same members evaluated alone give bit-identical losses; at the plain init every loss sits
+    at ln 4096 + Var(logits) / 2 (8.3177 for this head); with the head x30, halving sigma halves the pairs'
+    loss differences (first order) and quarters their means' offset from the unperturbed loss (second
+    order: the odd orders cancel between the members of a pair)."""
+    from pathlib import Path
+    import numpy as np
+    from noise_amd.eggroll import Weights, population_forward
+    from noise_amd.model import make_model
+    P = scaled_head(params, head_scale)
+    model = make_model('cpu', 0).to(DEV)
+    tables = _config4_tables(model, 512)
+    toks = torch.from_numpy(np.load(Path(__file__).resolve().parent / 'golden' / 'zipf_tokens_2049_seed0.npy')).long()
+    x, y = toks[:-1].to(DEV), toks[1:].to(DEV)
+    sign = torch.tensor([0.002, -0.002], device=DEV).repeat(512)
+    W = Weights({k: v.to(DEV) for k, v in P.items()})
+    print(f'config 4: 1024 members x 2048 tokens, head x{head_scale}', flush=True)
+    losses = population_forward(W, tables, sign, x, y, dir_div=2)
+    assert losses.shape == (1024,) and torch.isfinite(losses).all()
+    members = torch.tensor([0, 1, 2, 3, 1020, 1021, 1022, 1023])
+    dirs = members[::2] // 2
+    sub_tables = {n: (a[dirs.to(DEV)], b[dirs.to(DEV)]) for n, (a, b) in tables.items()}
+    sub = population_forward(W, sub_tables, sign[:8], x, y, dir_div=2)
+    assert torch.equal(sub, losses[members.to(DEV)])
+    onoise = {n: (a[dirs.to(DEV)].cpu().repeat_interleave(2, 0), b[dirs.to(DEV)].cpu().repeat_interleave(2, 0))
+              for n, (a, b) in tables.items()}
+    ref = om.population_loss(P, onoise, sign[:8].cpu(), x.cpu(), y.cpu(), members_per_chunk=2)
+    got = sub.cpu()
+    check(got, ref)
+    if head_scale == 1.0:
+        assert abs(losses.mean().item() - 8.3177) < 1e-3
+    else:
+        # L(+) + L(-) - 2 L0 = sigma^2 e^T H e + O(sigma^4) (the odd orders cancel) and L(+) - L(-) = O(sigma):
+        # halving sigma quarters the pair means' offset and halves the pair differences
+        base = population_forward(W, {}, torch.zeros(2, device=DEV), x, y)[0].item()
+        half = population_forward(W, tables, sign / 2, x, y, dir_div=2)
+        def orders(ls):
+            ls = ls.double().cpu()
+            return ((ls[0::2] + ls[1::2]) / 2 - base).abs().mean().item(), (ls[0::2] - ls[1::2]).abs().mean().item()
+        (s1, f1), (s2, f2) = orders(losses), orders(half)
+        print(f'config 4 x30: second order {s1:.3e} -> {s2:.3e} (x{s1 / s2:.2f}), first order {f1:.3e} -> '
+              f'{f2:.3e} (x{f1 / f2:.2f}) when sigma halves', flush=True)
+        assert 1.8 < f1 / f2 < 2.2
+        assert 3.0 < s1 / s2 < 4.8   # quadratic; a sign mix-up within pairs would make it linear (x2)
