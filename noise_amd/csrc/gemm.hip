@@ -659,38 +659,45 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     const int nf0 = n0 + wn0;
     const float *arow = vec + wn0, *brow = vec + 256 + wn0;  // zeros when absent
     __bf16 *stg = lds + wave * 64 * kStg;
+    // feature-major: each a / b vector chunk is read from LDS once and used for both tokens
+    int64_t row[2];
+    float corr[2], pd[2] = {0.f, 0.f};
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
-        const int t = t0 + wm0 + 32 * tb + j;
-        const int64_t row = (int64_t)m * T + t;
-        const float corr = sgn * dt[tb];  // dt = 0 without perturbation
-        const __bf16 *jr = JIT ? p.jit + row * 2048 + nf0 : nullptr;
-        float pd = 0.f;
+        row[tb] = (int64_t)m * T + t0 + wm0 + 32 * tb + j;
+        corr[tb] = sgn * dt[tb];  // dt = 0 without perturbation
+    }
 #pragma unroll
-        for (int fb = 0; fb < 4; ++fb)
+    for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int f = 32 * fb + 8 * g + 4 * hf;
-                const float4 a4 = ld4(arow + f), b4 = ld4(brow + f);
+        for (int g = 0; g < 4; ++g) {
+            const int f = 32 * fb + 8 * g + 4 * hf;
+            const float4 a4 = ld4(arow + f), b4 = ld4(brow + f);
+            const bf16x2 b01{(__bf16)b4.x, (__bf16)b4.y}, b23{(__bf16)b4.z, (__bf16)b4.w};
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
                 bf16x4 jv;
-                if constexpr (JIT) jv = *reinterpret_cast<const bf16x4 *>(jr + f);
+                if constexpr (JIT) jv = *reinterpret_cast<const bf16x4 *>(p.jit + row[tb] * 2048 + nf0 + f);
                 bf16x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float y = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
+                    float y = acc[fb][tb][4 * g + e] + corr[tb] * f4get(a4, e);
                     if constexpr (JIT) y += (float)jv[e];
                     if constexpr (EAGER) y = bfr(y);
                     y = fmaxf(y, 0.f);
                     o[e] = (__bf16)(y * y);
                 }
                 // act . b with both in bf16, as the reference's autocast x @ b (eggroll.py:58) multiplies them
-                pd = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{o[0], o[1]}, bf16x2{(__bf16)b4.x, (__bf16)b4.y}, pd, false);
-                pd = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{o[2], o[3]}, bf16x2{(__bf16)b4.z, (__bf16)b4.w}, pd, false);
+                pd[tb] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{o[0], o[1]}, b01, pd[tb], false);
+                pd[tb] = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{o[2], o[3]}, b23, pd[tb], false);
                 store_bf16x4(stg + (32 * tb + j) * kStg + f, o);
             }
-        if (p.pdots) {
-            pd += swap_halves(pd);
-            if (hf == 0) p.pdots[row * 16 + nf0 / 128] = pd;
+        }
+    if (p.pdots) {
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            const float t = pd[tb] + swap_halves(pd[tb]);
+            if (hf == 0) p.pdots[row[tb] * 16 + nf0 / 128] = t;
         }
     }
     // whole-line stores of act rows [m][t][nf0 .. nf0 + 128) (256 B each)
