@@ -659,6 +659,18 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
     const int nf0 = n0 + wn0;
     const float *arow = vec + wn0, *brow = vec + 256 + wn0;  // zeros when absent
     __bf16 *stg = lds + wave * 64 * kStg;
+    if constexpr (JIT) {
+        // the wave's jitter rows [64 tokens][128 features] staged by whole-line loads (read in the MFMA
+        // layout, one 8 B load would touch 32 rows); each lane then reads its values from the staging rows and
+        // writes its outputs over them
+        const __bf16 *jbase = p.jit + ((int64_t)m * T + t0 + wm0) * 2048 + nf0;
+#pragma unroll 4
+        for (int it = 0; it < 16; ++it) {
+            const int c = it * 64 + lane, r = c >> 4, ch = c & 15;
+            store_bf16x8(stg + r * kStg + ch * 8, load_bf16x8(jbase + (int64_t)r * 2048 + ch * 8));
+        }
+        wave_lds_sync();
+    }
     // feature-major: each a / b vector chunk is read from LDS once and used for both tokens
     int64_t row[2];
     float corr[2], pd[2] = {0.f, 0.f};
@@ -677,7 +689,7 @@ __global__ __launch_bounds__(kThreads) void fc_kernel(FcArgs p) {
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) {
                 bf16x4 jv;
-                if constexpr (JIT) jv = *reinterpret_cast<const bf16x4 *>(p.jit + row[tb] * 2048 + nf0 + f);
+                if constexpr (JIT) jv = *reinterpret_cast<const bf16x4 *>(stg + (32 * tb + j) * kStg + f);
                 bf16x4 o;
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
