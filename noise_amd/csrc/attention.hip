@@ -43,6 +43,7 @@ struct AttnArgs {
     int heads, seq, qtiles, bh_total;
     int window;
     int xcd_grouped;                    // 1: bh_total % 8 == 0, map heads onto XCDs
+    int o_lines;                        // 1: o 16 B aligned with strides multiple of 8 (staged row stores)
     float scale_log2;                   // softmax scale * log2(e)
     float shift;                        // fixed log2-domain shift of the bounded-score kernel
     // optional fused output: dot[b, t, h] = sum_d O[b,t,h,d] * dvec[(b / ddiv) * ds_b + h*D + d]
@@ -517,6 +518,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         float dsum = 0.f;
         const float *dv = a.dot ? a.dvec + (int64_t)(b / a.ddiv) * a.ds_b + h * kD : nullptr;
         __bf16 *orow = a.o + b * a.os_b + h * a.os_h + (int64_t)q * a.os_t;
+        // with 16 B aligned output rows the wave's 32 x 64 block is staged in LDS (the K / V ring, free once
+        // both groups are past their last tile) and stored as whole 128 B row segments: in the MFMA layout
+        // one 8 B store would touch 32 rows
+        constexpr int kOP = 72;  // staging row pitch (bf16)
+        static_assert(QB == 1, "one staging block per wave");
+        __bf16 *stg = reinterpret_cast<__bf16 *>(lds) + wave * 32 * kOP;
+        if (a.o_lines) __syncthreads();
+        __bf16 *dst = a.o_lines ? stg + j * kOP : orow;
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -525,12 +534,21 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
                 for (int e = 0; e < 4; ++e) v[e] = (__bf16)(o[db][qb][4 * g + e] * inv);
                 const int d = 32 * db + 8 * g + 4 * hf;
-                store_bf16x4(orow + d, v);
+                store_bf16x4(dst + d, v);
                 if (dv) {
 #pragma unroll
                     for (int e = 0; e < 4; ++e) dsum += (float)v[e] * dv[d + e];
                 }
             }
+        if (a.o_lines) {
+            wave_lds_sync();
+            __bf16 *ob = a.o + b * a.os_b + h * a.os_h + (int64_t)(q0w + 32 * qb) * a.os_t;
+#pragma unroll
+            for (int it = 0; it < 4; ++it) {
+                const int c = it * 64 + lane, r = c >> 3, ch = c & 7;
+                store_bf16x8(ob + (int64_t)r * a.os_t + ch * 8, load_bf16x8(stg + r * kOP + ch * 8));
+            }
+        }
         if (a.dot) {
             dsum += swap_halves(dsum);
             if (hf == 0) a.dot[((int64_t)b * T + q) * a.heads + h] = dsum;
@@ -586,6 +604,7 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     a.ks_b = ks_b; a.ks_h = ks_h; a.ks_t = ks_t;
     a.vs_b = vs_b; a.vs_h = vs_h; a.vs_x = vs_x;
     a.os_b = os_b; a.os_h = os_h; a.os_t = os_t;
+    a.o_lines = (aligned(o, 16) && os_b % 8 == 0 && os_h % 8 == 0 && os_t % 8 == 0) ? 1 : 0;
     a.heads = (int)heads; a.seq = (int)seq; a.qtiles = (int)qtiles; a.bh_total = (int)bh;
     a.window = (int)(window > seq ? seq : window);
     a.xcd_grouped = (bh % 8 == 0) ? 1 : 0;
