@@ -58,6 +58,25 @@ class KernelTimer:
 
 
 _TIMER = None
+_ROPE = {}
+
+
+def _rope_tables(T, dev):
+    """bf16 rotary tables of length T on dev, built once per (T, device): the copy from host memory waits for
+    the stream, so a per-call copy would stall the launch queue (the reference keeps them as model buffers,
+    model.py:177-183)."""
+    key = (T, dev.type, dev.index)
+    if key not in _ROPE:
+        cos, sin = rotary_tables(T)
+        _ROPE[key] = (cos.to(dev).bfloat16().contiguous(), sin.to(dev).bfloat16().contiguous())
+    return _ROPE[key]
+
+
+def _pair_signs(pairs, sigma, device):
+    """[+sigma, -sigma] * pairs built on the device (no host copy that would wait for the stream)."""
+    sign = torch.full((2 * pairs,), float(sigma), device=device)
+    sign[1::2] = -float(sigma)
+    return sign
 
 
 def set_timer(timer):
@@ -194,8 +213,7 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     pop = _lib.Population(m, T, sign.data_ptr(), dir_div, rounding)
     popp = ctypes.byref(pop)
     if rope is None:
-        cos, sin = rotary_tables(T)
-        rope = (cos.to(dev).bfloat16().contiguous(), sin.to(dev).bfloat16().contiguous())
+        rope = _rope_tables(T, dev)
     cos_t, sin_t = rope
     L = W.n_layer
     E = N_EMBD
@@ -447,7 +465,7 @@ class Eggroll:
                 p = self.params[name]
                 rows = self.buffer.gather(o, sum(p.shape), rows=directions)
                 noise[name] = tuple(rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
-            sign = torch.tensor([SIGMA, -SIGMA], device=self.device).repeat(n // 2)
+            sign = _pair_signs(n // 2, SIGMA, self.device)
             seq = start // per_seq
             losses[start - self.rank * per_rank:start - self.rank * per_rank + n] = population_forward(
                 W, noise, sign, x[seq], y[seq], dir_div=2)
@@ -555,6 +573,6 @@ def orthogonal_population(W, noise, x, y, sigma=SIGMA, chunk=1024, directions=No
     for start in range(0, len(dirs), chunk // 2):
         d = dirs[start:start + chunk // 2]
         sub = {k: (a[d], b[d]) for k, (a, b) in noise.items()}
-        sign = torch.tensor([sigma, -sigma], device=dev).repeat(len(d))
+        sign = _pair_signs(len(d), sigma, dev)
         losses.append(population_forward(W, sub, sign, x, y, dir_div=2))
     return torch.cat(losses)
