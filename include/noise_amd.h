@@ -149,13 +149,16 @@ typedef struct {
 } noise_population_t;
 
 /* Block entry (eggroll.py:74-79 for block 0; model.py:196-199): e = wte[idx[t]] (+ sign * a[idx[t]] * b,
- * lowrank_embed eggroll.py:61-63), x0 = norm(e), x = rl*x0 + ml*x0 (rl/ml = resid/x0 lambda of block 0,
- * + sign * eps when eps_* != NULL, eggroll.py:77-78), h = bf16(norm(x)). per_member = 0 writes one shared
- * [tokens][512] set (no embedding or lambda noise); per_member = 1 writes [members][tokens][512]. wte is
- * fp32 [V][512] (eggroll.py:50). x0, xin fp32, h bf16. */
-int noise_pop_embed(const noise_population_t *pop, int per_member, const float *wte, const int64_t *idx,
-                    const noise_rank1_t *emb_noise, float lam_r, float lam_x, const float *eps_r, const float *eps_x,
-                    int64_t eps_stride, float *x0, float *xin, void *h, noise_stream_t stream);
+ * lowrank_embed eggroll.py:61-63), x0 = norm(e), x = rl*x0 + ml*x0 (rl = *lam_r, ml = *lam_x: block 0's
+ * resid / x0 lambda, read on the device, + sign * eps when eps_* != NULL, eggroll.py:77-78),
+ * h = bf16(norm(x)). per_member = 0 writes one shared [tokens][512] set (no embedding or lambda noise);
+ * per_member = 1 writes [members][tokens][512]. wte is fp32 [vocab][512] (eggroll.py:50). x0, xin fp32,
+ * h bf16. A token id outside [0, vocab) reads no memory outside the table and yields NaN rows (the
+ * reference raises an IndexError there). */
+int noise_pop_embed(const noise_population_t *pop, int per_member, const float *wte, int64_t vocab,
+                    const int64_t *idx, const noise_rank1_t *emb_noise, const float *lam_r, const float *lam_x,
+                    const float *eps_r, const float *eps_x, int64_t eps_stride, float *x0, float *xin, void *h,
+                    noise_stream_t stream);
 
 /* out[(m*tokens + t)*nk + k] = sum_n x[m, t, n] * vecs[k].b[(m / dir_div)*b_stride + n], n < width:
  * the x . b factor of eggroll.py:58's rank-1 term for up to 3 matrices sharing input x. */
@@ -175,9 +178,10 @@ int noise_pop_gate(const noise_population_t *pop, noise_view_t x, const float *g
  * or NULL) when ve (fp32 [V][512]) is not NULL; idx_sm = 0 when every member reads the same sequence (the
  * population), else the member stride of per-member token ids (>= tokens: scoring distinct sequences); rotary (rope_cos/rope_sin: model.py:177-183's bf16 tables,
  * [tokens][32] bf16, 16 B aligned) then per-head RMSNorm on Q and K. Outputs bf16: Q, K
- * [members][8][tokens][64]; V transposed [members][8][64][tokens]. */
+ * [members][8][tokens][64]; V transposed [members][8][64][tokens]. ve has `vocab` rows: a token id outside
+ * [0, vocab) reads no memory outside it and makes that token's V NaN. */
 int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3], const noise_rank1_t r1[3],
-                  const float *dots, const void *rope_cos, const void *rope_sin, const float *ve,
+                  const float *dots, const void *rope_cos, const void *rope_sin, const float *ve, int64_t vocab,
                   const int64_t *idx, int64_t idx_sm, const float *gates, const noise_rank1_t *ve_noise,
                   void *const out[3], noise_stream_t stream);
 
@@ -193,12 +197,12 @@ int noise_pop_qkv_shared(const noise_population_t *pop, const float *base, const
 
 /* Residual writer (eggroll.py:92 attn.c_proj and :93 mlp.c_proj): y = xres + x w^T + sign * (sum of
  * dots_count dots at dots[row*dots_stride]) * a; if mix: y = rl*y + ml*x0 (the next block's mixing,
- * eggroll.py:79, lambdas + sign * eps); xout = y (fp32, may be NULL); hout = bf16(norm(y)) [m][T][512]
+ * eggroll.py:79, rl = *lam_r and ml = *lam_x read on the device, + sign * eps); xout = y (fp32, may be NULL); hout = bf16(norm(y)) [m][T][512]
  * or, with split3, its [hi | lo | hi] bf16 split [m][T][1536] for the fp32 head; next_dots[row*nnext+k]
  * = norm(y) . next[k].b (0 <= nnext <= 3). w bf16 [512][K], K = 512 (attn.c_proj) or 2048 (mlp.c_proj). */
 int noise_pop_residual(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K,
                        const noise_rank1_t *r1, const float *dots, int64_t dots_stride, int64_t dots_count,
-                       noise_view_t xres, float *xout, int mix, float lam_r, float lam_x, const float *eps_r,
+                       noise_view_t xres, float *xout, int mix, const float *lam_r, const float *lam_x, const float *eps_r,
                        const float *eps_x, int64_t eps_stride, noise_view_t x0, void *hout, int split3,
                        const noise_rank1_t *next, int64_t nnext, float *next_dots, noise_stream_t stream);
 
@@ -211,14 +215,17 @@ int noise_pop_fc(const noise_population_t *pop, noise_view_t x, const void *w, c
 
 /* Perturbed linear (eggroll.py:56-58 `lowrank`): y[m, t, :] = x[m, t, :] w^T + sign[m] * dots[m*T+t] *
  * a[m / dir_div] (dots = x . b from noise_member_dots; r1 NULL or r1->a NULL: plain linear). bf16 x and
- * w [N][K]; y bf16 or fp32 (y_fp32) with strides ys_m, ys_t. N multiple of 256, K of 64. */
+ * w [N][K]; y with strides ys_m, ys_t: bf16 (y_fp32 = 0), fp32 (1), or fp32 in autocast's form (2: the
+ * product and the dot rounded to bf16 before the fp32 sum, as eggroll.py:58 runs under autocast).
+ * N multiple of 256, K of 64. */
 int noise_pop_linear(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K, int64_t N,
                      const noise_rank1_t *r1, const float *dots, void *y, int y_fp32, int64_t ys_m, int64_t ys_t,
                      noise_stream_t stream);
 
 /* Head, soft cap 15 and per-token cross-entropy (eggroll.py:94-101, model.py:202-209, run.py:89-94):
  * logits = x w^T (+ sign * dots * a), z = 15 tanh(logits / 15), token_loss[m*T + t] = logsumexp(z) -
- * z[target] (0 where target < 0). w bf16 [vocab][K]; K = 512, or 1536 for the split-bf16x3 fp32 head
+ * z[target]: 0 where target == -1 (ignore_index), NaN for any other target outside [0, vocab) (where
+ * F.cross_entropy raises). w bf16 [vocab][K]; K = 512, or 1536 for the split-bf16x3 fp32 head
  * (x = [hi|lo|hi], w = [hi|hi|lo], noise_split3). targets int64 [T] shared (targets_sm = 0) or per member. */
 int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K, int64_t vocab,
                       const noise_rank1_t *r1, const float *dots, const int64_t *targets, int64_t targets_sm,
@@ -234,15 +241,26 @@ int noise_split3(const float *x, int64_t rows, int64_t width, int normalize, int
                  noise_stream_t stream);
 
 /* lowrank_embed (eggroll.py:61-63): out[m, t, :] = w[idx[t], :] + sign[m] * a[m/dir_div, idx[t]] *
- * b[m/dir_div, :] (r1 NULL or r1->a NULL: plain gather), fp32 [members][tokens][width]. */
+ * b[m/dir_div, :] (r1 NULL or r1->a NULL: plain gather), fp32 [members][tokens][width]. An id outside
+ * [0, vocab) reads nothing and gives a NaN row. */
 int noise_lowrank_embed(float *out, const float *w, int64_t vocab, int64_t width, const int64_t *idx,
                         const noise_population_t *pop, const noise_rank1_t *r1, noise_stream_t stream);
 
 /* Rank-1 expansion of a product shared by all members (eggroll.py:58 with x broadcast over members):
- * y[m, t, n] = base[t, n] + sign[m] * dots[m*T + t] * a[m/dir_div, n], y bf16 or fp32 [m][T][width],
- * base fp32 [T][width]. An HBM-write stream: the shared x W^T is computed once (noise_pop_linear). */
+ * y[m, t, n] = base[t, n] + sign[m] * dots[m*T + t] * a[m/dir_div, n], y bf16 (y_fp32 = 0) or fp32 (1;
+ * 2: the dot rounded to bf16 first, autocast's form) [m][T][width], base fp32 [T][width]. An HBM-write
+ * stream: the shared x W^T is computed once (noise_pop_linear). */
 int noise_rank1_expand(const noise_population_t *pop, const float *base, int64_t width, const float *dots,
                        const noise_rank1_t *r1, void *y, int y_fp32, noise_stream_t stream);
+
+/* lowrank (eggroll.py:56-58) for any shape, in autocast's form: y[m, t, o] = bf16(x[m, t, :] . w[o, :]) +
+ * sign[m] * bf16(x[m, t, :] . bf16(b[m/dir_div, :])) * a[m/dir_div, o], fp32 accumulation, y fp32
+ * [members][tokens][n_out]. x bf16 through the strided view (element (m, t, k) at x + m*sm + t*st + k),
+ * w bf16 [n_out][n_in]. Serves the call sites whose shapes the MFMA tiles of noise_pop_linear do not take,
+ * e.g. the value-embedding gate linear('attn.ve_gate.weight', h[..., :32]) (eggroll.py:88 via :80): w [8, 32]
+ * on a 32-wide slice of a 512-wide row. One thread per output element. */
+int noise_lowrank_rows(const noise_population_t *pop, noise_view_t x, int64_t n_in, const void *w, int64_t n_out,
+                       const noise_rank1_t *r1, float *y, noise_stream_t stream);
 
 /* ---- DUST --------------------------------------------------------------------------------------------- */
 

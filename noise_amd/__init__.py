@@ -5,3 +5,4 @@ mirrors of the reference's call sites: utils/model.py `attention`, train/val/egg
 `lowrank_embed`, `population_loss` and `Eggroll` noise bookkeeping, train/val/run.py `head_loss`.
 """
 from . import _lib  # noqa: F401
+from . import ops  # noqa: F401,E402  (registers the torch.ops.noise_amd drop-ins)

@@ -3,13 +3,12 @@
 There is no fallback: if the library is missing or does not load, every op raises.
 """
 import ctypes
-import os
 from pathlib import Path
 
 import torch
 
-# NOISE_AMD_LIB: path of another build of the library (A/B timing of kernel variants)
-LIB_PATH = Path(os.environ.get('NOISE_AMD_LIB') or Path(__file__).resolve().with_name('libnoise_amd.so'))
+# the in-tree build (noise_amd/build.py); no other library is ever loaded
+LIB_PATH = Path(__file__).resolve().with_name('libnoise_amd.so')
 
 _p, _i64, _u64, _i32, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint64, ctypes.c_int, ctypes.c_float
 
@@ -24,12 +23,12 @@ SIGNATURES = {
     'noise_orthogonal_draws': [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p],
     'noise_attention_fwd': [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _p, _p],
-    'noise_pop_embed': [_p, _i32, _p, _p, _p, _f32, _f32, _p, _p, _i64, _p, _p, _p, _p],
+    'noise_pop_embed': [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p],
     'noise_member_dots': [_p, 'View', _i64, _p, _i64, _p, _p],
-    'noise_pop_qkv': [_p, 'View', _p, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p],
+    'noise_pop_qkv': [_p, 'View', _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _p, _p],
     'noise_pop_gate': [_p, 'View', _p, _p, _p, _p],
     'noise_pop_qkv_shared': [_p, _p, _p, _p, _p, _p, _p, _p],
-    'noise_pop_residual': [_p, 'View', _p, _i64, _p, _p, _i64, _i64, 'View', _p, _i32, _f32, _f32, _p, _p,
+    'noise_pop_residual': [_p, 'View', _p, _i64, _p, _p, _i64, _i64, 'View', _p, _i32, _p, _p, _p, _p,
                            _i64, 'View', _p, _i32, _p, _i64, _p, _p],
     'noise_pop_fc': [_p, 'View', _p, _p, _p, _p, _p, _p, _p],
     'noise_pop_linear': [_p, 'View', _p, _i64, _i64, _p, _p, _p, _i32, _i64, _i64, _p],
@@ -38,6 +37,7 @@ SIGNATURES = {
     'noise_split3': [_p, _i64, _i64, _i32, _i32, _p, _p],
     'noise_lowrank_embed': [_p, _p, _i64, _i64, _p, _p, _p, _p],
     'noise_rank1_expand': [_p, _p, _i64, _p, _p, _p, _i32, _p],
+    'noise_lowrank_rows': [_p, 'View', _i64, _p, _i64, _p, _p, _p],
     'noise_coordinate_differences': [_p, _i32, _i64, _i64, _i64, _p, _f32, _p, _i64, _i64, _p],
     'noise_draw_errors': [_p, _p, _i64, _i64, _i64, _f32, _p, _p],
     'noise_dust_block_workspace_bytes': [_i64, _i64, _i32],
@@ -48,6 +48,9 @@ SIGNATURES = {
 }
 _RESTYPES = {'noise_last_error': ctypes.c_char_p, 'noise_update_workspace_bytes': ctypes.c_int64,
              'noise_dust_block_workspace_bytes': ctypes.c_int64}
+
+# y_fp32 of noise_pop_linear / noise_rank1_expand: fp32 output in autocast's form (bf16 product and dot)
+LINEAR_AUTOCAST = 2
 
 # noise_population_t.rounding (include/noise_amd.h)
 ROUNDING_FUSED = 0

@@ -54,4 +54,11 @@ __host__ __device__ inline float bf16_bits_to_f32(uint16_t h) {
 
 __host__ __device__ inline float round_bf16(float f) { return bf16_bits_to_f32(f32_to_bf16_bits(f)); }
 
+// DUST's block_forward chain (noise_dust_block) over a caller-provided workspace of workspace_bytes
+// (noise_dust_block_workspace_bytes); fn names the entry point in error messages.
+int dust_block_run(const float *x, float *x_out, int64_t sequences, int64_t tokens, const void *const w[7],
+                   const void *ve, const void *rope_cos, const void *rope_sin, int64_t window, const void *jit_o,
+                   const void *jit_attn, const void *jit_fc, const void *jit_mlp, void *workspace,
+                   int64_t workspace_bytes, noise_stream_t stream, const char *fn);
+
 }  // namespace noise

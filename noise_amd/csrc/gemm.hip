@@ -68,6 +68,7 @@ struct QkvArgs {
     int64_t ve_m;             // 0 (one table for all members) or the member stride of per-member rows
     const int64_t *idx;       // token ids: member m, token t at idx[m * idx_m + t]
     int64_t idx_m;            // 0 (one sequence for all members) or the member stride of per-member tokens
+    int64_t vocab;            // rows of the value table: other ids read row 0 and give NaN values
     const float *gates;       // [rows][8] value-embedding gates (noise_pop_gate)
     Rank1 ve_r1;              // value-embedding noise (a [dirs][V], b [dirs][512]) or a == NULL
     __bf16 *out[3];           // q, k: [m][8][T][64]; v transposed: [m][8][64][T]
@@ -143,9 +144,11 @@ __global__ __launch_bounds__(kThreads) void qkv_kernel(QkvArgs p) {
         const int64_t row = (int64_t)m * T + t;
         if (a0) dt[tb] = p.dots[row * 3 + mat];
         if (ve_on) {
-            tokv[tb] = p.idx[m * p.idx_m + t];
-            gt[tb][0] = p.gates[row * 8 + head0];
-            gt[tb][1] = p.gates[row * 8 + head0 + 1];
+            const int64_t tok = p.idx[m * p.idx_m + t];
+            const bool bad = tok < 0 || tok >= p.vocab;  // an id outside the table: no read leaves it, V is NaN
+            tokv[tb] = bad ? 0 : tok;
+            gt[tb][0] = bad ? __builtin_nanf("") : p.gates[row * 8 + head0];
+            gt[tb][1] = bad ? __builtin_nanf("") : p.gates[row * 8 + head0 + 1];
             if (p.ve_r1.a) vesc[tb] = p.ve_r1.a[dir * p.ve_r1.a_stride + tokv[tb]];
         }
     }
@@ -389,7 +392,7 @@ struct ResidArgs {
     int64_t xr_m, xr_t;
     float *xout;              // [m][T][512] or NULL
     int mix;
-    float lam_r, lam_x;
+    const float *lam_r, *lam_x;  // the next block's mixing scalars (device, read when mixing)
     const float *eps_r, *eps_x;  // per-direction lambda noise (eps[dir * eps_stride]) or NULL
     int64_t eps_stride;
     const float *x0;
@@ -457,8 +460,10 @@ __global__ __launch_bounds__(kThreads) void resid_kernel(ResidArgs p) {
             for (int i = 0; i < p.dots_count; ++i) dsum[tb] += p.dots[row * p.dots_stride + i];
         }
     }
-    float rl = p.lam_r, ml = p.lam_x;
+    float rl = 0.f, ml = 0.f;
     if (MIX) {
+        rl = *p.lam_r;
+        ml = *p.lam_x;
         if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
         if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
     }
@@ -734,7 +739,7 @@ struct LowrankArgs {
     Rank1 r1;
     const float *dots;        // [rows] (x . b per row) or NULL when unperturbed
     void *y;
-    int y_fp32;
+    int y_fp32;               // 0 bf16 out, 1 fp32, 2 fp32 of the bf16-rounded product and dot (autocast)
     int64_t ys_m, ys_t;
 };
 
@@ -759,7 +764,10 @@ __global__ __launch_bounds__(kThreads) void lowrank_kernel(LowrankArgs p) {
     for (int tb = 0; tb < 2; ++tb) {
         const int t = t0 + wm0 + 32 * tb + j;
         const int64_t row = (int64_t)m * T + t;
-        const float corr = p.r1.a ? sgn * p.dots[row] : 0.f;
+        // autocast form (y_fp32 == 2): the product and the x . b dot enter rounded to bf16, as autocast's
+        // matmuls return them (eggroll.py:58 under eggroll.py:144)
+        const bool ac = p.y_fp32 == 2;
+        const float corr = p.r1.a ? sgn * (ac ? bfr(p.dots[row]) : p.dots[row]) : 0.f;
 #pragma unroll
         for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
@@ -768,7 +776,10 @@ __global__ __launch_bounds__(kThreads) void lowrank_kernel(LowrankArgs p) {
                 float4 a4 = p.r1.a ? ld4(p.r1.a + dir * p.r1.a_stride + f) : float4{0, 0, 0, 0};
                 float o[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) o[e] = acc[fb][tb][4 * g + e] + corr * f4get(a4, e);
+                for (int e = 0; e < 4; ++e) {
+                    const float prod = acc[fb][tb][4 * g + e];
+                    o[e] = (ac ? bfr(prod) : prod) + corr * f4get(a4, e);
+                }
                 if (p.y_fp32) {
                     st4((float *)p.y + m * p.ys_m + (int64_t)t * p.ys_t + f, float4{o[0], o[1], o[2], o[3]});
                 } else {
@@ -798,7 +809,7 @@ struct HeadArgs {
     const float *dots;
     const int64_t *targets;   // [T] shared by all members, or [m][T] when targets_sm != 0
     int64_t targets_sm;
-    float *loss;              // [m][T] per-token CE (0 where target < 0)
+    float *loss;              // [m][T] per-token CE (0 where target == -1, NaN for targets outside [0, vocab))
 };
 
 // EAGER: logits rounded to bf16 before the soft cap (the autocast head's bf16 output; unperturbed calls only)
@@ -868,7 +879,9 @@ __global__ __launch_bounds__(kThreads) void head_ce_kernel(HeadArgs p) {
             const float s = red[(tl * 2) * 2] + red[(tl * 2 + 1) * 2];
             const float z = red[(tl * 2) * 2 + 1] + red[(tl * 2 + 1) * 2 + 1];
             const float ce = 15.0f + __logf(s) - z;
-            p.loss[(int64_t)m * T + t0 + tl] = tgt[tb] < 0 ? 0.f : ce;
+            // ignore_index -1 contributes 0; any other id outside [0, vocab) is an error, reported as NaN
+            const int64_t tg = tgt[tb];
+            p.loss[(int64_t)m * T + t0 + tl] = tg == -1 ? 0.f : (tg < 0 || tg >= p.vocab ? __builtin_nanf("") : ce);
         }
     }
 }
@@ -949,7 +962,7 @@ using namespace noise;
 
 extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, const void *const w[3],
                              const noise_rank1_t r1[3], const float *dots, const void *rope_cos, const void *rope_sin,
-                             const float *ve, const int64_t *idx, int64_t idx_sm, const float *gates,
+                             const float *ve, int64_t vocab, const int64_t *idx, int64_t idx_sm, const float *gates,
                              const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream) {
     clear_error();
     const char *fn = "noise_pop_qkv";
@@ -962,7 +975,7 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
         NOISE_CHECK_ARG(!r1 || !r1[i].a || (dots && pop->sign && aligned(r1[i].a, 16) && r1[i].a_stride % 4 == 0),
                         "%s: perturbed matrix %d needs dots, sign and 16 B aligned a rows", fn, i);
     }
-    NOISE_CHECK_ARG(!ve || (idx && gates), "%s: value embeddings need idx and gates", fn);
+    NOISE_CHECK_ARG(!ve || (idx && gates && vocab > 0), "%s: value embeddings need idx, gates and vocab", fn);
     NOISE_CHECK_ARG(idx_sm == 0 || idx_sm >= pop->tokens, "%s: idx_sm must be 0 or >= tokens", fn);
     NOISE_CHECK_ARG(!eager(pop) || ((!r1 || (!r1[0].a && !r1[1].a && !r1[2].a)) && (!ve_noise || !ve_noise->a)),
                     "%s: eager rounding is for unperturbed calls", fn);
@@ -976,6 +989,7 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
     }
     a.dots = dots; a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin; a.ve = ve; a.ve_m = 0; a.idx = idx;
     a.idx_m = idx_sm;
+    a.vocab = vocab;
     a.gates = gates;
     a.ve_r1 = make_r1(ve ? ve_noise : nullptr);
     NOISE_CHECK_ARG(!a.ve_r1.a || (pop->sign && aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
@@ -1019,7 +1033,7 @@ extern "C" int noise_pop_qkv_shared(const noise_population_t *pop, const float *
 
 extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x, const void *w, int64_t K,
                                   const noise_rank1_t *r1, const float *dots, int64_t dots_stride, int64_t dots_count,
-                                  noise_view_t xres, float *xout, int mix, float lam_r, float lam_x,
+                                  noise_view_t xres, float *xout, int mix, const float *lam_r, const float *lam_x,
                                   const float *eps_r, const float *eps_x, int64_t eps_stride, noise_view_t x0,
                                   void *hout, int split3, const noise_rank1_t *next, int64_t nnext, float *next_dots,
                                   noise_stream_t stream) {
@@ -1031,6 +1045,7 @@ extern "C" int noise_pop_residual(const noise_population_t *pop, noise_view_t x,
     NOISE_CHECK_ARG(xres.ptr && aligned(xres.ptr, 16) && xres.sm % 4 == 0 && xres.st % 4 == 0, "%s: bad xres", fn);
     NOISE_CHECK_ARG(!xout || aligned(xout, 16), "%s: xout must be 16 B aligned", fn);
     NOISE_CHECK_ARG(!mix || (x0.ptr && aligned(x0.ptr, 16) && x0.sm % 4 == 0 && x0.st % 4 == 0), "%s: mix needs x0", fn);
+    NOISE_CHECK_ARG(!mix || (lam_r && lam_x), "%s: mix needs the mixing scalars lam_r, lam_x", fn);
     NOISE_CHECK_ARG(hout && aligned(hout, 8), "%s: hout NULL or misaligned", fn);
     NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || (next && next_dots)), "%s: bad next-dot request", fn);
     NOISE_CHECK_ARG(!r1 || !r1->a || (dots && pop->sign && dots_count >= 1 && aligned(r1->a, 16) && r1->a_stride % 4 == 0),
@@ -1245,7 +1260,15 @@ extern "C" int noise_dust_block(const float *x, float *x_out, int64_t sequences,
                                 const void *jit_mlp, void *workspace, int64_t workspace_bytes,
                                 noise_stream_t stream) {
     clear_error();
-    const char *fn = "noise_dust_block";
+    return noise::dust_block_run(x, x_out, sequences, tokens, w, ve, rope_cos, rope_sin, window, jit_o, jit_attn,
+                                 jit_fc, jit_mlp, workspace, workspace_bytes, stream, "noise_dust_block");
+}
+
+// The DUST block chain over a caller-provided workspace (both dust-block entry points run it).
+int noise::dust_block_run(const float *x, float *x_out, int64_t sequences, int64_t tokens, const void *const w[7],
+                          const void *ve, const void *rope_cos, const void *rope_sin, int64_t window,
+                          const void *jit_o, const void *jit_attn, const void *jit_fc, const void *jit_mlp,
+                          void *workspace, int64_t workspace_bytes, noise_stream_t stream, const char *fn) {
     NOISE_CHECK_ARG(sequences >= 1 && tokens >= 256 && tokens % 256 == 0 && sequences * tokens < (1ll << 31),
                     "%s: tokens must be a positive multiple of 256 and sequences * tokens < 2^31", fn);
     NOISE_CHECK_ARG(x && x_out && aligned(x, 16) && aligned(x_out, 16), "%s: x / x_out NULL or misaligned", fn);
@@ -1292,7 +1315,7 @@ extern "C" int noise_dust_block(const float *x, float *x_out, int64_t sequences,
         for (int i = 0; i < 3; ++i) a.w[i] = (const __bf16 *)w[i];
         a.out[0] = q; a.out[1] = k; a.out[2] = v;
         a.cos_t = (const __bf16 *)rope_cos; a.sin_t = (const __bf16 *)rope_sin;
-        a.ve = vef; a.ve_m = tokens * 512; a.idx = iota; a.idx_m = 0; a.gates = gates;
+        a.ve = vef; a.ve_m = tokens * 512; a.idx = iota; a.idx_m = 0; a.vocab = tokens; a.gates = gates;
         hipLaunchKernelGGL(qkv_kernel<false>, dim3((unsigned)(6 * sequences * (tokens / 256))), dim3(kThreads), 0, s,
                            a);
         NOISE_TRY(launch_status(fn));

@@ -36,9 +36,10 @@ struct EmbedArgs {
     const float *sign;
     const float *ea, *eb;     // embedding noise rows or NULL
     int64_t ea_stride, eb_stride;
-    float lam_r, lam_x;
+    const float *lam_r, *lam_x;   // block 0's mixing scalars (device)
     const float *eps_r, *eps_x;
     int64_t eps_stride;
+    int64_t vocab;                // rows of wte; other ids give NaN rows
     float *x0, *xin;
     __bf16 *h;
 };
@@ -51,9 +52,15 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs p) {
     const int t = row - (p.per_member ? m * p.tokens : 0);
     const int dir = m / p.dir_div;
     const float sgn = p.per_member && p.sign ? p.sign[m] : 0.f;
-    const int64_t tok = p.idx[t];
+    const int64_t id = p.idx[t];
+    const bool bad = id < 0 || id >= p.vocab;  // an id outside the table: no read leaves it, the row is NaN
+    const int64_t tok = bad ? 0 : id;
     float e[8];
     ld8(p.wte + tok * 512 + lane * 8, e);
+    if (bad) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) e[i] = __builtin_nanf("");
+    }
     if (p.ea) {
         const float s = sgn * p.ea[dir * p.ea_stride + tok];
         float b[8];
@@ -65,7 +72,7 @@ __global__ __launch_bounds__(256) void embed_kernel(EmbedArgs p) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) ss += e[i] * e[i];
     float r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
-    float rl = p.lam_r, ml = p.lam_x;
+    float rl = *p.lam_r, ml = *p.lam_x;
     if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
     if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
     if (p.eager) {
@@ -188,14 +195,16 @@ unsigned rows_grid(int64_t rows) { return (unsigned)((rows + 3) / 4); }
 
 using namespace noise;
 
-extern "C" int noise_pop_embed(const noise_population_t *pop, int per_member, const float *wte, const int64_t *idx,
-                               const noise_rank1_t *emb_noise, float lam_r, float lam_x, const float *eps_r,
+extern "C" int noise_pop_embed(const noise_population_t *pop, int per_member, const float *wte, int64_t vocab,
+                               const int64_t *idx, const noise_rank1_t *emb_noise, const float *lam_r,
+                               const float *lam_x, const float *eps_r,
                                const float *eps_x, int64_t eps_stride, float *x0, float *xin, void *h,
                                noise_stream_t stream) {
     clear_error();
     const char *fn = "noise_pop_embed";
     NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
-    NOISE_CHECK_ARG(wte && idx && x0 && xin && h, "%s: NULL pointer", fn);
+    NOISE_CHECK_ARG(wte && idx && x0 && xin && h && lam_r && lam_x, "%s: NULL pointer", fn);
+    NOISE_CHECK_ARG(vocab > 0, "%s: vocab must be positive", fn);
     NOISE_CHECK_ARG(aligned(wte, 16) && aligned(x0, 16) && aligned(xin, 16) && aligned(h, 16), "%s: 16 B alignment", fn);
     const bool noisy = (emb_noise && emb_noise->a) || eps_r || eps_x;
     NOISE_CHECK_ARG(!noisy || (per_member && pop->sign), "%s: per-member noise needs per_member = 1 and sign", fn);
@@ -213,6 +222,7 @@ extern "C" int noise_pop_embed(const noise_population_t *pop, int per_member, co
     a.ea_stride = a.ea ? emb_noise->a_stride : 0;
     a.eb_stride = a.ea ? emb_noise->b_stride : 0;
     a.lam_r = lam_r; a.lam_x = lam_x; a.eps_r = eps_r; a.eps_x = eps_x; a.eps_stride = eps_stride;
+    a.vocab = vocab;
     a.x0 = x0; a.xin = xin; a.h = (__bf16 *)h;
     a.eager = pop->rounding == NOISE_ROUNDING_EAGER;
     hipLaunchKernelGGL(embed_kernel, dim3(rows_grid(a.rows)), dim3(256), 0, (hipStream_t)stream, a);
@@ -267,14 +277,20 @@ namespace {
 __global__ __launch_bounds__(256) void lowrank_embed_kernel(float *out, const float *w, const int64_t *idx, int tokens,
                                                             int width, const float *a, const float *b,
                                                             int64_t a_stride, int64_t b_stride, const float *sign,
-                                                            int dir_div, int64_t total) {
+                                                            int dir_div, int64_t vocab, int64_t total) {
     const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
     if (i >= total) return;
     const int64_t row = i / width;
     const int n = (int)(i - row * width);
     const int m = (int)(row / tokens), t = (int)(row - (int64_t)m * tokens);
     const int dir = m / dir_div;
-    const int64_t tok = idx[t];
+    const int64_t id = idx[t];
+    if (id < 0 || id >= vocab) {  // an id outside the table: no read leaves it, the row is NaN
+        const float nan = __builtin_nanf("");
+        *reinterpret_cast<float4 *>(out + i) = float4{nan, nan, nan, nan};
+        return;
+    }
+    const int64_t tok = id;
     float4 v = *reinterpret_cast<const float4 *>(w + tok * width + n);
     if (a) {
         const float s = sign[m] * a[dir * a_stride + tok];
@@ -285,7 +301,8 @@ __global__ __launch_bounds__(256) void lowrank_embed_kernel(float *out, const fl
 }
 
 // Rank-1 expansion of a shared product (lowrank with x broadcast over members, eggroll.py:58):
-// y[m, t, n] = base[t, n] + sign[m] * dots[m*T + t] * a[dir, n]; 8 outputs per thread, bf16 or fp32.
+// y[m, t, n] = base[t, n] + sign[m] * dots[m*T + t] * a[dir, n]; 8 outputs per thread, bf16 (y_fp32 = 0)
+// or fp32 (1; 2 = the dot rounded to bf16 first, as autocast's x . b product).
 __global__ __launch_bounds__(256) void rank1_expand_kernel(void *y, int y_fp32, const float *base, const float *dots,
                                                            const float *a, int64_t a_stride, const float *sign,
                                                            int dir_div, int tokens, int width, int64_t total) {
@@ -294,7 +311,7 @@ __global__ __launch_bounds__(256) void rank1_expand_kernel(void *y, int y_fp32, 
     const int64_t row = i / width;
     const int n = (int)(i - row * width);
     const int m = (int)(row / tokens), t = (int)(row - (int64_t)m * tokens);
-    const float c = sign[m] * dots[row];
+    const float c = sign[m] * (y_fp32 == 2 ? bfr(dots[row]) : dots[row]);  // 2: autocast's bf16 x . b
     const float *ar = a + (int64_t)(m / dir_div) * a_stride + n;
     const float *br = base + (int64_t)t * width + n;
     float o[8];
@@ -311,6 +328,36 @@ __global__ __launch_bounds__(256) void rank1_expand_kernel(void *y, int y_fp32, 
         for (int e = 0; e < 8; ++e) ob[e] = (__bf16)o[e];
         store_bf16x8((__bf16 *)y + i, ob);
     }
+}
+
+// lowrank (eggroll.py:56-58) for shapes the MFMA tiles do not take, such as the value-embedding gate's
+// [8, 32] weight applied to h[..., :32] (eggroll.py:88):
+//   y[m, t, o] = bf16(x[m, t] . W[o]) + sign[m] * bf16(x[m, t] . bf16(b[dir])) * a[dir, o]
+// with fp32 accumulation and the two products rounded to bf16 as autocast's matmuls return them (b enters
+// the matmul rounded, a multiplies in fp32); y fp32 [m][T][out]. One thread per output element.
+__global__ __launch_bounds__(256) void lowrank_rows_kernel(int tokens, int n_in, int n_out, int dir_div,
+                                                           const __bf16 *x, int64_t xs_m, int64_t xs_t,
+                                                           const __bf16 *w, const float *a, const float *b,
+                                                           int64_t a_stride, int64_t b_stride, const float *sign,
+                                                           float *y, int64_t total) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const int64_t row = i / n_out;
+    const int o = (int)(i - row * n_out);
+    const int m = (int)(row / tokens), t = (int)(row - (int64_t)m * tokens);
+    const int dir = m / dir_div;
+    const __bf16 *xr = x + m * xs_m + (int64_t)t * xs_t;
+    const __bf16 *wr = w + (int64_t)o * n_in;
+    const float *br = a ? b + dir * b_stride : nullptr;
+    float prod = 0.f, dot = 0.f;
+    for (int k = 0; k < n_in; ++k) {
+        const float xv = (float)xr[k];
+        prod += xv * (float)wr[k];
+        if (br) dot += xv * bfr(br[k]);
+    }
+    float v = bfr(prod);
+    if (a) v += sign[m] * bfr(dot) * a[dir * a_stride + o];
+    y[i] = v;
 }
 
 }  // namespace
@@ -330,7 +377,7 @@ extern "C" int noise_lowrank_embed(float *out, const float *w, int64_t vocab, in
     hipLaunchKernelGGL(lowrank_embed_kernel, dim3((unsigned)((total / 4 + 255) / 256)), dim3(256), 0,
                        (hipStream_t)stream, out, w, idx, (int)pop->tokens, (int)width, noisy ? r1->a : nullptr,
                        noisy ? r1->b : nullptr, noisy ? r1->a_stride : 0, noisy ? r1->b_stride : 0, pop->sign,
-                       (int)pop->dir_div, total);
+                       (int)pop->dir_div, vocab, total);
     return launch_status(fn);
 }
 
@@ -407,5 +454,22 @@ extern "C" int noise_pop_gate(const noise_population_t *pop, noise_view_t x, con
                        pop->sign, noisy ? gate_noise->a : nullptr, noisy ? gate_noise->b : nullptr,
                        noisy ? gate_noise->a_stride : 0, noisy ? gate_noise->b_stride : 0, gates,
                        (int)(pop->rounding == NOISE_ROUNDING_EAGER));
+    return launch_status(fn);
+}
+
+extern "C" int noise_lowrank_rows(const noise_population_t *pop, noise_view_t x, int64_t n_in, const void *w,
+                                  int64_t n_out, const noise_rank1_t *r1, float *y, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_lowrank_rows";
+    NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
+    NOISE_CHECK_ARG(x.ptr && w && y && n_in > 0 && n_out > 0, "%s: NULL pointer or empty shape", fn);
+    NOISE_CHECK_ARG(pop->members * pop->tokens * n_out < (1ll << 38), "%s: output too large", fn);
+    const bool noisy = r1 && r1->a;
+    NOISE_CHECK_ARG(!noisy || (pop->sign && r1->b), "%s: noise needs sign and b rows", fn);
+    const int64_t total = pop->members * pop->tokens * n_out;
+    hipLaunchKernelGGL(lowrank_rows_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (int)pop->tokens, (int)n_in, (int)n_out, (int)pop->dir_div, (const __bf16 *)x.ptr, x.sm, x.st,
+                       (const __bf16 *)w, noisy ? r1->a : nullptr, noisy ? r1->b : nullptr,
+                       noisy ? r1->a_stride : 0, noisy ? r1->b_stride : 0, pop->sign, y, total);
     return launch_status(fn);
 }

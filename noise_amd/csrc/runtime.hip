@@ -17,6 +17,6 @@ void clear_error() { g_error[0] = '\0'; }
 
 }  // namespace noise
 
-extern "C" int noise_abi_version(void) { return 1; }
+extern "C" int noise_abi_version(void) { return 2; }
 
 extern "C" const char *noise_last_error(void) { return noise::g_error; }

@@ -56,8 +56,9 @@ def head_loss(x, weight, targets, vocab):
 def coordinate_differences(raw, y, sigma):
     """run.py:121-137: per token and logit, (loss(raw_j + sigma) - loss(raw_j - sigma)) / (2 sigma) of the
     soft-capped cross-entropy, in closed form; zero at ignored tokens (y < 0). raw [..., V] bf16 or fp32
-    (unit inner stride), y [...] int64 -> fp32 [..., V]."""
-    return head_error(raw, y, raw.shape[-1], sigma)
+    (unit inner stride), y [...] int64 -> fp32 [..., V]. Runs as torch.ops.noise_amd.coordinate_differences,
+    so the reference's @torch.compile caller (run.py:120) traces it."""
+    return torch.ops.noise_amd.coordinate_differences(raw, y, float(sigma))
 
 
 def head_error(logits, y, vocab, sigma=0.1):
@@ -84,6 +85,14 @@ def _bf16_weight(t):
 
 
 def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=None):
+    """run.py:102-117 `block_forward(x, w, ve, cos, sin, window, o, attn, fc, mlp)` through the registered op
+    torch.ops.noise_amd.block_forward (the reference compiles it, run.py:102): w is the reference's dict
+    q, k, v, gate, proj, fc, out."""
+    ws = [w.get(k) if k == 'gate' else w[k] for k in ('q', 'k', 'v', 'gate', 'proj', 'fc', 'out')]
+    return torch.ops.noise_amd.block_forward(x, ws, ve, cos, sin, int(window), o, attn, fc, mlp)
+
+
+def block_forward_eager(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=None):
     """run.py:102-117: Block.forward on x [B, T, 512] with optional jitter at o (attention output), attn
     (attn.c_proj product), fc (mlp.c_fc product, before ReLU^2) or mlp (mlp.c_proj product), each
     [B, T, width]. w: the reference's dict q, k, v, gate (None without value embeddings), proj, fc, out.
@@ -98,7 +107,7 @@ def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=No
     out = torch.empty(B, T, C, dtype=F32, device=dev)
     gate = w.get('gate')
     ws = [_bf16_weight(w['q']), _bf16_weight(w['k']), _bf16_weight(w['v']),
-          None if gate is None else gate.detach().to(F32).contiguous(),
+          None if gate is None else _bf16_weight(gate).to(F32).contiguous(),  # autocast rounds it to bf16 too
           _bf16_weight(w['proj']), _bf16_weight(w['fc']), _bf16_weight(w['out'])]
     wp = (ctypes.c_void_p * 7)(*[None if t is None else t.data_ptr() for t in ws])
     if ve is not None:

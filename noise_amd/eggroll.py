@@ -129,8 +129,10 @@ class Weights:
             self.lm_head3 = torch.empty(w.shape[0], 3 * w.shape[1], dtype=BF16, device=dev)
             _lib.call('noise_split3', w.data_ptr(), w.shape[0], w.shape[1], 0, 1, self.lm_head3.data_ptr(),
                       _lib.stream_ptr(dev))
-        lam = torch.stack([p['resid_lambdas'].detach().float().cpu(), p['x0_lambdas'].detach().float().cpu()])
-        self.resid_lambdas, self.x0_lambdas = lam[0].tolist(), lam[1].tolist()
+        # the mixing scalars stay on the device: the kernels read them there (a host copy would wait for the
+        # stream at every update)
+        self.resid_lambdas = g('resid_lambdas').to(F32).contiguous()
+        self.x0_lambdas = g('x0_lambdas').to(F32).contiguous()
         self.blocks = []
         for i in range(n_layer):
             pre = f'transformer.h.{i}.'
@@ -143,6 +145,14 @@ class Weights:
                 blk['ve'] = g(f'value_embeds.{i}.weight').to(F32).contiguous()
             self.blocks.append(blk)
         self.windows = window_sizes(n_layer)
+
+    def lam_r(self, i):
+        """Device address of resid_lambdas[i] (fp32)."""
+        return self.resid_lambdas.data_ptr() + 4 * i
+
+    def lam_x(self, i):
+        """Device address of x0_lambdas[i] (fp32)."""
+        return self.x0_lambdas.data_ptr() + 4 * i
 
 
 class _Buffers:
@@ -233,8 +243,8 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     # per-member token rows go through as one sequence of m * T tokens: the entry is token-local)
     emb_r1 = _rank1(emb)
     embed_pop = _lib.Population(1, m * T, None, 1, rounding) if rows_in else pop
-    _call('noise_pop_embed', ctypes.byref(embed_pop), 1 if noisy_entry else 0, W.wte.data_ptr(), idx.data_ptr(),
-              ctypes.byref(emb_r1), W.resid_lambdas[0], W.x0_lambdas[0],
+    _call('noise_pop_embed', ctypes.byref(embed_pop), 1 if noisy_entry else 0, W.wte.data_ptr(), W.wte.shape[0],
+              idx.data_ptr(), ctypes.byref(emb_r1), W.lam_r(0), W.lam_x(0),
               None if eps_r is None else eps_r.data_ptr(), None if eps_x is None else eps_x.data_ptr(),
               0 if eps_r is None and eps_x is None else (eps_r if eps_r is not None else eps_x).stride(0),
               B.x0.data_ptr(), B.xin0.data_ptr(), B.h0.data_ptr(), stream)
@@ -281,7 +291,8 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
                   cos_t.data_ptr(), sin_t.data_ptr(), qkv_out, stream)
         else:
             _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
-                  sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, idx.data_ptr(), idx_sm,
+                  sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None,
+                  blk['ve'].shape[0] if 've' in blk else 0, idx.data_ptr(), idx_sm,
                   B.gates.data_ptr() if 've' in blk else None, ctypes.byref(ve_r1), qkv_out, stream)
         # attention; its epilogue also forms y . b_o per head for c_proj's rank-1 term
         no = nz(pre + 'attn.c_proj.weight')
@@ -301,7 +312,7 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
         xres = _view(B.xin0, sm_e, E) if i == 0 else _view(B.resid, T * E, E)
         nxt = dot_vecs([nfc], E) if nfc is not None else None
         _call('noise_pop_residual', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), E, ctypes.byref(o_r1),
-                  B.d_attn.data_ptr(), N_HEAD, N_HEAD, xres, B.resid.data_ptr(), 0, 0.0, 0.0, None, None, 0,
+                  B.d_attn.data_ptr(), N_HEAD, N_HEAD, xres, B.resid.data_ptr(), 0, None, None, None, None, 0,
                   _view(B.x0, sm_e, E), B.h.data_ptr(), 0, nxt, 1 if nfc is not None else 0,
                   B.d_fc.data_ptr(), stream, label='attn.c_proj')
         # mlp.c_fc, ReLU^2; partial dots for mlp.c_proj
@@ -319,14 +330,14 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
             nxt, nnext, ndots = (dot_vecs(nn, E), 3, B.d_qkv.data_ptr()) if want else (None, 0, None)
             _call('noise_pop_residual', popp, _view(B.act, T * 4 * E, 4 * E), blk['mp'].data_ptr(), 4 * E,
                   ctypes.byref(mp_r1), B.d_mp.data_ptr(), 16, 16, _view(B.resid, T * E, E), B.resid.data_ptr(),
-                  1, W.resid_lambdas[i + 1], W.x0_lambdas[i + 1], eps_ptr(eps_r, i + 1), eps_ptr(eps_x, i + 1),
+                  1, W.lam_r(i + 1), W.lam_x(i + 1), eps_ptr(eps_r, i + 1), eps_ptr(eps_x, i + 1),
                   eps_stride, _view(B.x0, sm_e, E), B.h.data_ptr(), 0, nxt, nnext, ndots, stream, label='mlp.c_proj')
         else:
             nh = nz('lm_head.weight')
             nxt, nnext, ndots = (dot_vecs([nh], E), 1, B.d_head.data_ptr()) if nh is not None else (None, 0, None)
             hout = B.h3 if W.fp32_head else B.h
             _call('noise_pop_residual', popp, _view(B.act, T * 4 * E, 4 * E), blk['mp'].data_ptr(), 4 * E,
-                  ctypes.byref(mp_r1), B.d_mp.data_ptr(), 16, 16, _view(B.resid, T * E, E), None, 0, 0.0, 0.0,
+                  ctypes.byref(mp_r1), B.d_mp.data_ptr(), 16, 16, _view(B.resid, T * E, E), None, 0, None, None,
                   None, None, 0, _view(B.x0, sm_e, E), hout.data_ptr(), 1 if W.fp32_head else 0, nxt, nnext,
                   ndots, stream, label='mlp.c_proj')
     nh = nz('lm_head.weight')
@@ -345,11 +356,33 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
 
 
 def population_loss(model, p, noise, sign, idx, targets, dir_div=1, fp32_head=False):
-    """eggroll.py:66-103 `population_loss(model, p, noise, sign, idx, targets)` on the GPU.
+    """eggroll.py:66-103 `population_loss(model, p, noise, sign, idx, targets)` on the GPU: the mean
+    cross-entropy [m] of m perturbed models on one sequence.
 
-    noise values may be per member (dir_div = 1, as the reference passes them after repeat_interleave)
-    or per direction with dir_div = 2 (member m uses row m // 2)."""
-    W = Weights(p, fp32_head=fp32_head, n_layer=model.config.n_layer if model is not None else 8)
+    p: parameters by name; noise: name -> (a, b) for matrices and embeddings, or eps [m, L] for the mixing
+    scalars (names absent from noise are unperturbed). noise values may be per member (dir_div = 1, as the
+    reference passes them after repeat_interleave(2), eggroll.py:141) or per direction with dir_div = 2
+    (member m uses row m // 2). The call goes through the registered op torch.ops.noise_amd.population_loss,
+    so it also runs behind the reference's `torch.compile(population_loss)` (eggroll.py:115) and under its
+    autocast (eggroll.py:144)."""
+    names = list(p.keys())
+    noise_a, noise_b = [], []
+    for n in names:
+        v = noise.get(n)
+        if isinstance(v, (tuple, list)):
+            noise_a.append(v[0])
+            noise_b.append(v[1])
+        else:
+            noise_a.append(v)
+            noise_b.append(None)
+    n_layer = model.config.n_layer if model is not None else 8
+    return torch.ops.noise_amd.population_loss('\n'.join(names), [p[n] for n in names], noise_a, noise_b, sign,
+                                               idx, targets, n_layer, dir_div, fp32_head)
+
+
+def population_loss_eager(p, noise, sign, idx, targets, n_layer=8, dir_div=1, fp32_head=False):
+    """The op behind population_loss: device weights from p, then the fused forward."""
+    W = Weights(p, fp32_head=fp32_head, n_layer=n_layer)
     return population_forward(W, noise, sign, idx, targets, dir_div=dir_div)
 
 
@@ -358,49 +391,75 @@ def _pop(m, T, sign, dir_div):
 
 
 def lowrank(x, weight, a, b, sign, dir_div=1):
+    """eggroll.py:56-58 `lowrank(x, weight, a, b, sign)`: lowrank_eager through the registered op
+    torch.ops.noise_amd.lowrank, so compiled callers trace it."""
+    return torch.ops.noise_amd.lowrank(x, weight, a, b, sign, dir_div)
+
+
+def lowrank_eager(x, weight, a, b, sign, dir_div=1):
     """eggroll.py:56-58: x [m, T, in] through W [out, in] + sign * a b^T per member, never materialised.
 
-    a [dirs, out], b [dirs, in] fp32 rows, member m uses row m // dir_div; sign [m]. x may broadcast over
-    members (stride 0 in dim 0): then x W^T is computed once and the rank-1 terms are streamed out.
-    Returns fp32 [m, T, out] (the reference's autocast promotion of the bf16 product plus the fp32
-    correction). in must be a multiple of 512, out of 256, T of 256."""
+    a [dirs, out], b [dirs, in] fp32 rows, member m uses row m // dir_div; sign [m]. Returns fp32
+    [m, T, out] in autocast's form (the reference calls it under torch.autocast, eggroll.py:144): the
+    product x W^T and the dot x . b are bf16, the rank-1 term is added in fp32. Any shape is served: in a
+    multiple of 512 with out and T multiples of 256 run on the MFMA tiles (x broadcast over members, stride 0
+    in dim 0, is multiplied once and the rank-1 terms streamed out); other shapes, such as the value-embedding
+    gate's [8, 32] weight on h[..., :32] (eggroll.py:88), on noise_lowrank_rows. x may be a strided view."""
     m, T, n_in = x.shape
     n_out = weight.shape[0]
     dev = x.device
-    if n_in % 512 or n_out % 256 or T % 256:
-        raise ValueError(f'lowrank: need in % 512 == 0, out % 256 == 0, T % 256 == 0; got {tuple(x.shape)} x {tuple(weight.shape)}')
+    if weight.shape[1] != n_in or a.shape[-1] != n_out or b.shape[-1] != n_in or sign.shape[0] != m:
+        raise ValueError(f'lowrank: x {tuple(x.shape)}, weight {tuple(weight.shape)}, a {tuple(a.shape)}, '
+                         f'b {tuple(b.shape)} and sign {tuple(sign.shape)} do not agree')
+    if a.shape[0] * dir_div < m or b.shape[0] * dir_div < m:
+        raise ValueError(f'lowrank: {a.shape[0]} noise rows cannot serve {m} members at dir_div {dir_div}')
     sign = sign.to(device=dev, dtype=F32).contiguous()
-    a = a if (a.dtype == F32 and a.stride(-1) == 1 and a.data_ptr() % 16 == 0 and a.stride(0) % 4 == 0) else a.float().contiguous()
-    b = b if (b.dtype == F32 and b.stride(-1) == 1 and b.data_ptr() % 16 == 0 and b.stride(0) % 4 == 0) else b.float().contiguous()
+    ok = lambda t: t.dtype == F32 and t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and t.stride(0) % 4 == 0
+    a = a if ok(a) else a.float().contiguous()
+    b = b.to(BF16).to(F32).contiguous()   # autocast rounds b to bf16 for the x . b matmul
     r1 = _rank1((a, b))
     stream = _lib.stream_ptr(dev)
+    w = weight.to(device=dev, dtype=BF16).contiguous()
     shared = x.stride(0) == 0
-    xb = x[:1] if shared else x
-    xb = xb.to(BF16)
+    xb = (x[:1] if shared else x).to(BF16)
+    pop = _pop(m, T, sign, dir_div)
+    y = torch.empty(m, T, n_out, dtype=F32, device=dev)
+    if n_in % 512 or n_out % 256 or T % 256:
+        # shapes outside the MFMA tiles: one thread per output element
+        if xb.stride(-1) != 1:
+            xb = xb.contiguous()
+        _lib.call('noise_lowrank_rows', ctypes.byref(pop), _lib.View(xb.data_ptr(), 0 if shared else xb.stride(0),
+                                                                      xb.stride(1)),
+                  n_in, w.data_ptr(), n_out, ctypes.byref(r1), y.data_ptr(), stream)
+        return y
     if xb.stride(-1) != 1 or xb.stride(1) % 8 or xb.data_ptr() % 16 or (not shared and xb.stride(0) % 8):
         xb = xb.contiguous()
     xs_m = 0 if shared else xb.stride(0)
-    w = weight.to(device=dev, dtype=BF16).contiguous()
-    pop = _pop(m, T, sign, dir_div)
     dots = torch.empty(m * T, dtype=F32, device=dev)
     _lib.call('noise_member_dots', ctypes.byref(pop), _lib.View(xb.data_ptr(), xs_m, xb.stride(1)), n_in,
               ctypes.byref(r1), 1, dots.data_ptr(), stream)
-    y = torch.empty(m, T, n_out, dtype=F32, device=dev)
     if shared:
         base = torch.empty(1, T, n_out, dtype=F32, device=dev)
         one = _pop(1, T, None, 1)
         _lib.call('noise_pop_linear', ctypes.byref(one), _lib.View(xb.data_ptr(), 0, xb.stride(1)), w.data_ptr(),
-                  n_in, n_out, None, None, base.data_ptr(), 1, T * n_out, n_out, stream)
+                  n_in, n_out, None, None, base.data_ptr(), _lib.LINEAR_AUTOCAST, T * n_out, n_out, stream)
         _lib.call('noise_rank1_expand', ctypes.byref(pop), base.data_ptr(), n_out, dots.data_ptr(), ctypes.byref(r1),
-                  y.data_ptr(), 1, stream)
+                  y.data_ptr(), _lib.LINEAR_AUTOCAST, stream)
     else:
         _lib.call('noise_pop_linear', ctypes.byref(pop), _lib.View(xb.data_ptr(), xs_m, xb.stride(1)), w.data_ptr(),
-                  n_in, n_out, ctypes.byref(r1), dots.data_ptr(), y.data_ptr(), 1, T * n_out, n_out, stream)
+                  n_in, n_out, ctypes.byref(r1), dots.data_ptr(), y.data_ptr(), _lib.LINEAR_AUTOCAST, T * n_out,
+                  n_out, stream)
     return y
 
 
 def lowrank_embed(weight, a, b, idx, sign, dir_div=1):
-    """eggroll.py:61-63: embedding rows of W [V, d] + sign * a b^T for token ids idx [T] -> fp32 [m, T, d]."""
+    """eggroll.py:61-63 `lowrank_embed(weight, a, b, idx, sign)` through the registered op."""
+    return torch.ops.noise_amd.lowrank_embed(weight, a, b, idx, sign, dir_div)
+
+
+def lowrank_embed_eager(weight, a, b, idx, sign, dir_div=1):
+    """eggroll.py:61-63: embedding rows of W [V, d] + sign * a b^T for token ids idx [T] -> fp32 [m, T, d]
+    (an id outside [0, V) gives a NaN row)."""
     dev = weight.device
     V, d = weight.shape
     m, T = sign.shape[0], idx.shape[0]

@@ -114,12 +114,21 @@ class GPT(nn.Module):
         for blk in self.transformer.h:
             if blk.attn.ve_gate is not None:
                 nn.init.zeros_(blk.attn.ve_gate.weight)
+        if self.transformer.wte.weight.device.type == 'cuda':
+            # on a GPU the token and value embeddings are stored in bf16 (model.py:171-175)
+            for emb in self._embeddings():
+                emb.to(dtype=BF16)
+
+    def _embeddings(self):
+        return [self.transformer.wte, *self.value_embeds.values()]
 
 
-def make_model(device='cpu', seed=0):
-    """The training scripts' model (eggroll.py:38-53, run.py:545-557): seeded init_weights, then the
-    output projections (every '*c_proj' Linear, in module order) re-drawn U(+-1.5 sqrt(3 / fan_in));
-    embeddings kept in fp32. Built on `device` (CPU: torch's CPU generator)."""
+def make_model(device='cpu', seed=0, fp32_embeddings=True):
+    """The training scripts' model: seeded init_weights, then the output projections (every '*c_proj'
+    Linear, in module order) re-drawn U(+-1.5 sqrt(3 / fan_in)). Built on `device` with that device's
+    generator. fp32_embeddings=True is EGGROLL's make_model (eggroll.py:38-53): the embeddings are cast to
+    fp32 for the ES updates, so on a GPU they hold init_weights' bf16-rounded values; False is DUST's
+    (run.py:545-557), which keeps the GPU's bf16 storage. On the CPU the embeddings are fp32 either way."""
     torch.manual_seed(seed)
     with torch.device('meta'):
         model = GPT(GPTConfig())
@@ -130,6 +139,9 @@ def make_model(device='cpu', seed=0):
             if 'c_proj' in name and isinstance(module, nn.Linear):
                 bound = 1.5 * (3 / module.weight.shape[1]) ** 0.5
                 nn.init.uniform_(module.weight, -bound, bound)
+    if fp32_embeddings:
+        for emb in model._embeddings():
+            emb.float()
     return model.requires_grad_(False)
 
 

@@ -14,6 +14,9 @@ Run: python tests/golden/make_reference_fixtures.py   (about a minute: Inductor 
 import hashlib
 import importlib.util
 import sys
+
+# importing the reference must not write bytecode caches into its (read-only) tree
+sys.dont_write_bytecode = True
 from pathlib import Path
 
 import numpy as np

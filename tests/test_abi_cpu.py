@@ -37,7 +37,7 @@ def test_every_declared_symbol_has_a_ctypes_signature():
 
 
 def test_abi_version(lib):
-    assert lib.noise_abi_version() == 1
+    assert lib.noise_abi_version() == 2
 
 
 def _err(lib):
@@ -62,6 +62,18 @@ def test_invalid_arguments_return_einval(lib):
     assert st == -1 and 'multiple of 256' in _err(lib)
     # missing population
     st = lib.noise_member_mean(None, 0, 10, None, None)
+    assert st == -1
+    # embedding entry: a vocabulary size is required (ids outside it become NaN rows on the device)
+    pop = _lib.Population(2, 256, None, 1)
+    st = lib.noise_pop_embed(ctypes.byref(pop), 0, 16, 0, 16, None, 16, 16, None, None, 0, 16, 16, 16, None)
+    assert st == -1 and 'vocab' in _err(lib)
+    # residual writer: mixing needs the device addresses of the mixing scalars
+    st = lib.noise_pop_residual(ctypes.byref(pop), _lib.View(16, 0, 512), 16, 512, None, None, 0, 0,
+                                _lib.View(16, 0, 512), None, 1, None, None, None, None, 0, _lib.View(16, 0, 512), 16,
+                                0, None, 0, None, None)
+    assert st == -1 and 'lam_r' in _err(lib)
+    # generic lowrank: empty shapes rejected
+    st = lib.noise_lowrank_rows(ctypes.byref(pop), _lib.View(16, 0, 32), 0, 16, 8, None, 16, None)
     assert st == -1
 
 

@@ -45,7 +45,7 @@ def _run(m, T, dirs, perturbed, seed):
                       sin.data_ptr(), op, stream)
         else:
             _lib.call('noise_pop_qkv', ctypes.byref(pop), _lib.View(x.data_ptr(), 0, 512), wp, r1, dots.data_ptr(),
-                      cos.data_ptr(), sin.data_ptr(), None, None, 0, None, None, op, stream)
+                      cos.data_ptr(), sin.data_ptr(), None, 0, None, 0, None, None, op, stream)
         torch.cuda.synchronize()
         outs.append(qkv.float().cpu())
     return outs
