@@ -295,6 +295,20 @@ int noise_dust_block(const float *x, float *x_out, int64_t sequences, int64_t to
                      const void *jit_attn, const void *jit_fc, const void *jit_mlp, void *workspace,
                      int64_t workspace_bytes, noise_stream_t stream);
 
+/* noise_dust_block without a workspace argument and without any allocation: the intermediates live in a
+ * static device array of the library (64 MiB per GPU, held until the process ends; its size is
+ * noise_dust_block_static_max_bytes()). No counterpart in the reference: it is for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc. Inputs whose
+ * noise_dust_block_workspace_bytes exceed the array are rejected with NOISE_EINVAL (about 4,000 sequence
+ * tokens with value embeddings, e.g. 2 sequences of 2048). All calls on one GPU share that GPU's array:
+ * calls that overlap on one GPU (other streams, other host threads) race and must be ordered by the caller.
+ * Same arguments and results as noise_dust_block otherwise. */
+int64_t noise_dust_block_static_max_bytes(void);
+int noise_dust_block_static(const float *x, float *x_out, int64_t sequences, int64_t tokens, const void *const w[7],
+                            const void *ve, const void *rope_cos, const void *rope_sin, int64_t window,
+                            const void *jit_o, const void *jit_attn, const void *jit_fc, const void *jit_mlp,
+                            noise_stream_t stream);
+
 /* ---- EGGROLL update reassembly (eggroll.py:151-163) ---------------------------------------------------- */
 
 /* Fitness weights (eggroll.py:151-154): f_i = losses[2i+1] - losses[2i] (i < members/2),

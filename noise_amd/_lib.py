@@ -42,12 +42,14 @@ SIGNATURES = {
     'noise_draw_errors': [_p, _p, _i64, _i64, _i64, _f32, _p, _p],
     'noise_dust_block_workspace_bytes': [_i64, _i64, _i32],
     'noise_dust_block': [_p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p],
+    'noise_dust_block_static_max_bytes': [],
+    'noise_dust_block_static': [_p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p],
     'noise_update_weights': [_p, _i64, _i64, _p, _p],
     'noise_update_workspace_bytes': [_p, _i32, _i64, _i64],
     'noise_update_gradients': [_p, _i32, _i64, _p, _f32, _i64, _i64, _u64, _u64, _i64, _p, _p, _i64, _p],
 }
 _RESTYPES = {'noise_last_error': ctypes.c_char_p, 'noise_update_workspace_bytes': ctypes.c_int64,
-             'noise_dust_block_workspace_bytes': ctypes.c_int64}
+             'noise_dust_block_workspace_bytes': ctypes.c_int64, 'noise_dust_block_static_max_bytes': ctypes.c_int64}
 
 # y_fp32 of noise_pop_linear / noise_rank1_expand: fp32 output in autocast's form (bf16 product and dot)
 LINEAR_AUTOCAST = 2
