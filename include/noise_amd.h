@@ -280,6 +280,14 @@ int noise_coordinate_differences(const void *raw, int raw_bf16, int64_t rows, in
 int noise_draw_errors(const float *reward, const void *a, int64_t n, int64_t rows, int64_t d, float scale,
                       float *errors, noise_stream_t stream);
 
+/* DUST.rerun's glue between blocks (run.py:262-268) over rows of width 512, fp32:
+ *   x0 == NULL: out[r] = norm(x[r mod x_rows] + add[r]) (add bf16 [rows][512] or NULL): the jittered embedding
+ *               entry x = x0 = norm(embedding.repeat(n) + jitter) (run.py:262-263);
+ *   x0 != NULL: out[r] = rl * x[r mod x_rows] + ml * x0[r mod x0_rows], rl = *lam_r, ml = *lam_x read on the
+ *               device: the mixing of the blocks after the entry (run.py:267-268), x0 repeated by indexing. */
+int noise_rerun_rows(const float *x, int64_t x_rows, const void *add, const float *x0, int64_t x0_rows,
+                     const float *lam_r, const float *lam_x, int64_t rows, float *out, noise_stream_t stream);
+
 /* DUST's block_forward (run.py:102-117) over `sequences` rows of `tokens` (a multiple of 256) tokens: the fixed
  * model's block (utils/model.py:103-110) on x fp32 [sequences][tokens][512] -> x_out fp32 (same layout), with
  * the weights unperturbed and optional jitter, bf16 [sequences][tokens][width] or NULL, added where the

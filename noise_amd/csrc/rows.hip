@@ -473,3 +473,57 @@ extern "C" int noise_lowrank_rows(const noise_population_t *pop, noise_view_t x,
                        noisy ? r1->a_stride : 0, noisy ? r1->b_stride : 0, pop->sign, y, total);
     return launch_status(fn);
 }
+
+namespace noise {
+namespace {
+
+// DUST.rerun's glue between blocks (run.py:262-268), over rows of 512 (one wave per row):
+//   entry (x0 == NULL): out[r] = norm(e[r % e_rows] (+ add[r]))      the jittered embedding entry
+//   mix   (x0 != NULL): out[r] = rl * x[r] + ml * x0[r % x0_rows]     the next block's mixing scalars
+// e / x fp32, add bf16 or NULL, x0 fp32; rl, ml read on the device.
+__global__ __launch_bounds__(256) void rerun_rows_kernel(const float *x, int64_t x_rows, const __bf16 *add,
+                                                         const float *x0, int64_t x0_rows, const float *lam_r,
+                                                         const float *lam_x, int64_t rows, float *out) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float v[8];
+    ld8(x + (row % x_rows) * 512 + lane * 8, v);
+    if (x0) {
+        const float rl = *lam_r, ml = *lam_x;
+        float z[8];
+        ld8(x0 + (row % x0_rows) * 512 + lane * 8, z);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = rl * v[i] + ml * z[i];
+    } else {
+        if (add) {
+            const bf16x8 a = load_bf16x8(add + row * 512 + lane * 8);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) v[i] += (float)a[i];
+        }
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+        const float r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] *= r;
+    }
+    st8(out + row * 512 + lane * 8, v);
+}
+
+}  // namespace
+}  // namespace noise
+
+extern "C" int noise_rerun_rows(const float *x, int64_t x_rows, const void *add, const float *x0, int64_t x0_rows,
+                                const float *lam_r, const float *lam_x, int64_t rows, float *out,
+                                noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_rerun_rows";
+    NOISE_CHECK_ARG(x && out && rows > 0 && x_rows > 0 && aligned(x, 16) && aligned(out, 16), "%s: bad x / out", fn);
+    NOISE_CHECK_ARG(!add || aligned(add, 16), "%s: add must be 16 B aligned", fn);
+    NOISE_CHECK_ARG(!x0 || (x0_rows > 0 && aligned(x0, 16) && lam_r && lam_x && !add),
+                    "%s: mixing needs x0 rows, both lambdas and no add", fn);
+    hipLaunchKernelGGL(rerun_rows_kernel, dim3(rows_grid(rows)), dim3(256), 0, (hipStream_t)stream, x, x_rows,
+                       (const __bf16 *)add, x0, x0_rows, lam_r, lam_x, rows, out);
+    return launch_status(fn);
+}

@@ -2,6 +2,7 @@
 
   head_loss(x, weight, targets, vocab)      run.py:89-94, the fp32 head of rerun (run.py:273-278)
   block_forward(x, w, ve, cos, sin, window, o, attn, fc, mlp)   run.py:102-117
+  rerun(dust, n, entry, jitter)             run.py:256-279 (DUST.rerun)
   draw_errors(errors, reward, a, sigma)     run.py:351-355 (direct_errors' estimate update)
   coordinate_differences(raw, y, sigma)     run.py:121-137
   head_error(logits, y, vocab, sigma)       run.py:380-389
@@ -139,3 +140,62 @@ def draw_errors(errors, reward, a, sigma):
     _lib.call('noise_draw_errors', r.data_ptr(), av.data_ptr(), n, rows, d, -1.0 / float(sigma), errors.data_ptr(),
               _lib.stream_ptr(errors.device))
     return errors
+
+
+# jitter sites of a block (run.py:97-98): block_forward keyword -> the reference's site name
+SITES = {'o': 'o@{}', 'attn': 'transformer.h.{}.attn.c_proj', 'fc': 'transformer.h.{}.mlp.c_fc',
+         'mlp': 'transformer.h.{}.mlp.c_proj'}
+
+
+def _rotary(model, T, dev):
+    """The model's bf16 rotary tables for T tokens (utils/model.py:144-147 buffers when the model has them)."""
+    if hasattr(model, 'cos'):
+        return model.cos[:, :T], model.sin[:, :T]
+    from .model import rotary_tables
+    cos, sin = rotary_tables(T)
+    return cos.bfloat16().to(dev), sin.bfloat16().to(dev)
+
+
+def rerun(dust, n, entry, jitter):
+    """DUST.rerun (run.py:256-279) with the same arguments and state: the per-token losses [n, batch, length]
+    of n jittered draws, rerun from block `entry` (None: from the embedding).
+
+    `dust` carries what the reference's DUST object holds after capture: model (resid_lambdas, x0_lambdas,
+    window_sizes, lm_head, config), length, batch, outputs ('transformer.wte' and 'value_embeds.{i}' outputs),
+    blocks (block inputs by layer), x0 (the normed embedding), y (targets) and weights (the per-block dicts of
+    run.py:172-175). jitter: site name -> [n * batch, length, width] (sigma * draws). The chain: the cached
+    input repeated n times (or the jittered embedding entry, normed), each later block's mixing, block_forward
+    with the entry block's jitter sites, then the final norm and the fp32 head (head_loss, split-bf16x3)."""
+    model = dust.model
+    T, b = dust.length, dust.batch
+    dev = dust.y.device
+    stream = _lib.stream_ptr(dev)
+    rows = n * b * T
+    L = model.config.n_layer
+    lam_r = model.resid_lambdas.detach().to(F32).contiguous()
+    lam_x = model.x0_lambdas.detach().to(F32).contiguous()
+    if entry is None:
+        emb = dust.outputs['transformer.wte'].detach().to(F32).contiguous()
+        add = jitter.get('transformer.wte')
+        add = None if add is None else add.reshape(n * b, T, -1).to(BF16).contiguous()
+        x = torch.empty(n * b, T, 512, dtype=F32, device=dev)
+        _lib.call('noise_rerun_rows', emb.data_ptr(), b * T, _lib.ptr(add), None, 0, None, None, rows, x.data_ptr(),
+                  stream)
+        x0, x0_rows = x, rows
+    else:
+        x = dust.blocks[entry].detach().to(F32).repeat(n, 1, 1).contiguous()
+        x0 = dust.x0.detach().to(F32).contiguous()
+        x0_rows = b * T
+    cos, sin = _rotary(model, T, dev)
+    for i in range(entry or 0, L):
+        if entry is None or i > entry:
+            xm = torch.empty_like(x)
+            _lib.call('noise_rerun_rows', x.data_ptr(), rows, None, x0.data_ptr(), x0_rows, lam_r.data_ptr() + 4 * i,
+                      lam_x.data_ptr() + 4 * i, rows, xm.data_ptr(), stream)
+            x = xm
+        ve = dust.outputs.get(f'value_embeds.{i}')
+        ve = None if ve is None else ve.detach().repeat(n, 1, 1)
+        sites = {key: jitter.get(site.format(i)) for key, site in SITES.items()} if i == entry else {}
+        x = block_forward_eager(x, dust.weights[i], ve, cos, sin, model.window_sizes[i][0], **sites)
+    loss = head_loss(x, model.lm_head.weight.detach().float(), dust.y.repeat(n, 1), model.config.vocab_size)
+    return loss.view(n, b, T)

@@ -1,4 +1,4 @@
-"""ORACLE (test infrastructure only): DUST's head error on the CPU.
+"""ORACLE (test infrastructure only): DUST's head error, block_forward, capture cache and rerun on the CPU.
 
 Restates train/val/run.py:121-137 (coordinate_differences) and run.py:380-389 (head_error) in float64
 numpy: z = 15 tanh(raw / 15), the moved logits z' = cap(raw +- sigma), w = softmax(z), and
@@ -62,3 +62,59 @@ def draw_errors(errors, reward, a, sigma):
     n = reward.shape[0]
     e = np.einsum('nbt,nbtd->btd', bf(reward), np.asarray(a, dtype=np.float64).reshape(n, *errors.shape))
     return np.asarray(errors, dtype=np.float64) - bf(e) / sigma
+
+
+def capture(P, idx):
+    """What DUST.capture (run.py:247-254) caches from the clean forward of GPT.forward (utils/model.py:193-209),
+    in fp32 on the CPU: the embedding output, every block's input (after its mixing), x0 = norm(embedding) and
+    the value-embedding outputs. idx [b, T]."""
+    from .model import norm, has_ve, rotary_tables, window_sizes, N_LAYER
+    T = idx.shape[1]
+    cos, sin = rotary_tables(T)
+    wins = window_sizes()   # the model's windows (sequence_len 2048), whatever T is
+    emb = P['transformer.wte.weight'][idx].float()
+    outputs = {'transformer.wte': emb}
+    x = x0 = norm(emb)
+    blocks = {}
+    for i in range(N_LAYER):
+        x = P['resid_lambdas'][i] * x + P['x0_lambdas'][i] * x0
+        blocks[i] = x
+        ve = P[f'value_embeds.{i}.weight'][idx].float() if has_ve(i) else None
+        if ve is not None:
+            outputs[f'value_embeds.{i}'] = ve
+        x = block_forward(x, block_weights(P, i), ve, cos, sin, wins[i])
+    return dict(outputs=outputs, blocks=blocks, x0=x0)
+
+
+def block_weights(P, i):
+    """run.py:172-175's per-block dict of the fixed model's weights."""
+    pre = f'transformer.h.{i}.'
+    return dict(q=P[pre + 'attn.c_q.weight'], k=P[pre + 'attn.c_k.weight'], v=P[pre + 'attn.c_v.weight'],
+                gate=P.get(pre + 'attn.ve_gate.weight'), proj=P[pre + 'attn.c_proj.weight'],
+                fc=P[pre + 'mlp.c_fc.weight'], out=P[pre + 'mlp.c_proj.weight'])
+
+
+SITES = {'o': 'o@{}', 'attn': 'transformer.h.{}.attn.c_proj', 'fc': 'transformer.h.{}.mlp.c_fc',
+         'mlp': 'transformer.h.{}.mlp.c_proj'}
+
+
+def rerun(P, cache, y, n, entry, jitter):
+    """DUST.rerun (run.py:256-279) in fp32 on the CPU: per-token losses [n, b, T] of n jittered draws rerun
+    from block `entry` (None: from the embedding) over the captured cache, jitter: site -> [n*b, T, width]."""
+    from .model import norm, rotary_tables, window_sizes, head_loss, N_LAYER
+    b, T = y.shape
+    cos, sin = rotary_tables(T)
+    wins = window_sizes()
+    if entry is None:
+        x = x0 = norm(cache['outputs']['transformer.wte'].repeat(n, 1, 1) + jitter['transformer.wte'].float())
+    else:
+        x, x0 = cache['blocks'][entry].repeat(n, 1, 1), cache['x0'].repeat(n, 1, 1)
+    for i in range(entry or 0, N_LAYER):
+        if entry is None or i > entry:
+            x = P['resid_lambdas'][i] * x + P['x0_lambdas'][i] * x0
+        ve = cache['outputs'].get(f'value_embeds.{i}')
+        sites = {k: jitter.get(s.format(i)) for k, s in SITES.items()} if i == entry else {}
+        sites = {k: (None if v is None else v.float()) for k, v in sites.items()}
+        x = block_forward(x, block_weights(P, i), None if ve is None else ve.repeat(n, 1, 1), cos, sin, wins[i],
+                          **sites)
+    return head_loss(x, P['lm_head.weight'], y.repeat(n, 1)).view(n, b, T)

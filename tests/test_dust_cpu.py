@@ -124,3 +124,55 @@ def test_block_forward_jitter_placement():
     f1 = odust.block_forward(x, w, ve, cos, sin, 128, fc=norm(x_mid) @ D.t())
     f2 = odust.block_forward(x, dict(w, fc=w['fc'] + D), ve, cos, sin, 128)
     assert torch.allclose(f1, f2, rtol=0, atol=1e-4)
+
+
+def test_draw_errors_oracle_matches_the_reference_bf16_einsum():
+    """oracle/dust.py:draw_errors against run.py:351-355 written as the reference writes it, with torch's own
+    bf16 einsum on the CPU: errors[site] -= einsum('nbt,nbtd->btd', reward.to(bf16), a).float() / sigma.
+    The einsum accumulates in fp32 and rounds its result to bf16, the oracle sums in float64 and rounds: the two
+    agree exactly except where the sums straddle a bf16 rounding boundary (then by one ulp). Planting a
+    dropped rounding (the reward left in fp32) breaks the agreement, so the check discriminates."""
+    import torch
+    rng = np.random.default_rng(7)
+    n, b, t, d, sigma = 16, 2, 64, 32, 0.05
+    reward = rng.normal(0, 0.3, size=(n, b, t)).astype(np.float32)
+    a = torch.as_tensor(rng.choice([-1.0, 1.0], size=(n, b, t, d)).astype(np.float32)).bfloat16()
+    errors = rng.normal(0, 1, size=(b, t, d))
+    got = odust.draw_errors(errors, reward, a.float().numpy(), sigma)
+    ref = torch.as_tensor(errors) - torch.einsum('nbt,nbtd->btd', torch.as_tensor(reward).bfloat16(),
+                                                 a).double() / sigma
+    e_got = (errors - got) * sigma
+    e_ref = (errors - ref.numpy()) * sigma
+    ulp = np.abs(e_ref) * 2.0 ** -7 + 1e-12
+    assert (np.abs(e_got - e_ref) <= ulp).all()
+    assert np.mean(np.abs(e_got - e_ref) <= 1e-9) > 0.99
+    # mutation: without the reward's bf16 rounding the oracle would differ from the reference far more often
+    e_fp32 = np.einsum('nbt,nbtd->btd', reward.astype(np.float64), a.float().numpy().astype(np.float64))
+    e_fp32 = torch.as_tensor(e_fp32).float().bfloat16().double().numpy()
+    assert np.mean(np.abs(e_fp32 - e_ref) > 1e-9) > 0.2
+
+
+def test_rerun_oracle_reduces_to_the_clean_forward():
+    """oracle/dust.py:capture + rerun (run.py:247-279) pinned against GPT.forward's own per-token losses
+    (oracle/model.py:gpt_forward, itself pinned by the reference's outputs): with zero jitter every draw rerun
+    from any entry -- the embedding or a cached block input -- reproduces the clean losses; a jitter at the
+    entry block moves them."""
+    import torch
+    from noise_amd.model import make_model
+    from oracle import model as om
+    P = {k: v.float() for k, v in make_model('cpu', 0).state_dict().items()}
+    P['lm_head.weight'] = P['lm_head.weight'] * 30
+    g = torch.Generator().manual_seed(8)
+    rows = torch.randint(0, 4096, (2, 257), generator=g)
+    x, y = rows[:, :-1], rows[:, 1:]
+    clean = om.gpt_forward(P, x, y, reduction='none').view(2, 256)
+    cache = odust.capture(P, x)
+    n = 2
+    zero = {'transformer.wte': torch.zeros(n * 2, 256, 512)}
+    for entry in (None, 0, 5, 7):
+        got = odust.rerun(P, cache, y, n, entry, zero)
+        assert got.shape == (n, 2, 256)
+        assert (got - clean).abs().max().item() <= 1e-5, entry
+    jit = {'o@5': 0.05 * torch.randn(n * 2, 256, 512, generator=g)}
+    moved = odust.rerun(P, cache, y, n, 5, jit)
+    assert (moved - clean).abs().max().item() > 1e-3

@@ -134,3 +134,57 @@ def test_draw_errors_matches_oracle(d):
     step = np.abs(ref - errors.double().numpy()) * 2 ** -7 + 1e-6
     print('max abs err', float(np.abs(got - ref).max()), flush=True)
     assert np.all(np.abs(got - ref) <= step)
+
+
+@pytest.mark.parametrize('entry,site,width', [(None, 'transformer.wte', 512), (3, 'transformer.h.{}.mlp.c_fc', 2048),
+                                              (6, 'o@{}', 512), (7, 'transformer.h.{}.mlp.c_proj', 512)],
+                         ids=['embedding', 'fc-3', 'o-6', 'mlp-7'])
+def test_rerun_matches_oracle(entry, site, width):
+    """DUST.rerun (run.py:256-279) end to end -- the cached input repeated n times (or the jittered embedding
+    entry), the later blocks' mixing, block_forward with the entry's jitter, the final norm and fp32 head --
+    against the oracle rerun composed from the pinned pieces (oracle/dust.py), per draw and per token. The
+    capture cache comes from the oracle's clean forward. Head x30 so the losses depend on the blocks; sigma
+    0.1 (+-1 draws in bf16 as the reference's) so the jitter moves them visibly. Each draw's mean loss stays
+    within 1e-3 of the fp32 oracle, and so does the jitter's effect (rerun minus the unjittered rerun, the
+    reward DUST forms) per draw. Per token, bf16 products and attention through up to 8 blocks (the
+    reference's autocast numerics) put single tokens up to 2e-2 from fp32 (measured 1.95e-2 from the
+    embedding): the per-token bound is 3e-2."""
+    from types import SimpleNamespace
+    from noise_amd.dust import rerun
+    from noise_amd.model import make_model
+    model = make_model('cpu', 0)
+    with torch.no_grad():
+        model.lm_head.weight.mul_(30)
+    P = {k: v.detach().float().clone() for k, v in model.named_parameters()}
+    g = torch.Generator().manual_seed(31)
+    b, T, n = 2, 256, 3
+    rows = torch.randint(0, 4096, (b, T + 1), generator=g)
+    x, y = rows[:, :-1], rows[:, 1:]
+    cache = odust.capture(P, x)
+    name = site.format(entry) if entry is not None else site
+    draws = (torch.randint(0, 2, (n * b, T, width), generator=g) * 2 - 1).bfloat16()
+    jitter = {name: (0.1 * draws.float()).bfloat16()}
+    print(f'rerun: entry {entry}, jitter at {name}, {n} draws x {b} sequences x {T} tokens', flush=True)
+    ref = odust.rerun(P, cache, y, n, entry, jitter)
+    ref0 = odust.rerun(P, cache, y, n, entry, {})  if entry is not None else \
+        odust.rerun(P, cache, y, n, entry, {name: torch.zeros(n * b, T, width)})
+    dev = torch.device('cuda', 0)
+    m = model.to(dev)
+    to = lambda d: {k: v.to(dev) for k, v in d.items()}
+    dust = SimpleNamespace(model=m, length=T, batch=b, outputs=to(cache['outputs']),
+                           blocks=to(cache['blocks']), x0=cache['x0'].to(dev), y=y.to(dev),
+                           weights=[{k: (None if v is None else v.to(dev)) for k, v in odust.block_weights(P, i).items()}
+                                    for i in range(8)])
+    got = rerun(dust, n, entry, to(jitter)).cpu()
+    got0 = rerun(dust, n, entry, {} if entry is not None else {name: torch.zeros(n * b, T, width, device=dev)}).cpu()
+    assert got.shape == (n, b, T) and torch.isfinite(got).all()
+    tok = (got - ref).abs().max().item()
+    mean = (got.mean(-1) - ref.mean(-1)).abs().max().item()
+    eff = ((got - got0).mean(-1) - (ref - ref0).mean(-1)).abs().max().item()
+    print(f'rerun: per-token {tok:.2e}, per-draw mean {mean:.2e}, jitter effect {eff:.2e}, effect size '
+          f'{(ref - ref0).mean(-1).abs().max().item():.2e}', flush=True)
+    assert tok <= 3e-2
+    assert mean <= 1e-3
+    assert eff <= 1e-3
+    effect = (ref - ref0).mean(-1).abs().max().item()
+    assert effect > max(1e-4, 10 * eff), 'the jitter must move the losses well beyond the error'
