@@ -231,6 +231,29 @@ int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, const void 
                       const noise_rank1_t *r1, const float *dots, const int64_t *targets, int64_t targets_sm,
                       float *token_loss, noise_stream_t stream);
 
+/* The block's whole MLP with its residual writer (eggroll.py:93, then the next block's mixing, eggroll.py:77-79,
+ * and what noise_pop_residual derives from the new residual): with x = h (bf16, the norm of the block's mid
+ * residual) and per member m,
+ *   hid = relu(x w_fc^T + sign * dots_fc * a_fc)^2 (bf16),  y = xres + hid w_proj^T + sign * (hid . b_proj) * a_proj,
+ *   if mix: y = rl*y + ml*x0 (rl = *lam_r, ml = *lam_x, + sign * eps); xout = y (fp32, may equal xres, may be
+ *   NULL); hout = bf16(norm(y)) [m][T][512] or its [hi | lo | hi] split [m][T][1536] (split3);
+ *   next_dots[row*nnext + k] = norm(y) . next[k].b.
+ * The [m][T][2048] hidden layer never reaches memory. w_fc: mlp.c_fc bf16 [2048][512]; w_proj: mlp.c_proj bf16
+ * [512][2048] in the layout noise_mlp_proj_layout writes. r_fc: c_fc's rank-1 noise (a [dirs][2048]) with
+ * dots_fc = x . b_fc per row (noise_pop_residual's next dots); r_proj: mlp.c_proj's (a [dirs][512],
+ * b [dirs][2048]); NULL or a == NULL: unperturbed. tokens a multiple of 128; fused rounding only. Same results
+ * as noise_pop_fc followed by noise_pop_residual with K = 2048, up to fp32 summation order. */
+int noise_pop_mlp(const noise_population_t *pop, noise_view_t x, const void *w_fc, const noise_rank1_t *r_fc,
+                  const float *dots_fc, const void *w_proj, const noise_rank1_t *r_proj, noise_view_t xres, float *xout,
+                  int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+                  int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next, int64_t nnext,
+                  float *next_dots, noise_stream_t stream);
+
+/* mlp.c_proj [rows][2048] bf16 -> the column order noise_pop_mlp reads: within every 16 columns, the groups of
+ * 4 are stored in the order 0, 2, 1, 3 (so each 16-deep slice of the hidden layer pairs with the registers the
+ * c_fc product leaves it in). out and w distinct; one pass per weight update. */
+int noise_mlp_proj_layout(const void *w, void *out, int64_t rows, noise_stream_t stream);
+
 /* out[m] = mean over tokens of token_loss[m][:] (eggroll.py:102), deterministic order. */
 int noise_member_mean(const float *token_loss, int64_t members, int64_t tokens, float *out, noise_stream_t stream);
 

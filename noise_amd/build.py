@@ -30,9 +30,14 @@ def hipcc():
     return exe
 
 
+# per-source additions: the fused MLP kernel (one wave per SIMD, 512 registers) needs the scheduler that keeps
+# LDS fragment reads ahead of the matrix products; the default one serialises them at that register pressure
+EXTRA = {'mlp.hip': ['-mllvm', '-amdgpu-sched-strategy=max-ilp']}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ / (src.stem + '.o')
-    cmd = [hipcc(), *HIPFLAGS, '-c', str(src), '-o', str(obj)]
+    cmd = [hipcc(), *HIPFLAGS, *EXTRA.get(src.name, []), '-c', str(src), '-o', str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f'hipcc failed on {src.name}:\n{res.stderr[-8000:]}')

@@ -139,6 +139,10 @@ class Weights:
             blk = dict(q=bf(pre + 'attn.c_q.weight'), k=bf(pre + 'attn.c_k.weight'), v=bf(pre + 'attn.c_v.weight'),
                        o=bf(pre + 'attn.c_proj.weight'), fc=bf(pre + 'mlp.c_fc.weight'),
                        mp=bf(pre + 'mlp.c_proj.weight'))
+            # mlp.c_proj in the fused MLP kernel's column order
+            blk['mp_perm'] = torch.empty_like(blk['mp'])
+            _lib.call('noise_mlp_proj_layout', blk['mp'].data_ptr(), blk['mp_perm'].data_ptr(), blk['mp'].shape[0],
+                      _lib.stream_ptr(dev))
             if has_ve(i, n_layer):
                 # the gate's product runs under autocast: its weights enter rounded to bf16
                 blk['gate'] = bf(pre + 'attn.ve_gate.weight').to(F32).contiguous()
@@ -156,7 +160,7 @@ class Weights:
 
 
 class _Buffers:
-    def __init__(self, m, T, dev, fp32_head, per_member):
+    def __init__(self, m, T, dev, fp32_head, per_member, eager=False):
         rows = m * T
         e = m if per_member else 1
         self.x0 = torch.empty(e, T, N_EMBD, dtype=F32, device=dev)
@@ -166,14 +170,15 @@ class _Buffers:
         self.h = torch.empty(m, T, N_EMBD, dtype=BF16, device=dev)
         self.qkv = torch.empty(3, m, N_HEAD, T, HEAD_DIM, dtype=BF16, device=dev)
         self.y = torch.empty(m, T, N_EMBD, dtype=BF16, device=dev)
-        self.act = torch.empty(m, T, 4 * N_EMBD, dtype=BF16, device=dev)
+        # the MLP hidden layer: materialised only by the eager-rounding path (the fused MLP keeps it on chip)
+        self.act = torch.empty(m, T, 4 * N_EMBD, dtype=BF16, device=dev) if eager else None
         self.h3 = torch.empty(m, T, 3 * N_EMBD, dtype=BF16, device=dev) if fp32_head else None
         # block 0's shared q/k/v product when every member reads the same block input
         self.qkv_base = None if per_member else torch.empty(T, 3 * N_EMBD, dtype=F32, device=dev)
         self.d_qkv = torch.empty(rows, 3, dtype=F32, device=dev)
         self.d_attn = torch.empty(rows, N_HEAD, dtype=F32, device=dev)
         self.d_fc = torch.empty(rows, dtype=F32, device=dev)
-        self.d_mp = torch.empty(rows, 16, dtype=F32, device=dev)
+        self.d_mp = torch.empty(rows, 16, dtype=F32, device=dev) if eager else None
         self.d_head = torch.empty(rows, 1, dtype=F32, device=dev)
         self.gates = torch.empty(rows, N_HEAD, dtype=F32, device=dev)
         self.loss_tok = torch.empty(rows, dtype=F32, device=dev)
@@ -238,7 +243,8 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     if rows_in and noisy_entry:
         raise ValueError('per-member token rows need the embedding and mixing scalars unperturbed')
     per_member = noisy_entry or rows_in
-    B = buffers if buffers is not None else _Buffers(m, T, dev, W.fp32_head, per_member)
+    B = buffers if buffers is not None else _Buffers(m, T, dev, W.fp32_head, per_member,
+                                                     eager=rounding == _lib.ROUNDING_EAGER)
     # block 0 entry: embedding, norm, mix, norm (shared by every member when nothing there is perturbed;
     # per-member token rows go through as one sequence of m * T tokens: the entry is token-local)
     emb_r1 = _rank1(emb)
@@ -315,15 +321,33 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
                   B.d_attn.data_ptr(), N_HEAD, N_HEAD, xres, B.resid.data_ptr(), 0, None, None, None, None, 0,
                   _view(B.x0, sm_e, E), B.h.data_ptr(), 0, nxt, 1 if nfc is not None else 0,
                   B.d_fc.data_ptr(), stream, label='attn.c_proj')
-        # mlp.c_fc, ReLU^2; partial dots for mlp.c_proj
         fc_r1 = _rank1(nfc)
+        mp_r1 = _rank1(nmp)
+        last = i == L - 1
+        if rounding == _lib.ROUNDING_FUSED:
+            # the whole MLP and its residual writer in one kernel: the [m, T, 2048] hidden layer stays on chip;
+            # then the next block's mix, norm and q/k/v dots (or the head input)
+            if not last:
+                nn = qkv_noise(i + 1)
+                want = any(v is not None for v in nn)
+                nxt, nnext, ndots = (dot_vecs(nn, E), 3, B.d_qkv.data_ptr()) if want else (None, 0, None)
+                hout, split3 = B.h, 0
+                mixargs = (1, W.lam_r(i + 1), W.lam_x(i + 1), eps_ptr(eps_r, i + 1), eps_ptr(eps_x, i + 1), eps_stride)
+            else:
+                nh = nz('lm_head.weight')
+                nxt, nnext, ndots = (dot_vecs([nh], E), 1, B.d_head.data_ptr()) if nh is not None else (None, 0, None)
+                hout, split3 = (B.h3, 1) if W.fp32_head else (B.h, 0)
+                mixargs = (0, None, None, None, None, 0)
+            _call('noise_pop_mlp', popp, _view(B.h, T * E, E), blk['fc'].data_ptr(), ctypes.byref(fc_r1),
+                  B.d_fc.data_ptr(), blk['mp_perm'].data_ptr(), ctypes.byref(mp_r1), _view(B.resid, T * E, E),
+                  None if last else B.resid.data_ptr(), *mixargs, _view(B.x0, sm_e, E), hout.data_ptr(), split3,
+                  nxt, nnext, ndots, stream, label='mlp')
+            continue
+        # eager rounding: mlp.c_fc, ReLU^2 and partial dots for mlp.c_proj, then mlp.c_proj + residual
         mp_next = _rank1(nmp)
         _call('noise_pop_fc', popp, _view(B.h, T * E, E), blk['fc'].data_ptr(), ctypes.byref(fc_r1),
                   B.d_fc.data_ptr(), B.act.data_ptr(), ctypes.byref(mp_next) if nmp is not None else None,
                   B.d_mp.data_ptr(), stream)
-        # mlp.c_proj + residual; next block's mix, norm and q/k/v dots (or the head input)
-        mp_r1 = _rank1(nmp)
-        last = i == L - 1
         if not last:
             nn = qkv_noise(i + 1)
             want = any(v is not None for v in nn)

@@ -80,7 +80,7 @@ def score_rows(weights, rows, batch_size=16):
         batch = batch.to(dev)
         m = batch.shape[0]
         if m not in buffers:
-            buffers[m] = _Buffers(m, T, dev, weights.fp32_head, True)
+            buffers[m] = _Buffers(m, T, dev, weights.fp32_head, True, eager=True)
         sign = torch.zeros(m, dtype=F32, device=dev)
         loss = population_forward(weights, {}, sign, batch[:, :-1].contiguous(), batch[:, 1:].contiguous(),
                                   buffers=buffers[m], per_token=True, rounding=_lib.ROUNDING_EAGER)

@@ -91,7 +91,7 @@ def test_eager_rows_match_oracle(params):
     tgt[1, 100:140] = -1  # ignored targets contribute 0
     print('eval: 3 rows x 512 tokens, eager rounding', flush=True)
     W = load_model(params, DEV)
-    B = _Buffers(3, 512, DEV, False, True)
+    B = _Buffers(3, 512, DEV, False, True, eager=True)
     got = population_forward(W, {}, torch.zeros(3, device=DEV), idx.to(DEV), tgt.to(DEV), buffers=B,
                              per_token=True, rounding=_lib.ROUNDING_EAGER).cpu()
     want = om.gpt_forward_eager(params, idx, tgt, 'none').view(3, 512)
