@@ -84,6 +84,51 @@ def block_matrix_names():
             for s in ('attn.c_q', 'attn.c_k', 'attn.c_v', 'attn.c_proj', 'mlp.c_fc', 'mlp.c_proj')]
 
 
+def host_cpu():
+    """Model name, physical cores and hardware threads of this host (lscpu), for the CPU baselines."""
+    import subprocess
+    info = dict(model=None, physical_cores=None, threads=os.cpu_count())
+    try:
+        out = subprocess.run(['lscpu'], capture_output=True, text=True, timeout=10).stdout
+    except (OSError, subprocess.SubprocessError):
+        return info
+    kv = {}
+    for line in out.splitlines():
+        if ':' in line:
+            k, v = line.split(':', 1)
+            kv[k.strip()] = v.strip()
+    info['model'] = kv.get('Model name')
+    try:
+        info['physical_cores'] = int(kv['Core(s) per socket']) * int(kv['Socket(s)'])
+    except (KeyError, ValueError):
+        pass
+    return info
+
+
+def cpu_forward_config1(threads=None):
+    """The reference's CPU plumbing case: the fixed model's fp32 forward + mean next-token CE (the oracle's
+    restatement of utils/model.py:193-209) on a batch of 4 x 2048 tokens ~ U[0, 4096) from a CPU generator
+    seeded 0, shifted by one (eggroll.py:217-229). One warmup, then the median of 3 runs."""
+    import torch
+    from noise_amd.model import make_model
+    from oracle import model as om
+    if threads:
+        torch.set_num_threads(threads)
+    P = {k: v.float() for k, v in make_model('cpu', 0).state_dict().items()}
+    batch = torch.randint(0, 4096, (4, TOKENS + 1), generator=torch.Generator().manual_seed(0))
+    x, y = batch[:, :-1], batch[:, 1:]
+    with torch.no_grad():
+        loss = om.gpt_forward(P, x, y)
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            loss = om.gpt_forward(P, x, y)
+            times.append(time.perf_counter() - t0)
+    dt = sorted(times)[1]
+    return dict(value=round(x.numel() / dt, 1), unit='tokens/s', loss=round(float(loss), 6), seconds=round(dt, 3),
+                threads=torch.get_num_threads(), batch='4 x 2048 tokens ~ U[0, 4096), seed 0')
+
+
 def cpu_baseline(P, tables, x, y, members):
     """The oracle forward (fp32, torch CPU) on `members` members of the same workload."""
     import torch
@@ -100,7 +145,7 @@ def cpu_baseline(P, tables, x, y, members):
     dt = time.perf_counter() - t0
     return dict(value=members * x.numel() / dt, unit='member-tokens/s', cores=threads, kind='port',
                 sample=f'{members} members x {x.numel()} tokens, fp32 oracle forward (oracle/model.py), '
-                       f'{dt:.1f} s on {threads} threads'), losses
+                       f'{dt:.1f} s on {threads} threads', host=host_cpu()), losses
 
 
 def main():
@@ -108,7 +153,8 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
-    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update', 'head-error', 'dust-block'),
+    ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update', 'head-error', 'dust-block',
+                                           'attention', 'lowrank', 'cpu-forward'),
                     default='population')
     ap.add_argument('--pairs', type=int, default=None,
                     help='update workload: antithetic pairs (default 512; the reference trains with 131072)')
@@ -131,8 +177,8 @@ def main():
         print(json.dumps(dict(copy_bytes=2 ** 30)))
         return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
-        print('bench.py measures one GPU: this build has no multi-GPU path (members shard across GPUs with one '
-              'all_gather of the losses; see DESIGN.md). Run with --gpus 1.', file=sys.stderr)
+        print('bench.py measures one GPU: this build has no multi-GPU path (members would shard across GPUs with '
+              'one all_gather of the per-member losses). Run with --gpus 1.', file=sys.stderr)
         sys.exit(2)
 
     if args.workload == 'update':
@@ -141,6 +187,12 @@ def main():
         return bench_head_error(args)
     if args.workload == 'dust-block':
         return bench_dust_block(args)
+    if args.workload == 'attention':
+        return bench_attention(args)
+    if args.workload == 'lowrank':
+        return bench_lowrank(args)
+    if args.workload == 'cpu-forward':
+        return bench_cpu_forward(args)
     import torch
     from noise_amd import eggroll as eg
     from noise_amd.model import make_model, window_sizes
@@ -240,6 +292,8 @@ def main():
     )
     if args.cpu_members:
         cb, cpu_losses = cpu_baseline(P, {n: t for n, t in tables.items()}, x, y, args.cpu_members)
+        # the reference's CPU plumbing configuration (fixed model, 4 x 2048 tokens, plain forward + mean CE)
+        cb['config1_forward'] = cpu_forward_config1()
         line['cpu_baseline'] = cb
         line['cpu_parity_max_abs'] = float((cpu_losses - losses[:args.cpu_members].cpu()).abs().max())
     else:
@@ -357,6 +411,91 @@ def bench_dust_block(args):
         roofline=dict(bound='mfma', achieved=round(flops / ms / 1e9, 1), peak=BF16_PEAK / 1e12, unit='TFLOP/s',
                       frac=round(flops / ms / 1e9 / (BF16_PEAK / 1e12), 4), traffic=None),
         finite=bool(torch.isfinite(out).all().item()))), flush=True)
+
+
+def bench_attention(args):
+    """Causal attention alone through the attention(q, k, v, window) drop-in (utils/model.py:24-31): bf16 q, k,
+    v [B=16, H=8, T=2048, D=64] ~ N(0, 1) from one CPU generator seeded 0 (q, k, v in order), passed as the
+    [B, T, H, D] views the reference's attention takes, window = T (causal), scale 1/8. Algorithmic work 4 D
+    FLOPs per visible (query, key) pair: 16 x 8 x 2,098,176 x 256 = 68.75 GFLOP per call."""
+    import torch
+    from noise_amd.model import attention
+    dev = torch.device('cuda', 0)
+    g = torch.Generator().manual_seed(0)
+    B, H, T, D = 16, 8, 2048, 64
+    q, k, v = (torch.randn(B, H, T, D, generator=g).bfloat16().to(dev).transpose(1, 2) for _ in range(3))
+    for _ in range(args.warmup):
+        attention(q, k, v, T)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        out = attention(q, k, v, T)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    flops = 4 * D * B * H * visible_pairs(T, T)
+    print(json.dumps(dict(
+        metric='causal attention forward TFLOP/s, bf16 [16, 8, 2048, 64] on 1 GPU', value=round(flops / ms / 1e9, 1),
+        unit='TFLOP/s', n_gpus=1, steps=args.steps, warmup=args.warmup, ms_per_step=round(ms, 4),
+        higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16', data='synthetic',
+        config=dict(workload='causal attention, q/k/v [16, 8, 2048, 64] bf16 ~ N(0,1) seed 0, scale 1/8, through '
+                             'the attention(q, k, v, window) drop-in'),
+        roofline=dict(bound='mfma', achieved=round(flops / ms / 1e9, 1), peak=BF16_PEAK / 1e12, unit='TFLOP/s',
+                      frac=round(flops / ms / 1e9 / (BF16_PEAK / 1e12), 4), traffic=None, flops_per_launch=flops),
+        finite=bool(torch.isfinite(out.float()).all().item()))), flush=True)
+
+
+def bench_lowrank(args):
+    """The antithetic perturbed linear alone through the lowrank drop-in (eggroll.py:56-58): X bf16 [2048, 512]
+    and W bf16 [2048 out, 512 in] ~ N(0, 0.02^2) from one CPU generator seeded 0; 256 pairs (512 members),
+    sigma 1e-3; a, b per pair sliced from the seed-0 noise buffer at offsets ~ U[0, 2^28 - 2560) from a cuda
+    generator seeded 0. Output [512, 2048, 2048] fp32 in autocast's form (8.6 GB): bound by its HBM writes."""
+    import torch
+    from noise_amd.eggroll import lowrank
+    from noise_amd.noise import DeviceGenerator
+    dev = torch.device('cuda', 0)
+    g = torch.Generator().manual_seed(0)
+    X = torch.randn(2048, 512, generator=g).bfloat16().to(dev)
+    W = (torch.randn(2048, 512, generator=g) * 0.02).bfloat16().to(dev)
+    pairs, sigma, NOISE = 256, 1e-3, 2 ** 28
+    offs = torch.randint(0, NOISE - 2560, (pairs,), device=dev, generator=torch.Generator(dev).manual_seed(0))
+    rows = DeviceGenerator(0, dev).take(NOISE).gather(offs, 2560)
+    a, b = rows[:, :2048], rows[:, 2048:]
+    sign = torch.tensor([sigma, -sigma], device=dev).repeat(pairs)
+    xm = X[None].expand(2 * pairs, 2048, 512)
+    for _ in range(args.warmup):
+        y = lowrank(xm, W, a, b, sign, dir_div=2)
+        del y
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(args.steps):
+        y = lowrank(xm, W, a, b, sign, dir_div=2)
+    e.record()
+    torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    written = y.numel() * 4
+    print(json.dumps(dict(
+        metric='antithetic perturbed linear output GB/s, 512 members x [2048, 2048] on 1 GPU',
+        value=round(written / ms / 1e6, 1), unit='GB/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 4), higher_is_better=True, scaling='weak', vs_baseline=None,
+        dtype='bf16 product, fp32 rank-1 and output', data='synthetic',
+        config=dict(workload='lowrank drop-in: X [2048, 512] shared, W [2048, 512], 256 antithetic pairs, '
+                             'sigma 1e-3, output [512, 2048, 2048] fp32'),
+        roofline=dict(bound='hbm', achieved=round(written / ms / 1e6, 1), peak=HBM_PEAK / 1e9, unit='GB/s',
+                      frac=round(written / ms / 1e6 / (HBM_PEAK / 1e9), 4), traffic=None),
+        finite=bool(torch.isfinite(y[::97]).all().item()))), flush=True)
+
+
+def bench_cpu_forward(args):
+    """The reference's CPU plumbing configuration alone (no GPU): fixed model, seed-0 init, forward + mean
+    next-token CE on 4 x 2048 uniform tokens, fp32 torch CPU ops (the oracle's restatement of utils/model.py)."""
+    r = cpu_forward_config1()
+    print(json.dumps(dict(metric='reference CPU forward tokens/s (fixed 37.7M model, batch 4 x 2048)',
+                          value=r['value'], unit='tokens/s', n_gpus=0, steps=3, warmup=1, higher_is_better=True,
+                          vs_baseline=None, dtype='fp32', data='synthetic', config=dict(workload=r['batch']),
+                          loss=r['loss'], host=host_cpu(), threads=r['threads'])), flush=True)
 
 
 if __name__ == '__main__':

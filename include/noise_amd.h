@@ -97,6 +97,13 @@ int noise_orthogonal_draws(void *out, int out_bf16, int64_t n, int64_t bt, int64
  * (eggroll.py:58), NULL to skip. */
 #define NOISE_ATTN_V_TRANSPOSED 1
 #define NOISE_ATTN_QK_NORMED 2
+
+/* V element (b, t, h, d) at b*vs_b + h*vs_h + t*vs_t + d -> vt [batch][heads][64][seq] contiguous, the
+ * NOISE_ATTN_V_TRANSPOSED layout (no counterpart in the reference: the attention(q, k, v, window) drop-in,
+ * utils/model.py:24-31, transposes V with it so that noise_attention_fwd runs its transposed-V kernel).
+ * seq a multiple of 64, head_dim 64. */
+int noise_v_transpose(const void *v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, int64_t vs_b,
+                      int64_t vs_h, int64_t vs_t, void *vt, noise_stream_t stream);
 int noise_attention_fwd(const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,
                         int64_t seq, int64_t head_dim, int64_t qs_b, int64_t qs_h, int64_t qs_t, int64_t ks_b,
                         int64_t ks_h, int64_t ks_t, int64_t vs_b, int64_t vs_h, int64_t vs_x, int flags,

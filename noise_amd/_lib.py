@@ -23,6 +23,7 @@ SIGNATURES = {
     'noise_orthogonal_draws': [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p],
     'noise_attention_fwd': [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _p, _p],
+    'noise_v_transpose': [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
     'noise_pop_embed': [_p, _i32, _p, _i64, _p, _p, _p, _p, _p, _p, _i64, _p, _p, _p, _p],
     'noise_member_dots': [_p, 'View', _i64, _p, _i64, _p, _p],
     'noise_pop_qkv': [_p, 'View', _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _p, _p],

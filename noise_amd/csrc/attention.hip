@@ -43,6 +43,8 @@ struct AttnArgs {
     int heads, seq, qtiles, bh_total;
     int window;
     int xcd_grouped;                    // 1: bh_total % 8 == 0, map heads onto XCDs
+    int tile_major;                     // 1 (transposed-V kernel, small grids): all heads' heaviest query
+                                        //   tiles first, so the causal imbalance does not set the tail
     int o_lines;                        // 1: o 16 B aligned with strides multiple of 8 (staged row stores)
     float scale_log2;                   // softmax scale * log2(e)
     float shift;                        // fixed log2-domain shift of the bounded-score kernel
@@ -299,7 +301,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 
     int wg = blockIdx.x;
     int bh, qt;
-    if (a.xcd_grouped) {
+    if (a.tile_major) {
+        // query tile descending, then head: with bh_total % 8 == 0 head bh still runs on XCD bh % 8
+        bh = wg % a.bh_total;
+        qt = a.qtiles - 1 - wg / a.bh_total;
+    } else if (a.xcd_grouped) {
         int xcd = wg & 7, slot = wg >> 3;
         bh = (slot / a.qtiles) * 8 + xcd;
         qt = a.qtiles - 1 - (slot % a.qtiles);
@@ -558,10 +564,52 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 
 
 
+// V [b, t, h, d] (d contiguous) -> V^T [b][h][d][t]: one workgroup per (b*h, 64-token tile); each thread
+// reads two 16 B pieces of token rows and writes two 16 B pieces of dim rows through a padded LDS tile.
+__global__ __launch_bounds__(256) void v_transpose_kernel(const __bf16 *v, int64_t vs_b, int64_t vs_h, int64_t vs_t,
+                                                          int heads, int seq, __bf16 *vt) {
+    constexpr int kP = 72;  // LDS row pitch (bf16): 144 B rows keep the column reads 4 B apart in the banks
+    __shared__ __attribute__((aligned(16))) __bf16 tile[64 * kP];
+    const int tiles = seq / 64;
+    const int bh = blockIdx.x / tiles, t0 = (blockIdx.x % tiles) * 64;
+    const int b = bh / heads, h = bh - b * heads;
+    const __bf16 *src = v + b * vs_b + h * vs_h + (int64_t)t0 * vs_t;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + 256 * i, t = c >> 3, d8 = (c & 7) * 8;
+        const bf16x8 x = load_bf16x8(src + (int64_t)t * vs_t + d8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tile[(d8 + e) * kP + t] = x[e];
+    }
+    __syncthreads();
+    __bf16 *dst = vt + (int64_t)bh * kD * seq + t0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int c = threadIdx.x + 256 * i, d = c >> 3, t8 = (c & 7) * 8;
+        store_bf16x8(dst + (int64_t)d * seq + t8, *reinterpret_cast<const bf16x8 *>(tile + d * kP + t8));
+    }
+}
+
 }  // namespace
 }  // namespace noise
 
 using namespace noise;
+
+extern "C" int noise_v_transpose(const void *v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim,
+                                 int64_t vs_b, int64_t vs_h, int64_t vs_t, void *vt, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(head_dim == kD, "noise_v_transpose: head_dim must be 64, got %lld", (long long)head_dim);
+    NOISE_CHECK_ARG(batch > 0 && heads > 0 && seq > 0 && seq % 64 == 0 && seq <= (1 << 30),
+                    "noise_v_transpose: batch, heads > 0 and seq a positive multiple of 64 required");
+    NOISE_CHECK_ARG(v && vt && v != vt && aligned(v, 16) && aligned(vt, 16),
+                    "noise_v_transpose: distinct 16 B aligned buffers required");
+    NOISE_CHECK_ARG(vs_b % 8 == 0 && vs_h % 8 == 0 && vs_t % 8 == 0, "noise_v_transpose: strides must be multiples of 8");
+    const int64_t blocks = batch * heads * (seq / 64);
+    NOISE_CHECK_ARG(blocks < (1ll << 31), "noise_v_transpose: too many tiles");
+    hipLaunchKernelGGL(v_transpose_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (const __bf16 *)v, vs_b, vs_h, vs_t, (int)heads, (int)seq, (__bf16 *)vt);
+    return launch_status("noise_v_transpose");
+}
 
 extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, void *o, int64_t batch,
                                    int64_t heads, int64_t seq, int64_t head_dim, int64_t qs_b, int64_t qs_h,
@@ -608,6 +656,9 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     a.heads = (int)heads; a.seq = (int)seq; a.qtiles = (int)qtiles; a.bh_total = (int)bh;
     a.window = (int)(window > seq ? seq : window);
     a.xcd_grouped = (bh % 8 == 0) ? 1 : 0;
+    // a grid of a few rounds of the 512 resident workgroups (256 CUs x 2) is set by its heaviest tiles:
+    // start them all first. Larger grids keep a head's tiles together for its K / V in L2.
+    a.tile_major = (vt_path && bh * qtiles <= 8 * 512) ? 1 : 0;
     a.scale_log2 = scale * kLog2e;
     a.dvec = dot_vec; a.dot = dot_out; a.ds_b = dot_vec_stride; a.ddiv = (int)dot_div;
     // rows of RMS <= 1 (rounded to bf16): |q . k| <= D (1 + 2^-8)^2 < 1.0079 D

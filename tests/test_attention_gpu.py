@@ -157,3 +157,23 @@ def test_invalid_head_dim_raises():
     q = torch.zeros(1, 64, 2, 32, dtype=torch.bfloat16, device=DEV)
     with pytest.raises(RuntimeError, match='head_dim must be 64'):
         attention(q, q, q, 10)
+
+
+def test_v_transpose_layout_exact():
+    """noise_v_transpose: V [B, T, H, D] (a strided view) -> [B, H, D, T], bit for bit; the drop-in's
+    transposed-V route (T a multiple of 256) equals the general kernel's result within bf16 rounding."""
+    from noise_amd import _lib
+    from noise_amd.model import attention
+    g = torch.Generator().manual_seed(3)
+    v = torch.randn(2, 3, 512, 64, generator=g).bfloat16().to(DEV).transpose(1, 2)  # [B, T, H, D] view
+    vt = torch.empty(2, 3, 64, 512, dtype=torch.bfloat16, device=DEV)
+    _lib.call('noise_v_transpose', v.data_ptr(), 2, 3, 512, 64, v.stride(0), v.stride(2), v.stride(1),
+              vt.data_ptr(), _lib.stream_ptr(DEV))
+    assert torch.equal(vt, v.permute(0, 2, 3, 1))
+    with pytest.raises(RuntimeError, match='multiple of 64'):
+        _lib.call('noise_v_transpose', v.data_ptr(), 2, 3, 500, 64, v.stride(0), v.stride(2), v.stride(1),
+                  vt.data_ptr(), _lib.stream_ptr(DEV))
+    q, k = (torch.randn(2, 512, 3, 64, generator=g).bfloat16().to(DEV) for _ in range(2))
+    fast = attention(q, k, v, 200)
+    ref = fp32_reference_gpu(q, k, v, 200)
+    rel_ok(fast, ref)
