@@ -886,6 +886,127 @@ __global__ __launch_bounds__(kThreads) void head_ce_kernel(HeadArgs p) {
     }
 }
 
+// The bf16 head (K = 512) with each token row read once: a workgroup owns 256 tokens of one member in 8 waves
+// (two per SIMD); wave w keeps its 32 token rows [32 x 512] in registers as the B operand of every product and
+// the head weights stream through LDS in 64 steps of 64 vocabulary rows (64 KiB, double buffered, copied
+// global -> LDS by direct copies, wave w copying k-tile w). Per step a wave forms its 64 x 32 logits (64
+// MFMAs) and folds them into the running sum of exp(z - 15) (softcap identity above: 6 VALU operations per
+// logit, 3 of them transcendental); the target logit is picked in the steps whose 64 rows hold some lane's
+// target. Every row of the vocabulary is in one wave, so the per-token loss needs no workgroup reduction.
+constexpr int kHxThreads = 512, kHxTok = 256, kHxRows = 64;
+constexpr int kHxStepBytes = kHxRows * 512 * 2;  // [8 k-tiles][64 rows][128 B]
+
+template <bool EAGER, bool PERT>
+__global__ __launch_bounds__(kHxThreads, 1) void head_x_kernel(HeadArgs p) {
+    __shared__ __attribute__((aligned(16))) char lds[2 * kHxStepBytes];
+    const int T = p.pop.tokens, tiles_t = T / kHxTok;
+    const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * kHxTok;
+    const int tid = threadIdx.x, lane = tid & 63, jl = lane & 31, hf = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tok = t0 + 32 * wave + jl;
+    const int64_t row = (int64_t)m * T + tok;
+    const int dir = m / p.pop.dir_div;
+    const unsigned lbase = lds_addr(lds);
+    // copies of step js: wave w copies k-tile w of the step's 64 rows, 8 copies of 8 rows (chunk c of row r
+    // lands at position c ^ ((r >> 1) & 7) of the row's 128 B)
+    auto issue = [&](int js) {
+        const unsigned dst = lbase + (js & 1) * kHxStepBytes + wave * 8192;
+#pragma unroll
+        for (int ci = 0; ci < 8; ++ci) {
+            const int r = 8 * ci + (lane >> 3);
+            const int c = (lane & 7) ^ ((r >> 1) & 7);
+            lds_dma16_at(p.w + (int64_t)(kHxRows * js + 8 * ci) * 512 + wave * 64, (unsigned)((lane >> 3) * 1024 + c * 16),
+                         dst + ci * 1024);
+        }
+    };
+    issue(0);
+    // this lane's token row: xf[s] = x[tok][16 s + 8 hf .. + 8], the B operand of k-step s
+    bf16x8 xf[32];
+    {
+        const __bf16 *xr = p.x + m * p.xs_m + (int64_t)tok * p.xs_t + 8 * hf;
+#pragma unroll
+        for (int s = 0; s < 32; ++s) xf[s] = load_bf16x8(xr + 16 * s);
+    }
+    const int64_t tgt = p.targets[m * p.targets_sm + tok];
+    const float corr = PERT ? p.pop.sign[m] * p.dots[row] : 0.f;
+    const float *arow = PERT ? p.r1.a + dir * p.r1.a_stride + 4 * hf : nullptr;
+    const float k1 = (2.0f / 15.0f) * kLog2e;     // u = 2^(k1 l) = e^(2 l / 15)
+    const float c2 = 1.0f / (-30.0f * kLog2e);    // rcp(c2 (1 + u)) = -30 log2(e) / (1 + u) = log2 e^(z - 15)
+    float sum = 0.f, zl = 0.f;                    // sum of e^(z - 15) over this lane's rows; the target's logit
+    vm_wait<0>();
+    __syncthreads();
+    const int nsteps = p.vocab / kHxRows;
+    f32x16 acc[2];
+#pragma unroll 1
+    for (int js = 0; js < nsteps; ++js) {
+        if (js + 1 < nsteps) issue(js + 1);  // its buffer was last read in step js - 1, before the barrier below
+        const char *buf = lds + (js & 1) * kHxStepBytes;
+        auto frag = [&](int vb, int s) {
+            return *reinterpret_cast<const bf16x8 *>(buf + (s >> 2) * 8192 + (32 * vb + jl) * 128 +
+                                                     ((((2 * s + hf) & 7) ^ ((jl >> 1) & 7)) << 4));
+        };
+        acc[0] = f32x16{};
+        acc[1] = f32x16{};
+        bf16x8 fa[2][2];
+        fa[0][0] = frag(0, 0);
+        fa[0][1] = frag(1, 0);
+#pragma unroll
+        for (int s = 0; s < 32; ++s) {
+            if (s + 1 < 32) {
+                fa[(s + 1) & 1][0] = frag(0, s + 1);
+                fa[(s + 1) & 1][1] = frag(1, s + 1);
+            }
+            acc[0] = mfma32x32x16(fa[s & 1][0], xf[s], acc[0]);
+            acc[1] = mfma32x32x16(fa[s & 1][1], xf[s], acc[1]);
+        }
+        // register r of block vb holds vocabulary row v0 + 32 vb + 8 (r / 4) + 4 hf + r % 4
+        const int v0 = kHxRows * js;
+        // the logit of register r of block vb: rounded (eager) or with the rank-1 term (perturbed head)
+        auto logit = [&](int vb, int r, const float4 &a4) {
+            float x = acc[vb][r];
+            if constexpr (EAGER) x = bfr(x);
+            if constexpr (PERT) x = __builtin_fmaf(corr, f4get(a4, r & 3), x);
+            return x;
+        };
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                float4 a4{0.f, 0.f, 0.f, 0.f};
+                if constexpr (PERT) a4 = ld4(arow + v0 + 32 * vb + 8 * b);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float u = exp2_fast(logit(vb, 4 * b + e, a4) * k1);
+                    sum += exp2_fast(__builtin_amdgcn_rcpf(__builtin_fmaf(u, c2, c2)));
+                }
+            }
+        // the target's logit, in the steps whose rows hold some lane's target (-1 and out-of-range ids never do)
+        const bool here = (uint64_t)(tgt - v0) < (uint64_t)kHxRows;
+        if (__builtin_amdgcn_ballot_w64(here)) {
+            const int d = here ? (int)(tgt - v0) - 4 * hf : -1;
+#pragma unroll
+            for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    float4 a4{0.f, 0.f, 0.f, 0.f};
+                    if constexpr (PERT) a4 = ld4(arow + v0 + 32 * vb + 8 * b);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (d == 32 * vb + 8 * b + e) zl = logit(vb, 4 * b + e, a4);
+                }
+        }
+        vm_wait<0>();
+        __syncthreads();  // step js + 1 landed for every wave; every wave is done with buffer js & 1
+    }
+    sum += swap_halves(sum);
+    zl += swap_halves(zl);  // exactly one lane of the pair holds the target's row
+    if (hf == 0) {
+        const float z = 15.0f - 30.0f / (exp2_fast(zl * k1) + 1.0f);
+        const float ce = 15.0f + __logf(sum) - z;
+        p.loss[row] = tgt == -1 ? 0.f : (tgt < 0 || tgt >= p.vocab ? __builtin_nanf("") : ce);
+    }
+}
+
 Pop make_pop(const noise_population_t *pp) {
     Pop p;
     p.members = (int)pp->members;
@@ -1157,10 +1278,19 @@ extern "C" int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, 
     a.r1 = make_r1(r1);
     a.dots = dots; a.targets = targets; a.targets_sm = targets_sm; a.loss = token_loss;
     dim3 grid((unsigned)(pop->members * (pop->tokens / 256)));
-    if (eager(pop))
+    if (K == 512 && vocab % kHxRows == 0 && x.st % 8 == 0 && x.sm % 8 == 0) {
+        // the bf16 head: token rows resident in registers, weights streamed once per 256 tokens
+        if (eager(pop))
+            hipLaunchKernelGGL((head_x_kernel<true, false>), grid, dim3(kHxThreads), 0, (hipStream_t)stream, a);
+        else if (a.r1.a)
+            hipLaunchKernelGGL((head_x_kernel<false, true>), grid, dim3(kHxThreads), 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL((head_x_kernel<false, false>), grid, dim3(kHxThreads), 0, (hipStream_t)stream, a);
+    } else if (eager(pop)) {
         hipLaunchKernelGGL(head_ce_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
-    else
+    } else {
         hipLaunchKernelGGL(head_ce_kernel<false>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
+    }
     return launch_status(fn);
 }
 
