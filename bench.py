@@ -49,6 +49,8 @@ def kernel_flops_per_launch(name, label, members, T):
         return 2 * (2048 if label == 'mlp.c_proj' else 512) * 512 * rows
     if name == 'noise_pop_mlp':
         return 2 * 2 * 512 * 2048 * rows
+    if name == 'noise_pop_attn_mlp':
+        return 2 * (512 * 512 + 2 * 512 * 2048) * rows
     if name == 'noise_pop_head_ce':
         return 2 * 512 * 4096 * rows
     if name == 'noise_attention_fwd':
@@ -60,7 +62,8 @@ def kernel_flops_per_launch(name, label, members, T):
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'population_forward_1024x2048.md')
 ROCPROF_NAME = {'noise_pop_qkv': 'qkv_kernel', 'noise_pop_fc': 'fc_kernel', 'noise_pop_head_ce': 'head_ce_kernel',
                 'noise_pop_residual[attn.c_proj]': 'resid_kernel<512>',
-                'noise_pop_residual[mlp.c_proj]': 'resid_kernel<2048>', 'noise_pop_mlp[mlp]': 'mlp_kernel'}
+                'noise_pop_residual[mlp.c_proj]': 'resid_kernel<2048>', 'noise_pop_mlp[mlp]': 'mlp_kernel',
+                'noise_pop_attn_mlp[block]': 'mlp_kernel'}
 
 
 def profiled_traffic(kernel):

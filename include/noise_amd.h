@@ -256,6 +256,21 @@ int noise_pop_mlp(const noise_population_t *pop, noise_view_t x, const void *w_f
                   int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next, int64_t nnext,
                   float *next_dots, noise_stream_t stream);
 
+/* Attention projection, residual, RMSNorm and the whole MLP of a block in one kernel (eggroll.py:92-93 and
+ * the mixing, norm and next-matrix dots that follow, eggroll.py:77-82 / 94; replaces noise_pop_residual with
+ * K = 512 followed by noise_pop_mlp): x_mid = xres + y w_o^T + sign (sum of the o_dots_n partial dots
+ * o_dots[row][.]) a_o, h = norm(x_mid) (in registers), then noise_pop_mlp's arithmetic on h with x_mid as its
+ * residual. y: the attention output, bf16 [members][tokens][512]; w_o bf16 [512][512]; r_o: attn.c_proj's
+ * rank-1 noise (a [dirs][512]) or NULL; w_fc AND w_proj both in the column order noise_mlp_proj_layout
+ * writes (w_fc [2048][512] permuted as 512 rows of 2048); r_fc needs a and b (c_fc's x . b is formed here from
+ * the fp32 normalised row). Other arguments as noise_pop_mlp. Fused rounding only. */
+int noise_pop_attn_mlp(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
+                       const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
+                       const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout, int mix,
+                       const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+                       int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
+                       int64_t nnext, float *next_dots, noise_stream_t stream);
+
 /* mlp.c_proj [rows][2048] bf16 -> the column order noise_pop_mlp reads: within every 16 columns, the groups of
  * 4 are stored in the order 0, 2, 1, 3 (so each 16-deep slice of the hidden layer pairs with the registers the
  * c_fc product leaves it in). out and w distinct; one pass per weight update. */

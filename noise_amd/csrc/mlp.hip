@@ -22,6 +22,15 @@
 //     previous step is formed.
 // The residual epilogue then has every output of a token in one lane pair: RMSNorm and the next-matrix dots
 // need one exchange with lane ^ 32 and no workgroup reduction.
+//
+// With the attention projection in front (noise_pop_attn_mlp, eggroll.py:92 then 93), the same workgroup first
+// forms x_mid = x + y W_o^T + sign (y . b_o) a_o for its tokens: the attention output rows y take the register
+// slots of the h rows, W_o streams through the mlp.c_proj buffers in 16 steps of [512 rows x 32 k], and the
+// product accumulates in the output accumulators. After the residual add, h = bf16(norm(x_mid)) is packed
+// straight from the accumulators into the B operand of the first MLP product: the D layout's groups of four
+// (r % 4 within a lane, lane / 32 alternating) are that operand once the contraction index is permuted within
+// each 16, so c_fc's columns come in the same permuted order as mlp.c_proj's (noise_mlp_proj_layout). x_mid
+// stays in the accumulators, the MLP adds to it, and neither x_mid nor h ever reaches HBM.
 #include "common.hpp"
 #include "mfma.hpp"
 #include "tile.hpp"
@@ -43,7 +52,9 @@ constexpr int kAfc = kVecOff;                  // c_fc's a            [2048]
 constexpr int kBpj = kAfc + kHid * 4;          // mlp.c_proj's b      [2048]
 constexpr int kApj = kBpj + kHid * 4;          // mlp.c_proj's a      [512]
 constexpr int kNb = kApj + kEmb * 4;           // next matrices' b    [3][512]
-constexpr int kMlpLds = kNb + 3 * kEmb * 4;    // 152 KiB
+constexpr int kAo = kNb + 3 * kEmb * 4;        // attn.c_proj's a     [512] (with the projection in front)
+constexpr int kBfc = kAo + kEmb * 4;           // c_fc's b            [512] (with the projection in front)
+constexpr int kMlpLds = kBfc + kEmb * 4;       // 156 KiB
 static_assert(kMlpLds <= 160 * 1024, "LDS of one CU");
 
 struct MlpPop {
@@ -75,6 +86,15 @@ struct MlpArgs {
     const float *nb[3];
     int64_t nb_stride[3];
     float *ndots;                  // [rows][NNEXT]
+    // the attention projection in front (FRONT): x (above) is the attention output y, xres the block's
+    // residual input; c_fc's columns then come permuted like mlp.c_proj's and its x . b is formed here
+    const __bf16 *wo;              // attn.c_proj [512][512]
+    const float *ao;               // its rank-1 a [dirs][512] or NULL
+    int64_t ao_stride;
+    const float *odots;            // y . b_o partial sums [rows][odots_n] (per head)
+    int odots_n;
+    const float *bfc;              // c_fc's rank-1 b [dirs][512] (with afc)
+    int64_t bfc_stride;
 };
 
 // LDS offset of (k-tile kt, row r, 16 B chunk c) in a c_fc step buffer: 128 B rows, chunks XOR-swizzled by
@@ -83,7 +103,7 @@ __device__ __forceinline__ int fc_off(int kt, int r, int c) { return kt * 4096 +
 // ... and of (row r, chunk c) in an mlp.c_proj step buffer: 64 B rows, chunks swizzled by row quad
 __device__ __forceinline__ int pj_off(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 
-template <bool MIX, int NNEXT, bool SPLIT3>
+template <bool MIX, int NNEXT, bool SPLIT3, bool FRONT>
 __global__ __launch_bounds__(kMlpThreads, 1) void mlp_kernel(MlpArgs p) {
     __shared__ __attribute__((aligned(16))) char lds[kMlpLds];
     const int T = p.pop.tokens, tiles_t = T / kTileTok;
@@ -121,8 +141,13 @@ __global__ __launch_bounds__(kMlpThreads, 1) void mlp_kernel(MlpArgs p) {
         vcopy(p.apj ? p.apj + dir * p.apj_stride : nullptr, kApj, kEmb);
 #pragma unroll
         for (int k = 0; k < NNEXT; ++k) vcopy(p.nb[k] + dir * p.nb_stride[k], kNb + k * kEmb * 4, kEmb);
+        if constexpr (FRONT) {
+            vcopy(p.ao ? p.ao + dir * p.ao_stride : nullptr, kAo, kEmb);
+            vcopy(p.afc ? p.bfc + dir * p.bfc_stride : nullptr, kBfc, kEmb);
+        }
     }
-    const float corr_fc = p.afc ? sgn * p.dots_fc[row] : 0.f;
+    float corr_fc = 0.f;
+    if constexpr (!FRONT) corr_fc = p.afc ? sgn * p.dots_fc[row] : 0.f;
     vm_wait<0>();
     __syncthreads();
     // this lane's h row: the B operand of all 32 k-steps of the first product (k-tile s / 4, chunk 2s + hf)
@@ -166,6 +191,115 @@ __global__ __launch_bounds__(kMlpThreads, 1) void mlp_kernel(MlpArgs p) {
     f32x16 hacc;
     bf16x8 hb[2];
     float pd = 0.f;  // this lane's share of hid . b_proj
+
+    // whole-line copies of a quarter of the features (32 tokens x 512 B) of fp32 rows into LDS at dst: copy i
+    // covers rows 2i, 2i + 1; the 16 B chunk c of row r sits at position c ^ (r % 16), so the MFMA layout's reads
+    // (32 rows, one chunk) spread over the banks
+    auto issue_rows = [&](const float *src, int64_t ld, int q, unsigned dst) {
+        const int r = lane >> 5;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int cc = (lane & 31) ^ ((2 * i + r) & 15);
+            lds_dma16_at(src + (int64_t)(2 * i) * ld + 128 * q, (unsigned)(r * ld * 4 + cc * 16), dst + i * 1024);
+        }
+    };
+    if constexpr (FRONT) {
+        // x_mid = x + (y W_o^T + sign (y . b_o) a_o): W_o [512][512] through the mlp.c_proj buffers, step i holding
+        // columns 32 i .. 32 i + 31 of every row (the layout of an mlp.c_proj step); xf holds the y rows
+        auto issue_o = [&](int i) {
+            const unsigned dst = lbase + kPjOff + (i & 1) * kPjBytes;
+            const int c = (lane & 3) ^ ((lane >> 4) & 3);
+#pragma unroll
+            for (int ci = 0; ci < 8; ++ci) {
+                const int q = wave * 8 + ci;
+                lds_dma16_at(p.wo + (int64_t)(16 * q) * kEmb + kStep * i, (unsigned)((lane >> 2) * kEmb * 2 + c * 16),
+                             dst + q * 1024);
+            }
+        };
+        issue_o(0);
+        vm_wait<0>();
+        __syncthreads();
+        // (unrolled: the y rows are indexed by the step, and register arrays need static indices)
+#pragma unroll
+        for (int i = 0; i < kEmb / kStep; ++i) {
+            if (i + 1 < kEmb / kStep) issue_o(i + 1);  // its buffer was last read in step i - 1 (barrier below)
+            const char *bo = lds + kPjOff + (i & 1) * kPjBytes;
+            auto fo = [&](int s) {
+                return *reinterpret_cast<const bf16x8 *>(bo + pj_off(32 * (s >> 1) + jl, 2 * (s & 1) + hf));
+            };
+            bf16x8 pa[2];
+            pa[0] = fo(0);
+            pa[1] = fo(1);
+#pragma unroll
+            for (int s = 0; s < 32; ++s) {
+                const bf16x8 a = pa[s & 1];
+                if (s + 2 < 32) pa[s & 1] = fo(s + 2);
+                out[s >> 1] = mfma32x32x16(a, xf[2 * i + (s & 1)], out[s >> 1]);
+            }
+            vm_wait<0>();
+            __syncthreads();  // step i + 1 landed; every wave is done with buffer i & 1
+        }
+        // rank-1 term and the residual rows (x, by whole-line copies a quarter at a time, double buffered in the
+        // wave's own 32 KiB of the fc buffers and the first pj buffer)
+        float osum = 0.f;
+        if (p.ao) {
+            for (int k = 0; k < p.odots_n; ++k) osum += p.odots[row * p.odots_n + k];
+        }
+        const float corr_o = sgn * osum;  // 0 without perturbation (and the a_o vector is zeros then)
+        const float *xtile = p.xres + m * p.xr_m + (int64_t)(t0 + 32 * wave) * p.xr_t;
+        const float *ao = reinterpret_cast<const float *>(lds + kAo) + 4 * hf;
+        const unsigned wbase = lbase + wave * 32768;
+        issue_rows(xtile, p.xr_t, 0, wbase);
+        issue_rows(xtile, p.xr_t, 1, wbase + 16384);
+        float ssq = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            if (q < 3) vm_wait<16>(); else vm_wait<0>();
+            wave_lds_sync();
+            const char *xb = lds + wave * 32768 + (q & 1) * 16384 + jl * 512;
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int rb = 4 * q + r4;
+                    const int c = 8 * r4 + 2 * b + hf;
+                    const float4 xv = *reinterpret_cast<const float4 *>(xb + ((c ^ (jl & 15)) << 4));
+                    const float4 a4 = ld4(ao + 32 * rb + 8 * b);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float y = f4get(xv, e) + (out[rb][4 * b + e] + corr_o * f4get(a4, e));
+                        out[rb][4 * b + e] = y;
+                        ssq += y * y;
+                    }
+                }
+            wave_lds_sync();  // this quarter's reads are done before the next copies overwrite the buffer
+            if (q + 2 < 4) issue_rows(xtile, p.xr_t, q + 2, wbase + (q & 1) * 16384);
+        }
+        ssq += swap_halves(ssq);
+        const float rstd = rsqrtf(ssq * (1.0f / kEmb) + kNormEps);
+        // c_fc's x . b from the fp32 normalised row (as the residual writer forms it), and h = bf16(norm(x_mid))
+        // packed as the first product's B operand: k-step s holds features 16 s + 4 hf + (0..3) and
+        // 16 s + 8 + 4 hf + (0..3), registers 8 (s % 2) .. 8 (s % 2) + 7 of output block s / 2
+        if (p.afc) {
+            const float *bf = reinterpret_cast<const float *>(lds + kBfc) + 4 * hf;
+            float d = 0.f;
+#pragma unroll
+            for (int rb = 0; rb < 16; ++rb)
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const float4 b4 = ld4(bf + 32 * rb + 8 * b);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) d += out[rb][4 * b + e] * f4get(b4, e);
+                }
+            d += swap_halves(d);
+            corr_fc = sgn * (rstd * d);
+        }
+#pragma unroll
+        for (int s = 0; s < 32; ++s)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xf[s][e] = (__bf16)(out[s >> 1][8 * (s & 1) + e] * rstd);
+        __syncthreads();  // every wave is done with the residual rows: the buffers take the weight copies
+    }
 
     // first product of step js (32 k-steps), optionally interleaved with the second product of step js - 1
     // (32 MFMAs over the 16 output blocks), so consecutive products on the first product's accumulator always
@@ -265,28 +399,26 @@ __global__ __launch_bounds__(kMlpThreads, 1) void mlp_kernel(MlpArgs p) {
     // spread over the banks. Every load of the epilogue is such a copy, so the explicit waits count them all.
     __syncthreads();  // every wave is done with the operand buffers
     char *wst = lds + wave * 32768;
+    // the rows this epilogue loads: the residual x (unless it is already in the accumulators, FRONT) and x0
+    // (mixing); one kind double buffered, two kinds side by side
+    constexpr bool LOADX = !FRONT;
+    constexpr int NLOAD = (LOADX ? 1 : 0) + (MIX ? 1 : 0);
     const float *xtile = p.xres + m * p.xr_m + (int64_t)(t0 + 32 * wave) * p.xr_t;
     const float *ztile = MIX ? p.x0 + m * p.x0_m + (int64_t)(t0 + 32 * wave) * p.x0_t : nullptr;
-    auto issue_rows = [&](const float *src, int64_t ld, int q, unsigned dst) {
-        const int r = lane >> 5;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int cc = (lane & 31) ^ ((2 * i + r) & 15);
-            lds_dma16_at(src + (int64_t)(2 * i) * ld + 128 * q, (unsigned)(r * ld * 4 + cc * 16), dst + i * 1024);
-        }
-    };
     auto issue_q = [&](int q) {
-        const unsigned dst = lbase + wave * 32768 + (MIX ? 0 : (q & 1) * 16384);
-        issue_rows(xtile, p.xr_t, q, dst);
-        if constexpr (MIX) issue_rows(ztile, p.x0_t, q, dst + 16384);
+        const unsigned dst = lbase + wave * 32768 + (NLOAD == 2 ? 0 : (q & 1) * 16384);
+        if constexpr (LOADX) issue_rows(xtile, p.xr_t, q, dst);
+        if constexpr (MIX) issue_rows(ztile, p.x0_t, q, dst + (LOADX ? 16384 : 0));
     };
-    issue_q(0);
-    if constexpr (!MIX) issue_q(1);
+    if constexpr (NLOAD > 0) issue_q(0);
+    if constexpr (NLOAD == 1) issue_q(1);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        if (!MIX && q < 3) vm_wait<16>(); else vm_wait<0>();
-        wave_lds_sync();
-        const char *xb = wst + (MIX ? 0 : (q & 1) * 16384) + jl * 512;
+        if constexpr (NLOAD > 0) {
+            if (NLOAD == 1 && q < 3) vm_wait<16>(); else vm_wait<0>();
+            wave_lds_sync();
+        }
+        const char *xb = wst + (NLOAD == 2 ? 0 : (q & 1) * 16384) + jl * 512;
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4)
 #pragma unroll
@@ -294,20 +426,24 @@ __global__ __launch_bounds__(kMlpThreads, 1) void mlp_kernel(MlpArgs p) {
                 const int rb = 4 * q + r4;
                 const int c = 8 * r4 + 2 * b + hf;  // chunk of the quarter's row holding features 32 r4 + 8 b + 4 hf
                 const int pos = (c ^ (jl & 15)) << 4;
-                const float4 xv = *reinterpret_cast<const float4 *>(xb + pos);
-                float4 zv{0.f, 0.f, 0.f, 0.f};
-                if constexpr (MIX) zv = *reinterpret_cast<const float4 *>(xb + 16384 + pos);
+                float4 xv{0.f, 0.f, 0.f, 0.f}, zv{0.f, 0.f, 0.f, 0.f};
+                if constexpr (LOADX) xv = *reinterpret_cast<const float4 *>(xb + pos);
+                if constexpr (MIX) zv = *reinterpret_cast<const float4 *>(xb + (LOADX ? 16384 : 0) + pos);
                 const float4 a4 = ld4(apj + 32 * rb + 8 * b);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    float y = f4get(xv, e) + (out[rb][4 * b + e] + corr * f4get(a4, e));
+                    // FRONT: the accumulators already hold x_mid + the MLP product
+                    float y = LOADX ? f4get(xv, e) + (out[rb][4 * b + e] + corr * f4get(a4, e))
+                                    : out[rb][4 * b + e] + corr * f4get(a4, e);
                     if constexpr (MIX) y = rl * y + ml * f4get(zv, e);
                     out[rb][4 * b + e] = y;
                     ssq += y * y;
                 }
             }
-        wave_lds_sync();  // this quarter's reads are done before the next copies overwrite the buffer
-        if (MIX ? q + 1 < 4 : q + 2 < 4) issue_q(MIX ? q + 1 : q + 2);
+        if constexpr (NLOAD > 0) {
+            wave_lds_sync();  // this quarter's reads are done before the next copies overwrite the buffer
+            if (NLOAD == 2 ? q + 1 < 4 : q + 2 < 4) issue_q(NLOAD == 2 ? q + 1 : q + 2);
+        }
     }
     ssq += swap_halves(ssq);
     const float rstd = rsqrtf(ssq * (1.0f / kEmb) + kNormEps);
@@ -406,21 +542,21 @@ __global__ __launch_bounds__(256) void mlp_proj_layout_kernel(const __bf16 *w, _
     store_bf16x4(out + 4 * i, load_bf16x4(w + 16 * q + 4 * src));
 }
 
-template <bool MIX, int NNEXT>
+template <bool MIX, int NNEXT, bool FRONT>
 void launch_mlp_n(const MlpArgs &a, bool split3, dim3 grid, hipStream_t s) {
     if (split3)
-        hipLaunchKernelGGL((mlp_kernel<MIX, NNEXT, true>), grid, dim3(kMlpThreads), 0, s, a);
+        hipLaunchKernelGGL((mlp_kernel<MIX, NNEXT, true, FRONT>), grid, dim3(kMlpThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((mlp_kernel<MIX, NNEXT, false>), grid, dim3(kMlpThreads), 0, s, a);
+        hipLaunchKernelGGL((mlp_kernel<MIX, NNEXT, false, FRONT>), grid, dim3(kMlpThreads), 0, s, a);
 }
 
-template <bool MIX>
+template <bool MIX, bool FRONT>
 void launch_mlp(const MlpArgs &a, int nnext, bool split3, dim3 grid, hipStream_t s) {
     switch (nnext) {
-        case 0: launch_mlp_n<MIX, 0>(a, split3, grid, s); break;
-        case 1: launch_mlp_n<MIX, 1>(a, split3, grid, s); break;
-        case 2: launch_mlp_n<MIX, 2>(a, split3, grid, s); break;
-        default: launch_mlp_n<MIX, 3>(a, split3, grid, s); break;
+        case 0: launch_mlp_n<MIX, 0, FRONT>(a, split3, grid, s); break;
+        case 1: launch_mlp_n<MIX, 1, FRONT>(a, split3, grid, s); break;
+        case 2: launch_mlp_n<MIX, 2, FRONT>(a, split3, grid, s); break;
+        default: launch_mlp_n<MIX, 3, FRONT>(a, split3, grid, s); break;
     }
 }
 
@@ -439,13 +575,14 @@ extern "C" int noise_mlp_proj_layout(const void *w, void *out, int64_t rows, noi
     return launch_status("noise_mlp_proj_layout");
 }
 
-extern "C" int noise_pop_mlp(const noise_population_t *pop, noise_view_t x, const void *w_fc, const noise_rank1_t *r_fc,
-                             const float *dots_fc, const void *w_proj, const noise_rank1_t *r_proj, noise_view_t xres,
-                             float *xout, int mix, const float *lam_r, const float *lam_x, const float *eps_r,
-                             const float *eps_x, int64_t eps_stride, noise_view_t x0, void *hout, int split3,
-                             const noise_rank1_t *next, int64_t nnext, float *next_dots, noise_stream_t stream) {
-    clear_error();
-    const char *fn = "noise_pop_mlp";
+namespace {
+
+// Checks shared by both entry points and the MlpArgs they fill (dots_fc only without the projection in front).
+int mlp_setup(const char *fn, const noise_population_t *pop, noise_view_t x, const void *w_fc, const noise_rank1_t *r_fc,
+              const float *dots_fc, bool front, const void *w_proj, const noise_rank1_t *r_proj, noise_view_t xres,
+              float *xout, int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+              int64_t eps_stride, noise_view_t x0, void *hout, const noise_rank1_t *next, int64_t nnext,
+              float *next_dots, MlpArgs &a) {
     NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
     NOISE_CHECK_ARG(pop->tokens % kTileTok == 0, "%s: tokens (%lld) must be a multiple of %d", fn,
                     (long long)pop->tokens, kTileTok);
@@ -462,16 +599,22 @@ extern "C" int noise_pop_mlp(const noise_population_t *pop, noise_view_t x, cons
     NOISE_CHECK_ARG(hout && aligned(hout, 8), "%s: hout NULL or misaligned", fn);
     NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || (next && next_dots)), "%s: bad next-dot request", fn);
     const bool pfc = r_fc && r_fc->a, ppj = r_proj && r_proj->a;
-    NOISE_CHECK_ARG(!pfc || (dots_fc && pop->sign && aligned(r_fc->a, 16) && r_fc->a_stride % 4 == 0),
-                    "%s: c_fc noise needs dots, sign and 16 B aligned a rows", fn);
+    if (front)
+        NOISE_CHECK_ARG(!pfc || (pop->sign && r_fc->b && aligned(r_fc->a, 16) && aligned(r_fc->b, 16) &&
+                                 r_fc->a_stride % 4 == 0 && r_fc->b_stride % 4 == 0),
+                        "%s: c_fc noise needs sign and 16 B aligned a, b rows", fn);
+    else
+        NOISE_CHECK_ARG(!pfc || (dots_fc && pop->sign && aligned(r_fc->a, 16) && r_fc->a_stride % 4 == 0),
+                        "%s: c_fc noise needs dots, sign and 16 B aligned a rows", fn);
     NOISE_CHECK_ARG(!ppj || (pop->sign && r_proj->b && aligned(r_proj->a, 16) && aligned(r_proj->b, 16) &&
                              r_proj->a_stride % 4 == 0 && r_proj->b_stride % 4 == 0),
                     "%s: mlp.c_proj noise needs sign and 16 B aligned a, b rows", fn);
-    MlpArgs a{};
+    a = MlpArgs{};
     a.pop = MlpPop{(int)pop->members, (int)pop->tokens, pop->sign, (int)pop->dir_div};
     a.x = (const __bf16 *)x.ptr; a.xs_m = x.sm; a.xs_t = x.st;
     a.wfc = (const __bf16 *)w_fc; a.wpj = (const __bf16 *)w_proj;
-    a.afc = pfc ? r_fc->a : nullptr; a.afc_stride = pfc ? r_fc->a_stride : 0; a.dots_fc = dots_fc;
+    a.afc = pfc ? r_fc->a : nullptr; a.afc_stride = pfc ? r_fc->a_stride : 0; a.dots_fc = front ? nullptr : dots_fc;
+    a.bfc = front && pfc ? r_fc->b : nullptr; a.bfc_stride = front && pfc ? r_fc->b_stride : 0;
     a.apj = ppj ? r_proj->a : nullptr; a.bpj = ppj ? r_proj->b : nullptr;
     a.apj_stride = ppj ? r_proj->a_stride : 0; a.bpj_stride = ppj ? r_proj->b_stride : 0;
     a.xres = (const float *)xres.ptr; a.xr_m = xres.sm; a.xr_t = xres.st;
@@ -487,10 +630,52 @@ extern "C" int noise_pop_mlp(const noise_population_t *pop, noise_view_t x, cons
                             "%s: next b %d NULL or misaligned", fn, k);
     }
     a.ndots = next_dots;
+    return NOISE_OK;
+}
+
+}  // namespace
+
+extern "C" int noise_pop_mlp(const noise_population_t *pop, noise_view_t x, const void *w_fc, const noise_rank1_t *r_fc,
+                             const float *dots_fc, const void *w_proj, const noise_rank1_t *r_proj, noise_view_t xres,
+                             float *xout, int mix, const float *lam_r, const float *lam_x, const float *eps_r,
+                             const float *eps_x, int64_t eps_stride, noise_view_t x0, void *hout, int split3,
+                             const noise_rank1_t *next, int64_t nnext, float *next_dots, noise_stream_t stream) {
+    clear_error();
+    MlpArgs a;
+    const int st = mlp_setup("noise_pop_mlp", pop, x, w_fc, r_fc, dots_fc, false, w_proj, r_proj, xres, xout, mix, lam_r,
+                             lam_x, eps_r, eps_x, eps_stride, x0, hout, next, nnext, next_dots, a);
+    if (st != NOISE_OK) return st;
     const dim3 grid((unsigned)(pop->members * (pop->tokens / kTileTok)));
     if (mix)
-        launch_mlp<true>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
+        launch_mlp<true, false>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
     else
-        launch_mlp<false>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
+        launch_mlp<false, false>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
+    return launch_status("noise_pop_mlp");
+}
+
+extern "C" int noise_pop_attn_mlp(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
+                                  const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
+                                  const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout,
+                                  int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+                                  int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
+                                  int64_t nnext, float *next_dots, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_attn_mlp";
+    MlpArgs a;
+    const int st = mlp_setup(fn, pop, y, w_fc, r_fc, nullptr, true, w_proj, r_proj, xres, xout, mix, lam_r, lam_x, eps_r,
+                             eps_x, eps_stride, x0, hout, next, nnext, next_dots, a);
+    if (st != NOISE_OK) return st;
+    NOISE_CHECK_ARG(w_o && aligned(w_o, 16), "%s: w_o NULL or misaligned", fn);
+    const bool po = r_o && r_o->a;
+    NOISE_CHECK_ARG(!po || (pop->sign && o_dots && o_dots_n >= 1 && aligned(r_o->a, 16) && r_o->a_stride % 4 == 0),
+                    "%s: attn.c_proj noise needs sign, dots and 16 B aligned a rows", fn);
+    a.wo = (const __bf16 *)w_o;
+    a.ao = po ? r_o->a : nullptr; a.ao_stride = po ? r_o->a_stride : 0;
+    a.odots = po ? o_dots : nullptr; a.odots_n = po ? (int)o_dots_n : 0;
+    const dim3 grid((unsigned)(pop->members * (pop->tokens / kTileTok)));
+    if (mix)
+        launch_mlp<true, true>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
+    else
+        launch_mlp<false, true>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
     return launch_status(fn);
 }

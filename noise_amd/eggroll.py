@@ -139,10 +139,12 @@ class Weights:
             blk = dict(q=bf(pre + 'attn.c_q.weight'), k=bf(pre + 'attn.c_k.weight'), v=bf(pre + 'attn.c_v.weight'),
                        o=bf(pre + 'attn.c_proj.weight'), fc=bf(pre + 'mlp.c_fc.weight'),
                        mp=bf(pre + 'mlp.c_proj.weight'))
-            # mlp.c_proj in the fused MLP kernel's column order
-            blk['mp_perm'] = torch.empty_like(blk['mp'])
-            _lib.call('noise_mlp_proj_layout', blk['mp'].data_ptr(), blk['mp_perm'].data_ptr(), blk['mp'].shape[0],
-                      _lib.stream_ptr(dev))
+            # mlp.c_proj and mlp.c_fc in the fused block kernel's column order (within every 16 columns the
+            # groups of four permuted; c_fc's [2048][512] permuted as 512 rows of 2048)
+            for src, dst in (('mp', 'mp_perm'), ('fc', 'fc_perm')):
+                blk[dst] = torch.empty_like(blk[src])
+                _lib.call('noise_mlp_proj_layout', blk[src].data_ptr(), blk[dst].data_ptr(),
+                          blk[src].numel() // 2048, _lib.stream_ptr(dev))
             if has_ve(i, n_layer):
                 # the gate's product runs under autocast: its weights enter rounded to bf16
                 blk['gate'] = bf(pre + 'attn.ve_gate.weight').to(F32).contiguous()
@@ -312,21 +314,16 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
                   W.windows[i], 1.0 / math.sqrt(HEAD_DIM), None if no is None else no[1].data_ptr(),
                   0 if no is None else no[1].stride(0), dir_div, None if no is None else B.d_attn.data_ptr(),
                   stream, label=f'window {W.windows[i]}')
-        # attn.c_proj + residual; h = norm(x_mid); c_fc dot
         nfc, nmp = nz(pre + 'mlp.c_fc.weight'), nz(pre + 'mlp.c_proj.weight')
         o_r1 = _rank1(no)
         xres = _view(B.xin0, sm_e, E) if i == 0 else _view(B.resid, T * E, E)
-        nxt = dot_vecs([nfc], E) if nfc is not None else None
-        _call('noise_pop_residual', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), E, ctypes.byref(o_r1),
-                  B.d_attn.data_ptr(), N_HEAD, N_HEAD, xres, B.resid.data_ptr(), 0, None, None, None, None, 0,
-                  _view(B.x0, sm_e, E), B.h.data_ptr(), 0, nxt, 1 if nfc is not None else 0,
-                  B.d_fc.data_ptr(), stream, label='attn.c_proj')
         fc_r1 = _rank1(nfc)
         mp_r1 = _rank1(nmp)
         last = i == L - 1
         if rounding == _lib.ROUNDING_FUSED:
-            # the whole MLP and its residual writer in one kernel: the [m, T, 2048] hidden layer stays on chip;
-            # then the next block's mix, norm and q/k/v dots (or the head input)
+            # attn.c_proj, residual, norm and the whole MLP with its residual writer in one kernel: neither the
+            # mid-block residual, its norm nor the [m, T, 2048] hidden layer reaches HBM; then the next block's
+            # mix, norm and q/k/v dots (or the head input)
             if not last:
                 nn = qkv_noise(i + 1)
                 want = any(v is not None for v in nn)
@@ -338,12 +335,16 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
                 nxt, nnext, ndots = (dot_vecs([nh], E), 1, B.d_head.data_ptr()) if nh is not None else (None, 0, None)
                 hout, split3 = (B.h3, 1) if W.fp32_head else (B.h, 0)
                 mixargs = (0, None, None, None, None, 0)
-            _call('noise_pop_mlp', popp, _view(B.h, T * E, E), blk['fc'].data_ptr(), ctypes.byref(fc_r1),
-                  B.d_fc.data_ptr(), blk['mp_perm'].data_ptr(), ctypes.byref(mp_r1), _view(B.resid, T * E, E),
-                  None if last else B.resid.data_ptr(), *mixargs, _view(B.x0, sm_e, E), hout.data_ptr(), split3,
-                  nxt, nnext, ndots, stream, label='mlp')
+            _call('noise_pop_attn_mlp', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), ctypes.byref(o_r1),
+                  B.d_attn.data_ptr(), N_HEAD, xres, blk['fc_perm'].data_ptr(), ctypes.byref(fc_r1),
+                  blk['mp_perm'].data_ptr(), ctypes.byref(mp_r1), None if last else B.resid.data_ptr(), *mixargs,
+                  _view(B.x0, sm_e, E), hout.data_ptr(), split3, nxt, nnext, ndots, stream, label='block')
             continue
-        # eager rounding: mlp.c_fc, ReLU^2 and partial dots for mlp.c_proj, then mlp.c_proj + residual
+        # eager rounding: attn.c_proj + residual; h = norm(x_mid) (no rank-1 terms in this mode)
+        _call('noise_pop_residual', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), E, ctypes.byref(o_r1),
+                  B.d_attn.data_ptr(), N_HEAD, N_HEAD, xres, B.resid.data_ptr(), 0, None, None, None, None, 0,
+                  _view(B.x0, sm_e, E), B.h.data_ptr(), 0, None, 0, None, stream, label='attn.c_proj')
+        # mlp.c_fc, ReLU^2 and partial dots for mlp.c_proj, then mlp.c_proj + residual
         mp_next = _rank1(nmp)
         _call('noise_pop_fc', popp, _view(B.h, T * E, E), blk['fc'].data_ptr(), ctypes.byref(fc_r1),
                   B.d_fc.data_ptr(), B.act.data_ptr(), ctypes.byref(mp_next) if nmp is not None else None,

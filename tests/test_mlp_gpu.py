@@ -152,3 +152,121 @@ def test_fused_mlp_rejects_bad_arguments():
         _lib.call('noise_pop_mlp', ctypes.byref(pop), _lib.View(16, 0, 512), 16, None, None, 16, None,
                   _lib.View(16, 0, 512), None, 0, None, None, None, None, 0, _lib.View(16, 0, 512), 16, 0, None, 0,
                   None, None)
+
+
+def _attn_case(m, T, seed, perturbed):
+    c = _case(m, T, seed, perturbed)
+    g = torch.Generator().manual_seed(seed + 100)
+    dirs = m // 2
+    c['y'] = torch.randn(m, T, 512, generator=g).bfloat16().to(DEV)
+    c['wo'] = ((torch.rand(512, 512, generator=g) * 2 - 1) * 1.5 * (3 / 512) ** 0.5).bfloat16().to(DEV)
+    if perturbed:
+        c['ao'] = torch.randn(dirs, 512, generator=g).to(DEV)
+        c['odots'] = torch.randn(m * T, 8, generator=g).to(DEV)
+    else:
+        c['ao'] = c['odots'] = None
+    return c
+
+
+def _run_attn(c, fused, mix, nnext, split3, with_xout):
+    """noise_pop_attn_mlp (fused) or noise_pop_residual (K = 512, with the c_fc dot) then noise_pop_mlp."""
+    from noise_amd import _lib
+    m, T = c['m'], c['T']
+    rows = m * T
+    stream = _lib.stream_ptr(DEV)
+    pop = _lib.Population(m, T, c['sign'].data_ptr(), 2, _lib.ROUNDING_FUSED)
+    V = lambda t, w: _lib.View(t.data_ptr(), T * w, w)
+    R = lambda a, b: _lib.Rank1(None, None, 0, 0) if a is None else _lib.Rank1(a.data_ptr(), _lib.ptr(b), a.stride(0),
+                                                                               0 if b is None else b.stride(0))
+    r_o, r_fc, r_pj = R(c['ao'], None), R(c['afc'], c['bfc']), R(c['apj'], c['bpj'])
+    nxt = (_lib.Rank1 * 3)(*[_lib.Rank1(None, t.data_ptr(), 0, t.stride(0)) for t in c['nb']])
+    ndots = torch.full((rows, max(nnext, 1)), float('nan'), device=DEV)
+    xres = c['xres'].clone()  # the block's residual input (also its output when with_xout)
+    width = 1536 if split3 else 512
+    hout = torch.full((m, T, width), float('nan'), dtype=torch.bfloat16, device=DEV)
+    eps = c['eps']
+    mixargs = (1, c['lam'].data_ptr(), c['lam'].data_ptr() + 4, None if eps is None else eps[:, 0].data_ptr(),
+               None if eps is None else eps[:, 1].data_ptr(), 0 if eps is None else eps.stride(0)) if mix else \
+        (0, None, None, None, None, 0)
+    xout = xres if with_xout else None
+    perm = {}
+    for k in ('wfc', 'wpj'):
+        perm[k] = torch.empty_like(c[k])
+        _lib.call('noise_mlp_proj_layout', c[k].data_ptr(), perm[k].data_ptr(), c[k].numel() // 2048, stream)
+    if fused:
+        _lib.call('noise_pop_attn_mlp', ctypes.byref(pop), V(c['y'], 512), c['wo'].data_ptr(), ctypes.byref(r_o),
+                  _lib.ptr(c['odots']), 8, V(xres, 512), perm['wfc'].data_ptr(), ctypes.byref(r_fc),
+                  perm['wpj'].data_ptr(), ctypes.byref(r_pj), _lib.ptr(xout), *mixargs, V(c['x0'], 512),
+                  hout.data_ptr(), int(split3), nxt, nnext, ndots.data_ptr(), stream)
+    else:
+        xmid = torch.empty(m, T, 512, device=DEV)
+        h = torch.empty(m, T, 512, dtype=torch.bfloat16, device=DEV)
+        dfc = torch.zeros(rows, device=DEV)
+        fcb = (_lib.Rank1 * 1)(_lib.Rank1(None, c['bfc'].data_ptr(), 0, c['bfc'].stride(0))) if c['bfc'] is not None \
+            else None
+        _lib.call('noise_pop_residual', ctypes.byref(pop), V(c['y'], 512), c['wo'].data_ptr(), 512, ctypes.byref(r_o),
+                  _lib.ptr(c['odots']), 8, 8, V(xres, 512), xmid.data_ptr(), 0, None, None, None, None, 0,
+                  V(c['x0'], 512), h.data_ptr(), 0, fcb, 1 if fcb is not None else 0, dfc.data_ptr(), stream)
+        _lib.call('noise_pop_mlp', ctypes.byref(pop), V(h, 512), c['wfc'].data_ptr(), ctypes.byref(r_fc),
+                  dfc.data_ptr(), perm['wpj'].data_ptr(), ctypes.byref(r_pj), V(xmid, 512), _lib.ptr(xout), *mixargs,
+                  V(c['x0'], 512), hout.data_ptr(), int(split3), nxt, nnext, ndots.data_ptr(), stream)
+    torch.cuda.synchronize()
+    return (None if xout is None else xout.cpu()), hout.float().cpu(), ndots[:, :nnext].cpu()
+
+
+@pytest.mark.parametrize('perturbed', [False, True], ids=['plain', 'perturbed'])
+@pytest.mark.parametrize('mix,nnext,split3,with_xout', [(True, 3, False, True), (True, 0, False, True),
+                                                        (False, 1, False, False), (False, 0, True, False)],
+                         ids=['mix-qkv-dots', 'mix-no-dots', 'last-head-dot', 'last-split3'])
+def test_attn_mlp_matches_residual_then_mlp(perturbed, mix, nnext, split3, with_xout):
+    """noise_pop_attn_mlp (attention projection, residual, norm and the MLP in one kernel) against
+    noise_pop_residual with K = 512 followed by noise_pop_mlp on the same inputs. The two round h to bf16 from
+    fp32 values summed in different orders, so a hidden value can round one bf16 ulp apart: outputs agree to
+    2e-3 of their scale, as the fused MLP does against its two-kernel form."""
+    c = _attn_case(4, 256, 2, perturbed)
+    print(f'attn+MLP: 4 members x 256 tokens, perturbed {perturbed}, mix {mix}, nnext {nnext}, split3 {split3}',
+          flush=True)
+    xo_f, ho_f, nd_f = _run_attn(c, True, mix, nnext, split3, with_xout)
+    xo_r, ho_r, nd_r = _run_attn(c, False, mix, nnext, split3, with_xout)
+    assert torch.isfinite(ho_f).all() and torch.isfinite(nd_f).all()
+    if with_xout:
+        scale = xo_r.abs().max()
+        assert (xo_f - xo_r).abs().max() <= 2e-3 * scale
+    hscale = ho_r[..., :512].abs().max()
+    assert (ho_f[..., :512] - ho_r[..., :512]).abs().max() <= (2.0 ** -7 + 2e-3) * hscale
+    if split3:
+        assert torch.equal(ho_f[..., 1024:], ho_f[..., :512])
+        assert (ho_f[..., :512] + ho_f[..., 512:1024] - ho_r[..., :512] - ho_r[..., 512:1024]).abs().max() <= 2e-3 * hscale
+    if nnext:
+        assert (nd_f - nd_r).abs().max() <= 2e-3 * nd_r.abs().max()
+
+
+def test_attn_mlp_block0_shared_residual():
+    """Block 0's residual input is shared by all members (member stride 0): every member reads the same rows."""
+    from noise_amd import _lib
+    c = _attn_case(2, 128, 5, True)
+    shared = c['xres'][:1].contiguous()
+    m, T = 2, 128
+    pop = _lib.Population(m, T, c['sign'].data_ptr(), 2, _lib.ROUNDING_FUSED)
+    copied = shared.expand(m, T, 512).contiguous()
+    out = {}
+    for name, xr in (('shared', _lib.View(shared.data_ptr(), 0, 512)),
+                     ('copied', _lib.View(copied.data_ptr(), T * 512, 512))):
+        perm = {}
+        for k in ('wfc', 'wpj'):
+            perm[k] = torch.empty_like(c[k])
+            _lib.call('noise_mlp_proj_layout', c[k].data_ptr(), perm[k].data_ptr(), c[k].numel() // 2048,
+                      _lib.stream_ptr(DEV))
+        xo = torch.empty(m, T, 512, device=DEV)
+        h = torch.empty(m, T, 512, dtype=torch.bfloat16, device=DEV)
+        r_o = _lib.Rank1(c['ao'].data_ptr(), None, 512, 0)
+        r_fc = _lib.Rank1(c['afc'].data_ptr(), c['bfc'].data_ptr(), 2048, 512)
+        r_pj = _lib.Rank1(c['apj'].data_ptr(), c['bpj'].data_ptr(), 512, 2048)
+        _lib.call('noise_pop_attn_mlp', ctypes.byref(pop), _lib.View(c['y'].data_ptr(), T * 512, 512),
+                  c['wo'].data_ptr(), ctypes.byref(r_o), c['odots'].data_ptr(), 8, xr, perm['wfc'].data_ptr(),
+                  ctypes.byref(r_fc), perm['wpj'].data_ptr(), ctypes.byref(r_pj), xo.data_ptr(), 0, None, None, None,
+                  None, 0, _lib.View(c['x0'].data_ptr(), T * 512, 512), h.data_ptr(), 0, None, 0, None,
+                  _lib.stream_ptr(DEV))
+        torch.cuda.synchronize()
+        out[name] = (xo.cpu(), h.cpu())
+    assert torch.equal(out['shared'][0], out['copied'][0]) and torch.equal(out['shared'][1], out['copied'][1])
