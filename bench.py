@@ -60,16 +60,15 @@ def kernel_flops_per_launch(name, label, members, T):
 
 
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'population_forward_1024x2048.md')
-ROCPROF_NAME = {'noise_pop_qkv': 'qkv_kernel', 'noise_pop_fc': 'fc_kernel', 'noise_pop_head_ce': 'head_ce_kernel',
-                'noise_pop_residual[attn.c_proj]': 'resid_kernel<512>',
-                'noise_pop_residual[mlp.c_proj]': 'resid_kernel<2048>', 'noise_pop_mlp[mlp]': 'mlp_kernel',
-                'noise_pop_attn_mlp[block]': 'mlp_kernel'}
+# entry point (bench label) -> the kernel name in the committed trace of the default workload
+ROCPROF_NAME = {'noise_pop_qkv': 'qkv_kernel<false>', 'noise_pop_head_ce': 'head_x_kernel<false, false>',
+                'noise_pop_attn_mlp[block]': 'mlp_kernel<true, 3, false, true>'}
 
 
 def profiled_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 summary (FETCH_SIZE + WRITE_SIZE, scaled
     by the 1 GiB copy calibration), or None."""
-    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel' if kernel.startswith('noise_attention') else None)
+    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel<true>' if kernel.startswith('noise_attention') else None)
     if not name or not os.path.exists(PROFILE):
         return None
     for line in open(PROFILE):
@@ -77,6 +76,22 @@ def profiled_traffic(kernel):
         if len(cells) == 7 and cells[0] == name:
             try:
                 return int((float(cells[5]) + float(cells[6])) * 1e9)
+            except ValueError:
+                return None
+    return None
+
+
+def profiled_mfma_busy(kernel):
+    """The kernel's MFMA-busy fraction from the committed counter table (SQ_VALU_MFMA_BUSY_CYCLES over the
+    cycles it ran, on its own clock), or None."""
+    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel<true>' if kernel.startswith('noise_attention') else None)
+    if not name or not os.path.exists(PROFILE):
+        return None
+    for line in open(PROFILE):
+        cells = [c.strip() for c in line.strip().strip('|').split('|')]
+        if len(cells) == 10 and cells[0] == name:
+            try:
+                return float(cells[2])
             except ValueError:
                 return None
     return None
@@ -265,6 +280,7 @@ def main():
         dk = kernels[dominant]
         roofline = dict(bound='mfma', kernel=dominant, achieved=round(dk['tflops'], 1), peak=BF16_PEAK / 1e12,
                         unit='TFLOP/s', frac=dk['mfma_frac'], traffic=profiled_traffic(dominant),
+                        counter_mfma_busy=profiled_mfma_busy(dominant),
                         flops_per_launch=kernel_flops_per_launch(*(dominant.rstrip(']').split('[') + [None])[:2],
                                                                  chunk, TOKENS))
 
