@@ -49,7 +49,7 @@ def kernel_flops_per_launch(name, label, members, T):
         return 2 * (2048 if label == 'mlp.c_proj' else 512) * 512 * rows
     if name == 'noise_pop_mlp':
         return 2 * 2 * 512 * 2048 * rows
-    if name == 'noise_pop_attn_mlp':
+    if name in ('noise_pop_attn_mlp', 'noise_pop_block'):
         return 2 * (512 * 512 + 2 * 512 * 2048) * rows
     if name == 'noise_pop_head_ce':
         return 2 * 512 * 4096 * rows
@@ -62,7 +62,7 @@ def kernel_flops_per_launch(name, label, members, T):
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'population_forward_1024x2048.md')
 # entry point (bench label) -> the kernel name in the committed trace of the default workload
 ROCPROF_NAME = {'noise_pop_qkv': 'qkv_kernel<false>', 'noise_pop_head_ce': 'head_x_kernel<false, false>',
-                'noise_pop_attn_mlp[block]': 'mlp_kernel<true, 3, false, true>'}
+                'noise_pop_block[block]': 'block_kernel<true, 3, false>'}
 
 
 def profiled_traffic(kernel):

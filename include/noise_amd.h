@@ -271,6 +271,21 @@ int noise_pop_attn_mlp(const noise_population_t *pop, noise_view_t y, const void
                        int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
                        int64_t nnext, float *next_dots, noise_stream_t stream);
 
+/* noise_pop_attn_mlp's arithmetic with two waves per SIMD (8 waves of 16 tokens per 128-token tile on
+ * v_mfma_f32_16x16x32_bf16): same arguments and results (up to fp32 summation order), with w_fc and w_proj
+ * in the column order noise_block_weight_layout writes instead. hout 16 B aligned. No counterpart in the
+ * reference beyond the call sites noise_pop_attn_mlp replaces (eggroll.py:92-93). */
+int noise_pop_block(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
+                    const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc, const noise_rank1_t *r_fc,
+                    const void *w_proj, const noise_rank1_t *r_proj, float *xout, int mix, const float *lam_r,
+                    const float *lam_x, const float *eps_r, const float *eps_x, int64_t eps_stride, noise_view_t x0,
+                    void *hout, int split3, const noise_rank1_t *next, int64_t nnext, float *next_dots,
+                    noise_stream_t stream);
+
+/* w [rows][cols] bf16 -> the column order noise_pop_block reads: within every 32 columns, position 8g + j
+ * (g < 4) holds column 4g + j for j < 4 and 16 + 4g + (j - 4) for j >= 4. cols a multiple of 32. */
+int noise_block_weight_layout(const void *w, void *out, int64_t rows, int64_t cols, noise_stream_t stream);
+
 /* mlp.c_proj [rows][2048] bf16 -> the column order noise_pop_mlp reads: within every 16 columns, the groups of
  * 4 are stored in the order 0, 2, 1, 3 (so each 16-deep slice of the hidden layer pairs with the registers the
  * c_fc product leaves it in). out and w distinct; one pass per weight update. */

@@ -1,0 +1,532 @@
+// The tail of a population block in one kernel, two waves per SIMD (eggroll.py:92-93, then the next block's
+// mixing, norm and dots, eggroll.py:77-82 / 94):
+//
+//   x_mid = x + y W_o^T + sign (y . b_o) a_o                      attn.c_proj + residual      (never stored)
+//   h     = bf16(norm(x_mid))                                                                  (never stored)
+//   hid   = relu(h W_fc^T + sign (h . b_fc) a_fc)^2               mlp.c_fc, ReLU^2            (never stored)
+//   y     = x_mid + hid W_proj^T + sign (hid . b_proj) a_proj     mlp.c_proj + residual
+//   [y = rl y + ml x0]  ->  xout = y, hout = bf16(norm(y)), next_dots = norm(y) . b_next
+//
+// A workgroup owns 128 tokens of one member in 8 waves of 16 tokens, two waves per SIMD (about 250 registers
+// each), on v_mfma_f32_16x16x32_bf16 with the weights as the A operand and the wave's tokens as the B operand:
+//   - a wave's 16 token rows (y, then h) sit in registers as the B operand of every product (64 registers);
+//   - its [512 outputs x 16 tokens] accumulate in 32 blocks of 16 x 16 (128 registers): x_mid, then x_mid plus
+//     the MLP product;
+//   - weights stream through LDS by direct global -> LDS copies of whole rows segments, double buffered:
+//     W_o in 8 steps of 64 columns ([512 rows][128 B]), then 64 hidden steps of 32 units, each holding those
+//     units' c_fc rows ([8 k tiles][32 rows][128 B]) and mlp.c_proj columns ([512 rows][64 B]); the 16 B chunks
+//     of a row are XOR-swizzled by row so that a fragment read (16 rows, 4 consecutive chunks) hits every
+//     bank once;
+//   - the 16 x 16 D layout (lane l: token l % 16, rows 4 (l / 16) .. + 4) of two consecutive row blocks is the
+//     B operand of one 32-deep k block once the k index is permuted within each 32 (lane group g holds rows
+//     4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3): h goes from the x_mid accumulators into the first product's
+//     operand, and the ReLU^2 of the first product's two blocks into the second product's, without leaving the
+//     lane. c_fc and mlp.c_proj therefore come with their columns in that permuted order
+//     (noise_block_weight_layout);
+//   - a token's 512 features are spread over the four lanes l % 16 + 16 g: RMSNorm and the dots need two
+//     exchanges (lane ^ 16, lane ^ 32).
+// The second wave on each SIMD issues while the other waits on its fragment reads, its ReLU^2 or the barrier.
+#include "common.hpp"
+#include "mfma.hpp"
+#include "tile.hpp"
+
+namespace noise {
+namespace {
+
+constexpr float kBlkEps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps
+constexpr int kBlkThreads = 512;   // 8 waves, two per SIMD
+constexpr int kBlkTok = 128;       // tokens per workgroup (16 per wave)
+constexpr int kHidden = 2048, kModel = 512;
+constexpr int kUnits = 32;         // hidden units per step
+constexpr int kSteps = kHidden / kUnits;
+constexpr int kBuf = 65536;        // a W_o step ([512 rows][128 B]); two per LDS
+constexpr int kStage = 32768;      // an MLP stage (a step's c_fc rows or its mlp.c_proj columns); four per LDS
+constexpr int kVec = 2 * kBuf;     // fp32 vectors after the two step buffers:
+constexpr int kVAfc = kVec;                      // c_fc's a       [2048]
+constexpr int kVBpj = kVAfc + kHidden * 4;       // mlp.c_proj's b [2048]
+constexpr int kVApj = kVBpj + kHidden * 4;       // mlp.c_proj's a [512]
+constexpr int kVNb = kVApj + kModel * 4;         // next b         [3][512]
+constexpr int kVAo = kVNb + 3 * kModel * 4;      // attn.c_proj's a [512]
+constexpr int kVBfc = kVAo + kModel * 4;         // c_fc's b       [512]
+constexpr int kBlkLds = kVBfc + kModel * 4;      // 156 KiB
+static_assert(kBlkLds <= 160 * 1024, "LDS of one CU");
+
+struct BlockArgs {
+    int members, tokens, dir_div;
+    const float *sign;
+    const __bf16 *y;                       // attention output, bf16 [m][T][512] (strided)
+    int64_t ys_m, ys_t;
+    const __bf16 *wo;                      // attn.c_proj [512][512]
+    const float *ao;                       // its rank-1 a [dirs][512] or NULL
+    int64_t ao_stride;
+    const float *odots;                    // y . b_o partial sums [rows][odots_n]
+    int odots_n;
+    const float *xres;                     // block residual input fp32 (member stride may be 0)
+    int64_t xr_m, xr_t;
+    const __bf16 *wfc;                     // mlp.c_fc [2048][512], columns permuted
+    const float *afc, *bfc;                // c_fc rank-1 a [dirs][2048], b [dirs][512] or NULL
+    int64_t afc_stride, bfc_stride;
+    const __bf16 *wpj;                     // mlp.c_proj [512][2048], columns permuted
+    const float *apj, *bpj;                // mlp.c_proj rank-1 a [dirs][512], b [dirs][2048] or NULL
+    int64_t apj_stride, bpj_stride;
+    float *xout;                           // residual out [m][T][512] fp32, or NULL
+    const float *lam_r, *lam_x;            // next block's mixing scalars (device)
+    const float *eps_r, *eps_x;
+    int64_t eps_stride;
+    const float *x0;
+    int64_t x0_m, x0_t;
+    __bf16 *hout;                          // [m][T][512], or [m][T][1536] = [hi | lo | hi] with split3
+    const float *nb[3];
+    int64_t nb_stride[3];
+    float *ndots;                          // [rows][NNEXT]
+};
+
+// sum over the four lanes holding one token's features (l % 16 + 16 g)
+__device__ __forceinline__ float token_sum(float v) {
+    v += __shfl_xor(v, 16, 64);
+    return v + __shfl_xor(v, 32, 64);
+}
+
+template <bool MIX, int NNEXT, bool SPLIT3>
+__global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
+    __shared__ __attribute__((aligned(16))) char lds[kBlkLds];
+    const int T = p.tokens, tiles_t = T / kBlkTok;
+    const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * kBlkTok;
+    const int tid = threadIdx.x, lane = tid & 63, tl = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int dir = m / p.dir_div;
+    const float sgn = p.sign ? p.sign[m] : 0.f;
+    const int tok = t0 + 16 * wave + tl;
+    const int64_t row = (int64_t)m * T + tok;
+    const unsigned lbase = lds_addr(lds);
+
+    // per-member vectors into LDS (zeros when a matrix is unperturbed, so no branches later)
+    {
+        auto vcopy = [&](const float *src, int off, int n) {
+            float *dst = reinterpret_cast<float *>(lds + off);
+            for (int i = tid; i < n / 4; i += kBlkThreads)
+                st4(dst + 4 * i, src ? ld4(src + 4 * i) : float4{0.f, 0.f, 0.f, 0.f});
+        };
+        vcopy(p.afc ? p.afc + dir * p.afc_stride : nullptr, kVAfc, kHidden);
+        vcopy(p.apj ? p.bpj + dir * p.bpj_stride : nullptr, kVBpj, kHidden);
+        vcopy(p.apj ? p.apj + dir * p.apj_stride : nullptr, kVApj, kModel);
+#pragma unroll
+        for (int k = 0; k < NNEXT; ++k) vcopy(p.nb[k] + dir * p.nb_stride[k], kVNb + k * kModel * 4, kModel);
+        vcopy(p.ao ? p.ao + dir * p.ao_stride : nullptr, kVAo, kModel);
+        vcopy(p.afc ? p.bfc + dir * p.bfc_stride : nullptr, kVBfc, kModel);
+    }
+
+    // LDS byte offset of 16 B chunk c of row r: in 128 B rows (chunks swizzled by row pair) and in 64 B rows
+    // (swizzled by row quad); either way the 16 rows x 4 chunks of a fragment read cover all banks once
+    auto off128 = [](int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); };
+    auto off64 = [](int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); };
+    // copies of whole 128 B row segments (8 rows per wave-wide copy) and of 64 B ones (16 rows)
+    const int r8 = lane >> 3, p8 = lane & 7, r16 = lane >> 2, p16 = lane & 3;
+    auto copy128 = [&](const __bf16 *rows, int64_t ld, int r0, unsigned dst) {  // rows r0 .. r0 + 7
+        const int c = p8 ^ (((r0 + r8) >> 1) & 7);
+        lds_dma16_at(rows + (int64_t)r0 * ld, (unsigned)(r8 * ld * 2 + c * 16), dst + r0 * 128);
+    };
+    auto copy64 = [&](const __bf16 *rows, int64_t ld, int r0, unsigned dst) {  // rows r0 .. r0 + 15
+        const int c = p16 ^ (((r0 + r16) >> 2) & 3);
+        lds_dma16_at(rows + (int64_t)r0 * ld, (unsigned)(r16 * ld * 2 + c * 16), dst + r0 * 64);
+    };
+    auto issue_o = [&](int s) {  // W_o columns 64 s .. + 64: [512 rows][128 B], 64 copies, 8 per wave
+        const unsigned dst = lbase + (s & 1) * kBuf;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) copy128(p.wo + 64 * s, kModel, 8 * (8 * wave + i), dst);
+    };
+    // the MLP's weights in 128 stages of 32 KiB through four stage buffers: stage 2 js holds the c_fc rows of
+    // hidden units 32 js .. + 32 as [8 k tiles][32 rows][128 B] (wave w copies k tile w), stage 2 js + 1 their
+    // mlp.c_proj columns as [512 rows][64 B] (wave w copies rows 64 w .. + 64); 4 copies per wave per stage
+    auto issue_stage = [&](int k) {
+        const unsigned dst = lbase + (k & 3) * kStage;
+        const int js = k >> 1;
+        if ((k & 1) == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                copy128(p.wfc + (int64_t)(kUnits * js) * kModel + 64 * wave, kModel, 8 * i, dst + wave * 4096);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) copy64(p.wpj + kUnits * js, kHidden, 64 * wave + 16 * i, dst);
+        }
+    };
+    const int fr = lane & 15, fc = lane >> 4;  // the row and chunk a lane reads in a fragment
+    // A fragments: W_o rows 16 ob .. + 16, k block h of the step; c_fc rows 16 hb .. + 16 of k block kb;
+    // mlp.c_proj rows 16 ob .. + 16
+    auto frag_o = [&](const char *buf, int ob, int h) {
+        return *reinterpret_cast<const bf16x8 *>(buf + off128(16 * ob + fr, 4 * h + fc));
+    };
+    auto frag_fc = [&](const char *buf, int hb, int kb) {
+        return *reinterpret_cast<const bf16x8 *>(buf + (kb >> 1) * 4096 + off128(16 * hb + fr, 4 * (kb & 1) + fc));
+    };
+    auto frag_pj = [&](const char *buf, int ob) {
+        return *reinterpret_cast<const bf16x8 *>(buf + off64(16 * ob + fr, fc));
+    };
+
+    issue_o(0);
+    // this lane's y row: xf[kb] = y[tok][32 kb + 8 g .. + 8], the B operand of k block kb
+    bf16x8 xf[16];
+    {
+        const __bf16 *yr = p.y + m * p.ys_m + (int64_t)tok * p.ys_t + 8 * g;
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb) xf[kb] = load_bf16x8(yr + 32 * kb);
+    }
+    vm_wait<0>();
+    __syncthreads();
+
+    // ---- attn.c_proj: out[ob] = W_o[16 ob ..] . y^T in 8 steps of two k blocks (unrolled: xf is indexed by
+    // the step)
+    f32x4 out[32];
+#pragma unroll
+    for (int ob = 0; ob < 32; ++ob) out[ob] = f32x4{};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        if (s + 1 < 8) issue_o(s + 1);  // its buffer was last read in step s - 1, before the barrier below
+        const char *buf = lds + (s & 1) * kBuf;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            bf16x8 a[2];
+            a[0] = frag_o(buf, 0, h);
+#pragma unroll
+            for (int ob = 0; ob < 32; ++ob) {
+                if (ob + 1 < 32) a[(ob + 1) & 1] = frag_o(buf, ob + 1, h);
+                out[ob] = mfma16x16x32(a[ob & 1], xf[2 * s + h], out[ob]);
+            }
+        }
+        vm_wait<0>();
+        __syncthreads();
+    }
+    // all stage buffers are free: the first three MLP stages arrive during the epilogue below
+    issue_stage(0);
+    issue_stage(1);
+    issue_stage(2);
+
+    // ---- x_mid = x + (product + sign (y . b_o) a_o); h = bf16(norm(x_mid)) into xf; c_fc's h . b from fp32
+    float corr_fc = 0.f;
+    {
+        float osum = 0.f;
+        if (p.ao)
+            for (int k = 0; k < p.odots_n; ++k) osum += p.odots[row * p.odots_n + k];
+        const float corr_o = sgn * osum;
+        const float *xr = p.xres + m * p.xr_m + (int64_t)tok * p.xr_t + 4 * g;
+        const float *ao = reinterpret_cast<const float *>(lds + kVAo) + 4 * g;
+        float ssq = 0.f;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {  // 8 output blocks at a time: their residual loads in flight together
+            float4 xv[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i) xv[i] = ld4(xr + 16 * (8 * q + i));
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int ob = 8 * q + i;
+                const float4 a4 = ld4(ao + 16 * ob);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float v = f4get(xv[i], r) + (out[ob][r] + corr_o * f4get(a4, r));
+                    out[ob][r] = v;
+                    ssq += v * v;
+                }
+            }
+        }
+        const float rstd = rsqrtf(token_sum(ssq) * (1.0f / kModel) + kBlkEps);
+        if (p.afc) {
+            const float *bf = reinterpret_cast<const float *>(lds + kVBfc) + 4 * g;
+            float d = 0.f;
+#pragma unroll
+            for (int ob = 0; ob < 32; ++ob) {
+                const float4 b4 = ld4(bf + 16 * ob);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) d += out[ob][r] * f4get(b4, r);
+            }
+            corr_fc = sgn * (rstd * token_sum(d));
+        }
+        // k block kb of the first product: features 32 kb + 4 g + (0..3) from block 2 kb, 32 kb + 16 + 4 g + (0..3)
+        // from block 2 kb + 1 (c_fc's columns come in that order)
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                xf[kb][r] = (__bf16)(out[2 * kb][r] * rstd);
+                xf[kb][4 + r] = (__bf16)(out[2 * kb + 1][r] * rstd);
+            }
+    }
+
+    // ---- the MLP over 64 steps of 32 hidden units, accumulating onto x_mid
+    float pd = 0.f;  // this lane's share of hid . b_proj
+    const float *afc_l = reinterpret_cast<const float *>(lds + kVAfc) + 4 * g;
+    const float *bpj_l = reinterpret_cast<const float *>(lds + kVBpj) + 4 * g;
+    vm_wait<8>();     // stage 0 landed (stages 1 and 2 may still be in flight)
+    __syncthreads();
+    constexpr int kStages = 2 * kSteps;
+    // after stage k: stage k + 1 must have landed; the stages issued after it (up to k + 3) may still fly
+    auto stage_end = [&](int k) {
+        vm_wait_groups<4, 2>(kStages - 2 - k < 2 ? kStages - 2 - k : 2);
+        __syncthreads();  // every wave's copies of stage k + 1 landed; every wave is done with buffer k & 3
+    };
+#pragma unroll 1
+    for (int js = 0; js < kSteps; ++js) {
+        // stage 2 js (c_fc rows): its buffer was last read in stage 2 js - 1 ... the copies of stage 2 js + 3 go
+        // into the buffer of stage 2 js - 1, which every wave finished before the barrier that ended it
+        if (2 * js + 3 < kStages) issue_stage(2 * js + 3);
+        const char *buf;
+        buf = lds + ((2 * js) & 3) * kStage;
+        // first product: hacc[hb] = c_fc rows 32 js + 16 hb .. + 16 against the 16 k blocks of h
+        f32x4 hacc[2] = {f32x4{}, f32x4{}};
+        {
+            bf16x8 a[2];
+            a[0] = frag_fc(buf, 0, 0);
+#pragma unroll
+            for (int f = 0; f < 32; ++f) {
+                if (f + 1 < 32) a[(f + 1) & 1] = frag_fc(buf, (f + 1) & 1, (f + 1) >> 1);
+                hacc[f & 1] = mfma16x16x32(a[f & 1], xf[f >> 1], hacc[f & 1]);
+            }
+        }
+        stage_end(2 * js);
+        // stage 2 js + 1 (mlp.c_proj columns)
+        if (2 * js + 4 < kStages) issue_stage(2 * js + 4);
+        buf = lds + ((2 * js + 1) & 3) * kStage;
+        // ReLU^2 with the rank-1 term, bf16, packed as the second product's B operand (k = 8 g + j holds hidden unit
+        // 4 g + j of block 0 for j < 4, of block 1 for j >= 4); this lane's share of hid . b_proj
+        bf16x8 hb;
+        {
+            const float4 a0 = ld4(afc_l + kUnits * js), a1 = ld4(afc_l + kUnits * js + 16);
+            const float4 b0 = ld4(bpj_l + kUnits * js), b1 = ld4(bpj_l + kUnits * js + 16);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v0 = fmaxf(hacc[0][r] + corr_fc * f4get(a0, r), 0.f);
+                float v1 = fmaxf(hacc[1][r] + corr_fc * f4get(a1, r), 0.f);
+                hb[r] = (__bf16)(v0 * v0);
+                hb[4 + r] = (__bf16)(v1 * v1);
+            }
+            // hid . b with both in bf16, as the reference's autocast x @ b (eggroll.py:58) multiplies them
+#pragma unroll
+            for (int r = 0; r < 4; r += 2) {
+                pd = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{hb[r], hb[r + 1]},
+                                                     bf16x2{(__bf16)f4get(b0, r), (__bf16)f4get(b0, r + 1)}, pd, false);
+                pd = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{hb[4 + r], hb[5 + r]},
+                                                     bf16x2{(__bf16)f4get(b1, r), (__bf16)f4get(b1, r + 1)}, pd, false);
+            }
+        }
+        // second product: out[ob] += mlp.c_proj rows 16 ob .. + 16, columns of this step
+        {
+            bf16x8 a[2];
+            a[0] = frag_pj(buf, 0);
+#pragma unroll
+            for (int ob = 0; ob < 32; ++ob) {
+                if (ob + 1 < 32) a[(ob + 1) & 1] = frag_pj(buf, ob + 1);
+                out[ob] = mfma16x16x32(a[ob & 1], hb, out[ob]);
+            }
+        }
+        stage_end(2 * js + 1);
+    }
+
+    // ---- epilogue: y = out + sign (hid . b_proj) a_proj [, mixing], RMSNorm, next dots, stores
+    const float corr = p.apj ? sgn * token_sum(pd) : 0.f;
+    float rl = 0.f, ml = 0.f;
+    if constexpr (MIX) {
+        rl = *p.lam_r;
+        ml = *p.lam_x;
+        if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
+        if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
+    }
+    float ssq = 0.f;
+    {
+        const float *apj = reinterpret_cast<const float *>(lds + kVApj) + 4 * g;
+        const float *zr = MIX ? p.x0 + m * p.x0_m + (int64_t)tok * p.x0_t + 4 * g : nullptr;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            float4 zv[8];
+            if constexpr (MIX) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) zv[i] = ld4(zr + 16 * (8 * q + i));
+            }
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const int ob = 8 * q + i;
+                const float4 a4 = ld4(apj + 16 * ob);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float v = out[ob][r] + corr * f4get(a4, r);
+                    if constexpr (MIX) v = rl * v + ml * f4get(zv[i], r);
+                    out[ob][r] = v;
+                    ssq += v * v;
+                }
+            }
+        }
+    }
+    const float rstd = rsqrtf(token_sum(ssq) * (1.0f / kModel) + kBlkEps);
+#pragma unroll
+    for (int k = 0; k < NNEXT; ++k) {
+        const float *nb = reinterpret_cast<const float *>(lds + kVNb + k * kModel * 4) + 4 * g;
+        float d = 0.f;
+#pragma unroll
+        for (int ob = 0; ob < 32; ++ob) {
+            const float4 b4 = ld4(nb + 16 * ob);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) d += out[ob][r] * f4get(b4, r);
+        }
+        d = token_sum(d);
+        if (g == 0) p.ndots[row * NNEXT + k] = rstd * d;
+    }
+    // whole-line stores through the wave's 16 KiB of the (free) step buffers: rows of 1 KiB, 16 B chunk c of
+    // row t at position c ^ t
+    char *stg = lds + wave * 16384;
+    const int64_t row0 = (int64_t)m * T + t0 + 16 * wave;  // the wave's first token row
+    if (p.xout) {
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int ob = 16 * half + i, c = 4 * i + g;
+                st4(reinterpret_cast<float *>(stg + tl * 1024 + ((c ^ tl) << 4)),
+                    float4{out[ob][0], out[ob][1], out[ob][2], out[ob][3]});
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int it = 0; it < 16; ++it)
+                st4(p.xout + (row0 + it) * kModel + 256 * half + 4 * lane,
+                    *reinterpret_cast<const float4 *>(stg + it * 1024 + ((lane ^ it) << 4)));
+            wave_lds_sync();  // the staging rows are rewritten next
+        }
+    }
+    // bf16 rows (hi, and lo for the split3 head input): 1 KiB rows, 16 B chunk c of row t at c ^ t
+    const int width = SPLIT3 ? 3 * kModel : kModel;
+#pragma unroll
+    for (int part = 0; part < (SPLIT3 ? 2 : 1); ++part) {
+#pragma unroll
+        for (int ob = 0; ob < 32; ++ob) {
+            bf16x4 v;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float h = out[ob][r] * rstd;
+                const __bf16 hi = (__bf16)h;
+                v[r] = part == 0 ? hi : (__bf16)(h - (float)hi);
+            }
+            const int c16 = 2 * ob + (g >> 1);
+            store_bf16x4(reinterpret_cast<__bf16 *>(stg + tl * 1024 + ((c16 ^ tl) << 4) + 8 * (g & 1)), v);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int it = 0; it < 16; ++it) {
+            const bf16x8 v = *reinterpret_cast<const bf16x8 *>(stg + it * 1024 + ((lane ^ it) << 4));
+            __bf16 *dst = p.hout + (row0 + it) * width + 8 * lane;
+            if (part == 0) {
+                store_bf16x8(dst, v);
+                if constexpr (SPLIT3) store_bf16x8(dst + 2 * kModel, v);
+            } else {
+                store_bf16x8(dst + kModel, v);
+            }
+        }
+        wave_lds_sync();
+    }
+}
+
+// w [rows][cols] bf16 -> the column order block_kernel reads: within every 32 columns, position 8 g + j holds
+// column 4 g + j (j < 4) or 16 + 4 g + (j - 4) (j >= 4). One thread per 4-wide group.
+__global__ __launch_bounds__(256) void block_layout_kernel(const __bf16 *w, __bf16 *out, int64_t groups) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= groups) return;
+    const int64_t q = i >> 3;        // 32-wide block
+    const int pos = (int)(i & 7);    // 4-wide group at positions 4 pos .. 4 pos + 3
+    const int gq = pos >> 1, hi = pos & 1;
+    const int src = hi ? 4 + gq : gq;  // source 4-wide group within the 32
+    store_bf16x4(out + 4 * i, load_bf16x4(w + 32 * q + 4 * src));
+}
+
+template <bool MIX, int NNEXT>
+void launch_block_n(const BlockArgs &a, bool split3, dim3 grid, hipStream_t s) {
+    if (split3)
+        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, true>), grid, dim3(kBlkThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, false>), grid, dim3(kBlkThreads), 0, s, a);
+}
+
+template <bool MIX>
+void launch_block(const BlockArgs &a, int nnext, bool split3, dim3 grid, hipStream_t s) {
+    switch (nnext) {
+        case 0: launch_block_n<MIX, 0>(a, split3, grid, s); break;
+        case 1: launch_block_n<MIX, 1>(a, split3, grid, s); break;
+        case 2: launch_block_n<MIX, 2>(a, split3, grid, s); break;
+        default: launch_block_n<MIX, 3>(a, split3, grid, s); break;
+    }
+}
+
+}  // namespace
+}  // namespace noise
+
+using namespace noise;
+
+extern "C" int noise_block_weight_layout(const void *w, void *out, int64_t rows, int64_t cols, noise_stream_t stream) {
+    clear_error();
+    NOISE_CHECK_ARG(w && out && w != out && rows > 0 && cols > 0 && cols % 32 == 0 && aligned(w, 8) && aligned(out, 8),
+                    "noise_block_weight_layout: distinct 8 B aligned buffers, rows > 0, cols a multiple of 32");
+    const int64_t groups = rows * cols / 4;
+    hipLaunchKernelGGL(block_layout_kernel, dim3((unsigned)((groups + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (const __bf16 *)w, (__bf16 *)out, groups);
+    return launch_status("noise_block_weight_layout");
+}
+
+extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
+                               const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
+                               const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout,
+                               int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+                               int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
+                               int64_t nnext, float *next_dots, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_block";
+    NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
+    NOISE_CHECK_ARG(pop->tokens % kBlkTok == 0, "%s: tokens (%lld) must be a multiple of %d", fn,
+                    (long long)pop->tokens, kBlkTok);
+    NOISE_CHECK_ARG(pop->members * pop->tokens < (1ll << 31), "%s: members * tokens must stay below 2^31", fn);
+    NOISE_CHECK_ARG(pop->rounding == NOISE_ROUNDING_FUSED, "%s: fused rounding only", fn);
+    NOISE_CHECK_ARG(y.ptr && aligned(y.ptr, 16) && y.sm % 8 == 0 && y.st % 8 == 0, "%s: y misaligned", fn);
+    NOISE_CHECK_ARG(w_o && w_fc && w_proj && aligned(w_o, 16) && aligned(w_fc, 16) && aligned(w_proj, 16),
+                    "%s: weights NULL or misaligned", fn);
+    NOISE_CHECK_ARG(xres.ptr && aligned(xres.ptr, 16) && xres.sm % 4 == 0 && xres.st % 4 == 0, "%s: bad xres", fn);
+    NOISE_CHECK_ARG(!xout || aligned(xout, 16), "%s: xout misaligned", fn);
+    NOISE_CHECK_ARG(!mix || (x0.ptr && aligned(x0.ptr, 16) && x0.sm % 4 == 0 && x0.st % 4 == 0 && lam_r && lam_x),
+                    "%s: mixing needs x0 and the mixing scalars", fn);
+    NOISE_CHECK_ARG(!(eps_r || eps_x) || (mix && pop->sign), "%s: mixing-scalar noise needs mix and sign", fn);
+    NOISE_CHECK_ARG(hout && aligned(hout, 16), "%s: hout NULL or misaligned", fn);
+    NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || (next && next_dots)), "%s: bad next-dot request", fn);
+    const bool po = r_o && r_o->a, pfc = r_fc && r_fc->a, ppj = r_proj && r_proj->a;
+    NOISE_CHECK_ARG(!po || (pop->sign && o_dots && o_dots_n >= 1 && aligned(r_o->a, 16) && r_o->a_stride % 4 == 0),
+                    "%s: attn.c_proj noise needs sign, dots and 16 B aligned a rows", fn);
+    NOISE_CHECK_ARG(!pfc || (pop->sign && r_fc->b && aligned(r_fc->a, 16) && aligned(r_fc->b, 16) &&
+                             r_fc->a_stride % 4 == 0 && r_fc->b_stride % 4 == 0),
+                    "%s: c_fc noise needs sign and 16 B aligned a, b rows", fn);
+    NOISE_CHECK_ARG(!ppj || (pop->sign && r_proj->b && aligned(r_proj->a, 16) && aligned(r_proj->b, 16) &&
+                             r_proj->a_stride % 4 == 0 && r_proj->b_stride % 4 == 0),
+                    "%s: mlp.c_proj noise needs sign and 16 B aligned a, b rows", fn);
+    BlockArgs a{};
+    a.members = (int)pop->members; a.tokens = (int)pop->tokens; a.dir_div = (int)pop->dir_div; a.sign = pop->sign;
+    a.y = (const __bf16 *)y.ptr; a.ys_m = y.sm; a.ys_t = y.st;
+    a.wo = (const __bf16 *)w_o;
+    a.ao = po ? r_o->a : nullptr; a.ao_stride = po ? r_o->a_stride : 0;
+    a.odots = po ? o_dots : nullptr; a.odots_n = po ? (int)o_dots_n : 0;
+    a.xres = (const float *)xres.ptr; a.xr_m = xres.sm; a.xr_t = xres.st;
+    a.wfc = (const __bf16 *)w_fc;
+    a.afc = pfc ? r_fc->a : nullptr; a.bfc = pfc ? r_fc->b : nullptr;
+    a.afc_stride = pfc ? r_fc->a_stride : 0; a.bfc_stride = pfc ? r_fc->b_stride : 0;
+    a.wpj = (const __bf16 *)w_proj;
+    a.apj = ppj ? r_proj->a : nullptr; a.bpj = ppj ? r_proj->b : nullptr;
+    a.apj_stride = ppj ? r_proj->a_stride : 0; a.bpj_stride = ppj ? r_proj->b_stride : 0;
+    a.xout = xout;
+    a.lam_r = lam_r; a.lam_x = lam_x; a.eps_r = eps_r; a.eps_x = eps_x; a.eps_stride = eps_stride;
+    a.x0 = (const float *)x0.ptr; a.x0_m = x0.sm; a.x0_t = x0.st;
+    a.hout = (__bf16 *)hout;
+    for (int k = 0; k < 3; ++k) {
+        a.nb[k] = k < nnext ? next[k].b : nullptr;
+        a.nb_stride[k] = k < nnext ? next[k].b_stride : 0;
+        if (k < nnext)
+            NOISE_CHECK_ARG(next[k].b && aligned(next[k].b, 16) && next[k].b_stride % 4 == 0,
+                            "%s: next b %d NULL or misaligned", fn, k);
+    }
+    a.ndots = next_dots;
+    const dim3 grid((unsigned)(pop->members * (pop->tokens / kBlkTok)));
+    if (mix)
+        launch_block<true>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
+    else
+        launch_block<false>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
+    return launch_status(fn);
+}

@@ -139,12 +139,11 @@ class Weights:
             blk = dict(q=bf(pre + 'attn.c_q.weight'), k=bf(pre + 'attn.c_k.weight'), v=bf(pre + 'attn.c_v.weight'),
                        o=bf(pre + 'attn.c_proj.weight'), fc=bf(pre + 'mlp.c_fc.weight'),
                        mp=bf(pre + 'mlp.c_proj.weight'))
-            # mlp.c_proj and mlp.c_fc in the fused block kernel's column order (within every 16 columns the
-            # groups of four permuted; c_fc's [2048][512] permuted as 512 rows of 2048)
-            for src, dst in (('mp', 'mp_perm'), ('fc', 'fc_perm')):
+            # mlp.c_fc and mlp.c_proj in the block kernel's column order (within every 32 columns)
+            for src, dst in (('mp', 'mp_blk'), ('fc', 'fc_blk')):
                 blk[dst] = torch.empty_like(blk[src])
-                _lib.call('noise_mlp_proj_layout', blk[src].data_ptr(), blk[dst].data_ptr(),
-                          blk[src].numel() // 2048, _lib.stream_ptr(dev))
+                _lib.call('noise_block_weight_layout', blk[src].data_ptr(), blk[dst].data_ptr(), blk[src].shape[0],
+                          blk[src].shape[1], _lib.stream_ptr(dev))
             if has_ve(i, n_layer):
                 # the gate's product runs under autocast: its weights enter rounded to bf16
                 blk['gate'] = bf(pre + 'attn.ve_gate.weight').to(F32).contiguous()
@@ -335,9 +334,9 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
                 nxt, nnext, ndots = (dot_vecs([nh], E), 1, B.d_head.data_ptr()) if nh is not None else (None, 0, None)
                 hout, split3 = (B.h3, 1) if W.fp32_head else (B.h, 0)
                 mixargs = (0, None, None, None, None, 0)
-            _call('noise_pop_attn_mlp', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), ctypes.byref(o_r1),
-                  B.d_attn.data_ptr(), N_HEAD, xres, blk['fc_perm'].data_ptr(), ctypes.byref(fc_r1),
-                  blk['mp_perm'].data_ptr(), ctypes.byref(mp_r1), None if last else B.resid.data_ptr(), *mixargs,
+            _call('noise_pop_block', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), ctypes.byref(o_r1),
+                  B.d_attn.data_ptr(), N_HEAD, xres, blk['fc_blk'].data_ptr(), ctypes.byref(fc_r1),
+                  blk['mp_blk'].data_ptr(), ctypes.byref(mp_r1), None if last else B.resid.data_ptr(), *mixargs,
                   _view(B.x0, sm_e, E), hout.data_ptr(), split3, nxt, nnext, ndots, stream, label='block')
             continue
         # eager rounding: attn.c_proj + residual; h = norm(x_mid) (no rank-1 terms in this mode)

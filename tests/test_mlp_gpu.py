@@ -270,3 +270,78 @@ def test_attn_mlp_block0_shared_residual():
         torch.cuda.synchronize()
         out[name] = (xo.cpu(), h.cpu())
     assert torch.equal(out['shared'][0], out['copied'][0]) and torch.equal(out['shared'][1], out['copied'][1])
+
+
+def _run_block(c, mix, nnext, split3, with_xout, kernel):
+    """noise_pop_block (two waves per SIMD) or noise_pop_attn_mlp on the same inputs."""
+    from noise_amd import _lib
+    m, T = c['m'], c['T']
+    rows = m * T
+    stream = _lib.stream_ptr(DEV)
+    pop = _lib.Population(m, T, c['sign'].data_ptr(), 2, _lib.ROUNDING_FUSED)
+    V = lambda t, w: _lib.View(t.data_ptr(), T * w, w)
+    R = lambda a, b: _lib.Rank1(None, None, 0, 0) if a is None else _lib.Rank1(a.data_ptr(), _lib.ptr(b), a.stride(0),
+                                                                               0 if b is None else b.stride(0))
+    r_o, r_fc, r_pj = R(c['ao'], None), R(c['afc'], c['bfc']), R(c['apj'], c['bpj'])
+    nxt = (_lib.Rank1 * 3)(*[_lib.Rank1(None, t.data_ptr(), 0, t.stride(0)) for t in c['nb']])
+    ndots = torch.full((rows, max(nnext, 1)), float('nan'), device=DEV)
+    xres = c['xres'].clone()
+    width = 1536 if split3 else 512
+    hout = torch.full((m, T, width), float('nan'), dtype=torch.bfloat16, device=DEV)
+    eps = c['eps']
+    mixargs = (1, c['lam'].data_ptr(), c['lam'].data_ptr() + 4, None if eps is None else eps[:, 0].data_ptr(),
+               None if eps is None else eps[:, 1].data_ptr(), 0 if eps is None else eps.stride(0)) if mix else \
+        (0, None, None, None, None, 0)
+    xout = xres if with_xout else None
+    perm = {}
+    for k in ('wfc', 'wpj'):
+        perm[k] = torch.empty_like(c[k])
+        if kernel == 'noise_pop_block':
+            _lib.call('noise_block_weight_layout', c[k].data_ptr(), perm[k].data_ptr(), c[k].shape[0], c[k].shape[1],
+                      stream)
+        else:
+            _lib.call('noise_mlp_proj_layout', c[k].data_ptr(), perm[k].data_ptr(), c[k].numel() // 2048, stream)
+    _lib.call(kernel, ctypes.byref(pop), V(c['y'], 512), c['wo'].data_ptr(), ctypes.byref(r_o),
+              _lib.ptr(c['odots']), 8, V(xres, 512), perm['wfc'].data_ptr(), ctypes.byref(r_fc),
+              perm['wpj'].data_ptr(), ctypes.byref(r_pj), _lib.ptr(xout), *mixargs, V(c['x0'], 512),
+              hout.data_ptr(), int(split3), nxt, nnext, ndots.data_ptr(), stream)
+    torch.cuda.synchronize()
+    return (None if xout is None else xout.cpu()), hout.float().cpu(), ndots[:, :nnext].cpu()
+
+
+def test_block_weight_layout():
+    """noise_block_weight_layout: within every 32 columns, position 8g + j holds column 4g + j (j < 4) or
+    16 + 4g + j - 4 (j >= 4)."""
+    from noise_amd import _lib
+    w = torch.arange(3 * 64, dtype=torch.float32).view(3, 64).bfloat16().to(DEV)
+    out = torch.empty_like(w)
+    _lib.call('noise_block_weight_layout', w.data_ptr(), out.data_ptr(), 3, 64, _lib.stream_ptr(DEV))
+    perm = [4 * (p // 8) + p % 8 if p % 8 < 4 else 16 + 4 * (p // 8) + p % 8 - 4 for p in range(32)]
+    idx = torch.tensor(perm + [32 + q for q in perm])
+    assert torch.equal(out.cpu(), w.cpu()[:, idx])
+
+
+@pytest.mark.parametrize('perturbed', [False, True], ids=['plain', 'perturbed'])
+@pytest.mark.parametrize('mix,nnext,split3,with_xout', [(True, 3, False, True), (True, 0, False, True),
+                                                        (False, 1, False, False), (False, 0, True, False)],
+                         ids=['mix-qkv-dots', 'mix-no-dots', 'last-head-dot', 'last-split3'])
+def test_block_matches_attn_mlp(perturbed, mix, nnext, split3, with_xout):
+    """noise_pop_block against noise_pop_attn_mlp (itself checked against the residual writer + fused MLP pair):
+    the same arithmetic with fp32 sums in a different order, so h and the hidden layer can round one bf16 ulp
+    apart; outputs agree to 2e-3 of their scale. Also bit-stable across two calls."""
+    c = _attn_case(4, 256, 3, perturbed)
+    print(f'block: 4 members x 256 tokens, perturbed {perturbed}, mix {mix}, nnext {nnext}, split3 {split3}', flush=True)
+    xo_b, ho_b, nd_b = _run_block(c, mix, nnext, split3, with_xout, 'noise_pop_block')
+    xo_r, ho_r, nd_r = _run_block(c, mix, nnext, split3, with_xout, 'noise_pop_attn_mlp')
+    assert torch.isfinite(ho_b).all() and torch.isfinite(nd_b).all()
+    if with_xout:
+        assert (xo_b - xo_r).abs().max() <= 2e-3 * xo_r.abs().max()
+    hscale = ho_r[..., :512].abs().max()
+    assert (ho_b[..., :512] - ho_r[..., :512]).abs().max() <= (2.0 ** -7 + 2e-3) * hscale
+    if split3:
+        assert torch.equal(ho_b[..., 1024:], ho_b[..., :512])
+        assert (ho_b[..., :512] + ho_b[..., 512:1024] - ho_r[..., :512] - ho_r[..., 512:1024]).abs().max() <= 2e-3 * hscale
+    if nnext:
+        assert (nd_b - nd_r).abs().max() <= 2e-3 * nd_r.abs().max()
+    again = _run_block(c, mix, nnext, split3, with_xout, 'noise_pop_block')
+    assert torch.equal(again[1], ho_b) and torch.equal(again[2], nd_b)
