@@ -61,4 +61,11 @@ int dust_block_run(const float *x, float *x_out, int64_t sequences, int64_t toke
                    const void *jit_attn, const void *jit_fc, const void *jit_mlp, void *workspace,
                    int64_t workspace_bytes, noise_stream_t stream, const char *fn);
 
+// noise_pop_qkv's fused-rounding path with two waves per SIMD (qkv.hip): arguments validated by the caller,
+// tokens a multiple of 128, outputs 16 B aligned, one value table for every member.
+int qkv_rows_launch(const noise_population_t *pop, noise_view_t x, const void *const w[3], const noise_rank1_t r1[3],
+                    const float *dots, const void *rope_cos, const void *rope_sin, const float *ve, int64_t vocab,
+                    const int64_t *idx, int64_t idx_sm, const float *gates, const noise_rank1_t *ve_noise,
+                    void *const out[3], noise_stream_t stream);
+
 }  // namespace noise

@@ -1115,6 +1115,9 @@ extern "C" int noise_pop_qkv(const noise_population_t *pop, noise_view_t x, cons
     a.ve_r1 = make_r1(ve ? ve_noise : nullptr);
     NOISE_CHECK_ARG(!a.ve_r1.a || (pop->sign && aligned(a.ve_r1.b, 16) && a.ve_r1.b_stride % 4 == 0),
                     "%s: value-embedding noise b rows must be 16 B aligned", fn);
+    if (!eager(pop) && aligned(out[0], 16) && aligned(out[1], 16) && aligned(out[2], 16))
+        return qkv_rows_launch(pop, x, w, r1, dots, rope_cos, rope_sin, ve, vocab, idx, idx_sm, gates, ve_noise, out,
+                               stream);
     dim3 grid((unsigned)(6 * pop->members * (pop->tokens / 256)));
     if (eager(pop))
         hipLaunchKernelGGL(qkv_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
