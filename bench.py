@@ -61,7 +61,7 @@ def kernel_flops_per_launch(name, label, members, T):
 
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'population_forward_1024x2048.md')
 # entry point (bench label) -> the kernel name in the committed trace of the default workload
-ROCPROF_NAME = {'noise_pop_qkv': 'qkv_kernel<false>', 'noise_pop_head_ce': 'head_x_kernel<false, false>',
+ROCPROF_NAME = {'noise_pop_qkv': 'qkv16_kernel<false>', 'noise_pop_head_ce': 'head_x_kernel<false, false>',
                 'noise_pop_block[block]': 'block_kernel<true, 3, false>'}
 
 

@@ -15,8 +15,9 @@
 //   - weights stream through LDS by direct global -> LDS copies of whole rows segments, double buffered:
 //     W_o in 8 steps of 64 columns ([512 rows][128 B]), then 64 hidden steps of 32 units, each holding those
 //     units' c_fc rows ([8 k tiles][32 rows][128 B]) and mlp.c_proj columns ([512 rows][64 B]); the 16 B chunks
-//     of a row are XOR-swizzled by row so that a fragment read (16 rows, 4 consecutive chunks) hits every
-//     bank once;
+//     of a row are XOR-swizzled by row so that a fragment read (16 rows, 4 consecutive chunks) is free of bank
+//     conflicts: gfx950 serves a wave's ds_read_b128 in four passes of 16 lanes (lanes with equal bit 5 and
+//     equal parity of bits 2..4, found with the LDS bank-conflict counter), each pass covering the 64 banks;
 //   - the 16 x 16 D layout (lane l: token l % 16, rows 4 (l / 16) .. + 4) of two consecutive row blocks is the
 //     B operand of one 32-deep k block once the k index is permuted within each 32 (lane group g holds rows
 //     4g .. 4g + 3 and 16 + 4g .. 16 + 4g + 3): h goes from the x_mid accumulators into the first product's
@@ -116,10 +117,10 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         vcopy(p.afc ? p.bfc + dir * p.bfc_stride : nullptr, kVBfc, kModel);
     }
 
-    // LDS byte offset of 16 B chunk c of row r: in 128 B rows (chunks swizzled by row pair) and in 64 B rows
-    // (swizzled by row quad); either way the 16 rows x 4 chunks of a fragment read cover all banks once
+    // LDS byte offset of 16 B chunk c of row r: in 128 B rows and in 64 B rows, chunks swizzled by row pair;
+    // either way each 16-lane pass of a fragment read (rows r with 4 consecutive chunks) covers all banks once
     auto off128 = [](int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); };
-    auto off64 = [](int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); };
+    auto off64 = [](int r, int c) { return r * 64 + ((c ^ ((r >> 1) & 3)) << 4); };
     // copies of whole 128 B row segments (8 rows per wave-wide copy) and of 64 B ones (16 rows)
     const int r8 = lane >> 3, p8 = lane & 7, r16 = lane >> 2, p16 = lane & 3;
     auto copy128 = [&](const __bf16 *rows, int64_t ld, int r0, unsigned dst) {  // rows r0 .. r0 + 7
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         lds_dma16_at(rows + (int64_t)r0 * ld, (unsigned)(r8 * ld * 2 + c * 16), dst + r0 * 128);
     };
     auto copy64 = [&](const __bf16 *rows, int64_t ld, int r0, unsigned dst) {  // rows r0 .. r0 + 15
-        const int c = p16 ^ (((r0 + r16) >> 2) & 3);
+        const int c = p16 ^ (((r0 + r16) >> 1) & 3);
         lds_dma16_at(rows + (int64_t)r0 * ld, (unsigned)(r16 * ld * 2 + c * 16), dst + r0 * 64);
     };
     auto issue_o = [&](int s) {  // W_o columns 64 s .. + 64: [512 rows][128 B], 64 copies, 8 per wave
