@@ -40,6 +40,15 @@ constexpr int kBlkTok = 128;       // tokens per workgroup (16 per wave)
 constexpr int kHidden = 2048, kModel = 512;
 constexpr int kUnits = 32;         // hidden units per step
 constexpr int kSteps = kHidden / kUnits;
+// fragment reads in flight ahead of the product that uses them; each product ends a scheduling region so that
+// the compiler keeps them that far ahead (left to itself it moves each read next to its product)
+#ifndef BLOCK_AHEAD
+#define BLOCK_AHEAD 4
+#endif
+constexpr int kAhead = BLOCK_AHEAD;
+#ifndef BLOCK_PIN
+#define BLOCK_PIN() __builtin_amdgcn_sched_barrier(0)
+#endif
 constexpr int kBuf = 65536;        // a W_o step ([512 rows][128 B]); two per LDS
 constexpr int kStage = 32768;      // an MLP stage (a step's c_fc rows or its mlp.c_proj columns); four per LDS
 constexpr int kVec = 2 * kBuf;     // fp32 vectors after the two step buffers:
@@ -186,12 +195,14 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         const char *buf = lds + (s & 1) * kBuf;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            bf16x8 a[2];
-            a[0] = frag_o(buf, 0, h);
+            bf16x8 a[kAhead + 1];
+#pragma unroll
+            for (int i = 0; i < kAhead; ++i) a[i] = frag_o(buf, i, h);
 #pragma unroll
             for (int ob = 0; ob < 32; ++ob) {
-                if (ob + 1 < 32) a[(ob + 1) & 1] = frag_o(buf, ob + 1, h);
-                out[ob] = mfma16x16x32(a[ob & 1], xf[2 * s + h], out[ob]);
+                if (ob + kAhead < 32) a[(ob + kAhead) % (kAhead + 1)] = frag_o(buf, ob + kAhead, h);
+                out[ob] = mfma16x16x32(a[ob % (kAhead + 1)], xf[2 * s + h], out[ob]);
+                BLOCK_PIN();
             }
         }
         vm_wait<0>();
@@ -274,12 +285,14 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         // first product: hacc[hb] = c_fc rows 32 js + 16 hb .. + 16 against the 16 k blocks of h
         f32x4 hacc[2] = {f32x4{}, f32x4{}};
         {
-            bf16x8 a[2];
-            a[0] = frag_fc(buf, 0, 0);
+            bf16x8 a[kAhead + 1];
+#pragma unroll
+            for (int i = 0; i < kAhead; ++i) a[i] = frag_fc(buf, i & 1, i >> 1);
 #pragma unroll
             for (int f = 0; f < 32; ++f) {
-                if (f + 1 < 32) a[(f + 1) & 1] = frag_fc(buf, (f + 1) & 1, (f + 1) >> 1);
-                hacc[f & 1] = mfma16x16x32(a[f & 1], xf[f >> 1], hacc[f & 1]);
+                if (f + kAhead < 32) a[(f + kAhead) % (kAhead + 1)] = frag_fc(buf, (f + kAhead) & 1, (f + kAhead) >> 1);
+                hacc[f & 1] = mfma16x16x32(a[f % (kAhead + 1)], xf[f >> 1], hacc[f & 1]);
+                BLOCK_PIN();
             }
         }
         stage_end(2 * js);
@@ -310,12 +323,14 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         }
         // second product: out[ob] += mlp.c_proj rows 16 ob .. + 16, columns of this step
         {
-            bf16x8 a[2];
-            a[0] = frag_pj(buf, 0);
+            bf16x8 a[kAhead + 1];
+#pragma unroll
+            for (int i = 0; i < kAhead; ++i) a[i] = frag_pj(buf, i);
 #pragma unroll
             for (int ob = 0; ob < 32; ++ob) {
-                if (ob + 1 < 32) a[(ob + 1) & 1] = frag_pj(buf, ob + 1);
-                out[ob] = mfma16x16x32(a[ob & 1], hb, out[ob]);
+                if (ob + kAhead < 32) a[(ob + kAhead) % (kAhead + 1)] = frag_pj(buf, ob + kAhead);
+                out[ob] = mfma16x16x32(a[ob % (kAhead + 1)], hb, out[ob]);
+                BLOCK_PIN();
             }
         }
         stage_end(2 * js + 1);

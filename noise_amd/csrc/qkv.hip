@@ -27,6 +27,15 @@ constexpr int kQVt = 4 * kQStage;       // V^T staging [64 dims][128 tokens] bf1
 constexpr int kQQk = kQVt + 16384;      // Q / K staging per wave [16 tokens][128 B] (2 KiB)
 constexpr int kQLds = kQQk + 8 * 2048;  // 160 KiB
 static_assert(kQLds <= 160 * 1024, "LDS of one CU");
+// fragment reads in flight ahead of the product that uses them; each product ends a scheduling region so that
+// the compiler keeps them that far ahead
+#ifndef QKV_AHEAD
+#define QKV_AHEAD 4
+#endif
+constexpr int kQAhead = QKV_AHEAD;
+#ifndef QKV_PIN
+#define QKV_PIN() __builtin_amdgcn_sched_barrier(0)
+#endif
 
 struct QkvRowsArgs {
     int members, tokens, dir_div;
@@ -187,12 +196,14 @@ __global__ __launch_bounds__(kQThreads, 1) void qkv16_kernel(QkvRowsArgs p) {
                 acc[0] = f32x4{}; acc[1] = f32x4{}; acc[2] = f32x4{}; acc[3] = f32x4{};
             }
             {
-                bf16x8 a[2];
-                a[0] = frag(buf, 0, 0);
+                bf16x8 a[kQAhead + 1];
+#pragma unroll
+                for (int i = 0; i < kQAhead; ++i) a[i] = frag(buf, i & 1, i >> 1);
 #pragma unroll
                 for (int f = 0; f < 32; ++f) {
-                    if (f + 1 < 32) a[(f + 1) & 1] = frag(buf, (f + 1) & 1, (f + 1) >> 1);
-                    acc[2 * h + (f & 1)] = mfma16x16x32(a[f & 1], xf[f >> 1], acc[2 * h + (f & 1)]);
+                    if (f + kQAhead < 32) a[(f + kQAhead) % (kQAhead + 1)] = frag(buf, (f + kQAhead) & 1, (f + kQAhead) >> 1);
+                    acc[2 * h + (f & 1)] = mfma16x16x32(a[f % (kQAhead + 1)], xf[f >> 1], acc[2 * h + (f & 1)]);
+                    QKV_PIN();
                 }
             }
             if (h == 1) {
