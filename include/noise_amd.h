@@ -307,11 +307,13 @@ int noise_lowrank_embed(float *out, const float *w, int64_t vocab, int64_t width
                         const noise_population_t *pop, const noise_rank1_t *r1, noise_stream_t stream);
 
 /* Rank-1 expansion of a product shared by all members (eggroll.py:58 with x broadcast over members):
- * y[m, t, n] = base[t, n] + sign[m] * dots[m*T + t] * a[m/dir_div, n], y bf16 (y_fp32 = 0) or fp32 (1;
- * 2: the dot rounded to bf16 first, autocast's form) [m][T][width], base fp32 [T][width]. An HBM-write
- * stream: the shared x W^T is computed once (noise_pop_linear). */
+ * y[m, t, n] = base[t, n] + sign[m] * dots[t * dots_stride + m/dir_div] * a[m/dir_div, n], y bf16
+ * (y_fp32 = 0) or fp32 (1; 2: the dot rounded to bf16 first, autocast's form) [m][T][width], base fp32
+ * [T][width], width a multiple of 4. With x shared the dot x[t] . b depends on the direction only: dots
+ * [T][dots_stride >= directions]. An HBM-write stream: the shared x W^T and x B^T are computed once
+ * (noise_pop_linear). */
 int noise_rank1_expand(const noise_population_t *pop, const float *base, int64_t width, const float *dots,
-                       const noise_rank1_t *r1, void *y, int y_fp32, noise_stream_t stream);
+                       int64_t dots_stride, const noise_rank1_t *r1, void *y, int y_fp32, noise_stream_t stream);
 
 /* lowrank (eggroll.py:56-58) for any shape, in autocast's form: y[m, t, o] = bf16(x[m, t, :] . w[o, :]) +
  * sign[m] * bf16(x[m, t, :] . bf16(b[m/dir_div, :])) * a[m/dir_div, o], fp32 accumulation, y fp32

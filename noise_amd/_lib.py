@@ -45,7 +45,7 @@ SIGNATURES = {
     'noise_member_mean': [_p, _i64, _i64, _p, _p],
     'noise_split3': [_p, _i64, _i64, _i32, _i32, _p, _p],
     'noise_lowrank_embed': [_p, _p, _i64, _i64, _p, _p, _p, _p],
-    'noise_rank1_expand': [_p, _p, _i64, _p, _p, _p, _i32, _p],
+    'noise_rank1_expand': [_p, _p, _i64, _p, _i64, _p, _p, _i32, _p],
     'noise_lowrank_rows': [_p, 'View', _i64, _p, _i64, _p, _p, _p],
     'noise_coordinate_differences': [_p, _i32, _i64, _i64, _i64, _p, _f32, _p, _i64, _i64, _p],
     'noise_draw_errors': [_p, _p, _i64, _i64, _i64, _f32, _p, _p],

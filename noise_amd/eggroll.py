@@ -458,21 +458,31 @@ def lowrank_eager(x, weight, a, b, sign, dir_div=1):
         return y
     if xb.stride(-1) != 1 or xb.stride(1) % 8 or xb.data_ptr() % 16 or (not shared and xb.stride(0) % 8):
         xb = xb.contiguous()
-    xs_m = 0 if shared else xb.stride(0)
-    dots = torch.empty(m * T, dtype=F32, device=dev)
-    _lib.call('noise_member_dots', ctypes.byref(pop), _lib.View(xb.data_ptr(), xs_m, xb.stride(1)), n_in,
-              ctypes.byref(r1), 1, dots.data_ptr(), stream)
     if shared:
-        base = torch.empty(1, T, n_out, dtype=F32, device=dev)
+        # x is the same for every member, so x W^T and the dots x . b (one per direction) are computed once,
+        # as two products over the shared rows (the b rows as a bf16 weight, padded to the 256-row tile); the
+        # members' outputs are then a rank-1 expansion
+        xv = _lib.View(xb.data_ptr(), 0, xb.stride(1))
         one = _pop(1, T, None, 1)
-        _lib.call('noise_pop_linear', ctypes.byref(one), _lib.View(xb.data_ptr(), 0, xb.stride(1)), w.data_ptr(),
-                  n_in, n_out, None, None, base.data_ptr(), _lib.LINEAR_AUTOCAST, T * n_out, n_out, stream)
-        _lib.call('noise_rank1_expand', ctypes.byref(pop), base.data_ptr(), n_out, dots.data_ptr(), ctypes.byref(r1),
-                  y.data_ptr(), _lib.LINEAR_AUTOCAST, stream)
-    else:
-        _lib.call('noise_pop_linear', ctypes.byref(pop), _lib.View(xb.data_ptr(), xs_m, xb.stride(1)), w.data_ptr(),
-                  n_in, n_out, ctypes.byref(r1), dots.data_ptr(), y.data_ptr(), _lib.LINEAR_AUTOCAST, T * n_out,
-                  n_out, stream)
+        base = torch.empty(1, T, n_out, dtype=F32, device=dev)
+        _lib.call('noise_pop_linear', ctypes.byref(one), xv, w.data_ptr(), n_in, n_out, None, None, base.data_ptr(),
+                  _lib.LINEAR_AUTOCAST, T * n_out, n_out, stream)
+        dirs = -(-m // dir_div)
+        dpad = -(-dirs // 256) * 256
+        bw = torch.zeros(dpad, n_in, dtype=BF16, device=dev)
+        bw[:dirs] = b[:dirs]  # b holds bf16 values already: exact
+        dots = torch.empty(T, dpad, dtype=F32, device=dev)
+        _lib.call('noise_pop_linear', ctypes.byref(one), xv, bw.data_ptr(), n_in, dpad, None, None, dots.data_ptr(),
+                  _lib.LINEAR_AUTOCAST, T * dpad, dpad, stream)
+        _lib.call('noise_rank1_expand', ctypes.byref(pop), base.data_ptr(), n_out, dots.data_ptr(), dpad,
+                  ctypes.byref(r1), y.data_ptr(), _lib.LINEAR_AUTOCAST, stream)
+        return y
+    dots = torch.empty(m * T, dtype=F32, device=dev)
+    _lib.call('noise_member_dots', ctypes.byref(pop), _lib.View(xb.data_ptr(), xb.stride(0), xb.stride(1)), n_in,
+              ctypes.byref(r1), 1, dots.data_ptr(), stream)
+    _lib.call('noise_pop_linear', ctypes.byref(pop), _lib.View(xb.data_ptr(), xb.stride(0), xb.stride(1)), w.data_ptr(),
+              n_in, n_out, ctypes.byref(r1), dots.data_ptr(), y.data_ptr(), _lib.LINEAR_AUTOCAST, T * n_out,
+              n_out, stream)
     return y
 
 

@@ -41,6 +41,39 @@ def test_lowrank_vs_oracle(shared):
     assert (d - rank1).abs().max() <= 2e-2 * rank1.abs().max()
 
 
+@pytest.mark.parametrize('dir_div,y_fp32,T,width', [(1, 1, 10, 1028), (3, 0, 7, 2048), (2, 2, 9, 4), (2, 0, 12, 1040)])
+def test_rank1_expand_generic(dir_div, y_fp32, T, width):
+    """noise_rank1_expand against the formula on shapes off the population's: directions of 1 or 3 members
+    (and a last direction with fewer), token counts that end inside a 4-row tile, widths that end inside a
+    1024-column tile, bf16 output and the dot rounded to bf16 (y_fp32 = 2). fp32: exact up to the fma
+    contraction (1e-6 relative); bf16: one bf16 ulp."""
+    import ctypes
+    from noise_amd import _lib
+    g = torch.Generator().manual_seed(11)
+    m = 7
+    dirs = -(-m // dir_div)
+    base = torch.randn(T, width, generator=g)
+    a = torch.randn(dirs, width, generator=g)
+    dots = torch.randn(T, dirs + 3, generator=g)  # row stride larger than the directions
+    sign = torch.randn(m, generator=g)
+    bd, ad, dd, sd = (t.to(DEV).contiguous() for t in (base, a, dots, sign))
+    y = torch.empty(m, T, width, dtype=torch.float32 if y_fp32 else torch.bfloat16, device=DEV)
+    pop = _lib.Population(m, T, sd.data_ptr(), dir_div)
+    r1 = _lib.Rank1(ad.data_ptr(), None, width, 0)
+    _lib.call('noise_rank1_expand', ctypes.byref(pop), bd.data_ptr(), width, dd.data_ptr(), dirs + 3,
+              ctypes.byref(r1), y.data_ptr(), y_fp32, _lib.stream_ptr(DEV))
+    dir_of = torch.arange(m) // dir_div
+    dv = dots[:, dir_of].t()                       # [m, T]
+    if y_fp32 == 2:
+        dv = dv.bfloat16().float()
+    ref = base[None] + (sign[:, None] * dv)[:, :, None] * a[dir_of][:, None, :]
+    out = y.float().cpu()
+    if y_fp32:
+        assert torch.allclose(out, ref, rtol=1e-6, atol=1e-6)
+    else:
+        assert torch.equal(out, ref.bfloat16().float()) or (out - ref).abs().max() <= ref.abs().max() * 2.0 ** -8
+
+
 def test_lowrank_embed_exact():
     from noise_amd.eggroll import lowrank_embed
     g = torch.Generator().manual_seed(1)
