@@ -1007,6 +1007,141 @@ __global__ __launch_bounds__(kHxThreads, 1) void head_x_kernel(HeadArgs p) {
     }
 }
 
+// The fp32 head as split-bf16x3 (K = 1536: x rows [hi | lo | hi], w rows [hi | hi | lo]), logits = x_hi w_hi +
+// x_lo w_hi + x_hi w_lo, with each token row read once: a workgroup owns 128 tokens of one member in 8 waves
+// (two per SIMD) of 16; wave w keeps its tokens' hi and lo rows (x's first two segments; the third repeats hi
+// and is not read) in registers as the B operands of v_mfma_f32_16x16x32_bf16 (128 registers) and the weights'
+// hi and lo segments stream through LDS in steps of 32 vocabulary rows (2 x 32 KiB, double buffered; wave w
+// copies k-tile w of both). Per step and k block a wave reads the two weight fragments once for its three
+// products. The soft-capped log-sum-exp and the target pick are those of head_x_kernel; a token's rows sit in
+// the four lanes l % 16 + 16 g, which are summed at the end.
+constexpr int kH3Threads = 512, kH3Tok = 128, kH3Rows = 32;
+constexpr int kH3Part = kH3Rows * 512 * 2;    // one segment's rows of a step: [8 k-tiles][32 rows][128 B]
+constexpr int kH3Step = 2 * kH3Part;          // hi then lo
+#ifndef HEAD3_AHEAD
+#define HEAD3_AHEAD 4
+#endif
+
+template <bool PERT>
+__global__ __launch_bounds__(kH3Threads, 1) void head3_kernel(HeadArgs p) {
+    __shared__ __attribute__((aligned(16))) char lds[2 * kH3Step];
+    const int T = p.pop.tokens, tiles_t = T / kH3Tok;
+    const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * kH3Tok;
+    const int tid = threadIdx.x, lane = tid & 63, tl = lane & 15, g = lane >> 4;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tok = t0 + 16 * wave + tl;
+    const int64_t row = (int64_t)m * T + tok;
+    const int dir = m / p.pop.dir_div;
+    const unsigned lbase = lds_addr(lds);
+    // copies of step js: wave w copies k-tile w (columns 64 w .. + 64) of the step's 32 rows of both segments,
+    // 4 copies of 8 rows each; chunk c of row r lands at position c ^ ((r >> 1) & 7) of the row's 128 B
+    const int r8 = lane >> 3, p8 = lane & 7;
+    auto issue = [&](int js) {
+        const unsigned dst = lbase + (js & 1) * kH3Step + wave * 4096;
+#pragma unroll
+        for (int part = 0; part < 2; ++part)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r0 = 8 * i;
+                const int c = p8 ^ (((r0 + r8) >> 1) & 7);
+                lds_dma16_at(p.w + (int64_t)(kH3Rows * js + r0) * 1536 + 1024 * part + 64 * wave,
+                             (unsigned)(r8 * 1536 * 2 + c * 16), dst + part * kH3Part + r0 * 128);
+            }
+    };
+    issue(0);
+    // this lane's rows: xh[kb] = x_hi[tok][32 kb + 8 g .. + 8], xl[kb] the same of x_lo
+    bf16x8 xh[16], xl[16];
+    {
+        const __bf16 *xr = p.x + m * p.xs_m + (int64_t)tok * p.xs_t + 8 * g;
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb) {
+            xh[kb] = load_bf16x8(xr + 32 * kb);
+            xl[kb] = load_bf16x8(xr + 512 + 32 * kb);
+        }
+    }
+    const int64_t tgt = p.targets[m * p.targets_sm + tok];
+    const float corr = PERT ? p.pop.sign[m] * p.dots[row] : 0.f;
+    const float *arow = PERT ? p.r1.a + dir * p.r1.a_stride + 4 * g : nullptr;
+    const float k1 = (2.0f / 15.0f) * kLog2e;     // u = 2^(k1 l) = e^(2 l / 15)
+    const float c2 = 1.0f / (-30.0f * kLog2e);    // rcp(c2 (1 + u)) = -30 log2(e) / (1 + u) = log2 e^(z - 15)
+    float sum = 0.f, zl = 0.f;                    // sum of e^(z - 15) over this lane's rows; the target's logit
+    vm_wait<0>();
+    __syncthreads();
+    const int nsteps = p.vocab / kH3Rows;
+    const int fr = lane & 15, fc = lane >> 4;
+    constexpr int kA = HEAD3_AHEAD;
+#pragma unroll 1
+    for (int js = 0; js < nsteps; ++js) {
+        if (js + 1 < nsteps) issue(js + 1);  // its buffer was last read in step js - 1, before the barrier below
+        const char *buf = lds + (js & 1) * kH3Step;
+        // fragment f = 4 kb + 2 vb + part: rows 16 vb .. + 16 of segment part, k block kb
+        auto frag = [&](int f) {
+            const int kb = f >> 2, vb = (f >> 1) & 1, part = f & 1;
+            const int r = 16 * vb + fr, c = 4 * (kb & 1) + fc;
+            return *reinterpret_cast<const bf16x8 *>(buf + part * kH3Part + (kb >> 1) * 4096 + r * 128 +
+                                                     ((c ^ ((r >> 1) & 7)) << 4));
+        };
+        f32x4 acc[2] = {f32x4{}, f32x4{}};
+        bf16x8 a[kA + 2];
+#pragma unroll
+        for (int i = 0; i < kA; ++i) a[i] = frag(i);
+#pragma unroll
+        for (int f = 0; f < 64; f += 2) {
+            // the two fragments of (kb, vb) are f and f + 1; the reads run kA fragments ahead
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                if (f + kA + i < 64) a[(f + kA + i) % (kA + 2)] = frag(f + kA + i);
+            const int kb = f >> 2, vb = (f >> 1) & 1;
+            const bf16x8 ah = a[f % (kA + 2)], al = a[(f + 1) % (kA + 2)];
+            acc[vb] = mfma16x16x32(ah, xh[kb], acc[vb]);
+            acc[vb] = mfma16x16x32(ah, xl[kb], acc[vb]);
+            acc[vb] = mfma16x16x32(al, xh[kb], acc[vb]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // register r of block vb holds vocabulary row v0 + 16 vb + 4 g + r
+        const int v0 = kH3Rows * js;
+        float4 a4[2] = {float4{0.f, 0.f, 0.f, 0.f}, float4{0.f, 0.f, 0.f, 0.f}};
+        if constexpr (PERT) {
+            a4[0] = ld4(arow + v0);
+            a4[1] = ld4(arow + v0 + 16);
+        }
+        auto logit = [&](int vb, int r) {
+            float x = acc[vb][r];
+            if constexpr (PERT) x = __builtin_fmaf(corr, f4get(a4[vb], r), x);
+            return x;
+        };
+#pragma unroll
+        for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float u = exp2_fast(logit(vb, r) * k1);
+                sum += exp2_fast(__builtin_amdgcn_rcpf(__builtin_fmaf(u, c2, c2)));
+            }
+        // the target's logit, in the steps whose rows hold some lane's target (-1 and out-of-range ids never do)
+        const bool here = (uint64_t)(tgt - v0) < (uint64_t)kH3Rows;
+        if (__builtin_amdgcn_ballot_w64(here)) {
+            const int d = here ? (int)(tgt - v0) - 4 * g : -1;
+#pragma unroll
+            for (int vb = 0; vb < 2; ++vb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (d == 16 * vb + r) zl = logit(vb, r);
+        }
+        vm_wait<0>();
+        __syncthreads();  // step js + 1 landed for every wave; every wave is done with buffer js & 1
+    }
+    // the four lanes of a token: sums add; exactly one of them holds the target's row (the others hold 0)
+    sum += __shfl_xor(sum, 16, 64);
+    sum += __shfl_xor(sum, 32, 64);
+    zl += __shfl_xor(zl, 16, 64);
+    zl += __shfl_xor(zl, 32, 64);
+    if (g == 0) {
+        const float z = 15.0f - 30.0f / (exp2_fast(zl * k1) + 1.0f);
+        const float ce = 15.0f + __logf(sum) - z;
+        p.loss[row] = tgt == -1 ? 0.f : (tgt < 0 || tgt >= p.vocab ? __builtin_nanf("") : ce);
+    }
+}
+
 Pop make_pop(const noise_population_t *pp) {
     Pop p;
     p.members = (int)pp->members;
@@ -1289,6 +1424,13 @@ extern "C" int noise_pop_head_ce(const noise_population_t *pop, noise_view_t x, 
             hipLaunchKernelGGL((head_x_kernel<false, true>), grid, dim3(kHxThreads), 0, (hipStream_t)stream, a);
         else
             hipLaunchKernelGGL((head_x_kernel<false, false>), grid, dim3(kHxThreads), 0, (hipStream_t)stream, a);
+    } else if (K == 1536 && !eager(pop) && vocab % kH3Rows == 0 && x.st % 8 == 0 && x.sm % 8 == 0) {
+        // the split-bf16x3 fp32 head: hi and lo token rows resident in registers, weights streamed once per 128 tokens
+        const dim3 g3((unsigned)(pop->members * (pop->tokens / kH3Tok)));
+        if (a.r1.a)
+            hipLaunchKernelGGL(head3_kernel<true>, g3, dim3(kH3Threads), 0, (hipStream_t)stream, a);
+        else
+            hipLaunchKernelGGL(head3_kernel<false>, g3, dim3(kH3Threads), 0, (hipStream_t)stream, a);
     } else if (eager(pop)) {
         hipLaunchKernelGGL(head_ce_kernel<true>, grid, dim3(kThreads), 0, (hipStream_t)stream, a);
     } else {

@@ -98,3 +98,53 @@ def test_bf16_head_eager_rounding():
     assert (diff <= 5e-5).float().mean().item() >= 0.99
     assert diff.max().item() <= 0.1
     assert (got - ref).nan_to_num().mean(-1).abs().max().item() <= 1e-4
+
+
+def _split(v):
+    hi = v.bfloat16()
+    return hi, (v - hi.float()).bfloat16()
+
+
+@pytest.mark.parametrize('perturbed', [False, True], ids=['plain', 'perturbed'])
+def test_split3_head_matches_fp64_reference(perturbed):
+    """K = 1536, the split-bf16x3 fp32 head: x rows [hi | lo | hi], w rows [hi | hi | lo] (noise_split3's layouts).
+    Against the same three products summed in float64 on the CPU: per-token losses within 5e-5 (fp32
+    accumulation in the kernel's own order); against the unsplit fp32 logits within 2e-4 (the split's own error,
+    ~2^-16 relative per product). The third x segment repeats hi and is not read: it holds NaN here."""
+    g = torch.Generator().manual_seed(23)
+    m, T, V = 4, 256, 4096
+    x = torch.randn(m, T, 512, generator=g)
+    w = torch.randn(V, 512, generator=g) * 0.4
+    targets = torch.randint(0, V, (T,), generator=g)
+    targets[5], targets[77], targets[130] = -1, V - 1, V + 3
+    xh, xl = _split(x)
+    wh, wl = _split(w)
+    x3 = torch.cat([xh, xl, torch.full_like(xh, float('nan'))], -1)
+    w3 = torch.cat([wh, wh, wl], -1)
+    logits = (xh.double() @ wh.double().t() + xl.double() @ wh.double().t() + xh.double() @ wl.double().t())
+    exact = x.double() @ w.double().t()
+    kw = {}
+    if perturbed:
+        a = torch.randn(2, V, generator=g)
+        b = torch.randn(2, 512, generator=g)
+        sign = torch.tensor([0.05, -0.05, 0.05, -0.05])
+        dots = (x @ b.repeat_interleave(2, 0)[:, :, None])[..., 0].reshape(-1)
+        r1 = (sign[:, None] * dots.view(m, -1))[..., None].double() * a.repeat_interleave(2, 0)[:, None, :].double()
+        logits, exact = logits + r1, exact + r1
+        kw = dict(sign=sign, dots=dots, a=a, b=b)
+    print(f'head K=1536 (split-bf16x3): {m} members x {T} tokens, perturbed {perturbed}', flush=True)
+    got = _run(x3, w3, targets, **kw)
+
+    def ce(lg):
+        z = 15 * torch.tanh(lg / 15)
+        t = targets.clamp(0, V - 1)
+        out = torch.logsumexp(z, -1) - z.gather(-1, t.expand(m, -1)[..., None])[..., 0]
+        out = torch.where(targets == -1, torch.zeros_like(out), out)
+        return torch.where((targets < -1) | (targets >= V), torch.full_like(out, float('nan')), out).float()
+
+    ref, ref_exact = ce(logits), ce(exact)
+    assert torch.equal(torch.isnan(got), torch.isnan(ref))
+    ok = ~torch.isnan(ref)
+    assert (got[ok] - ref[ok]).abs().max().item() <= 5e-5
+    assert (got[ok] - ref_exact[ok]).abs().max().item() <= 2e-4
+    assert (got[:, 5] == 0).all()
