@@ -35,9 +35,15 @@ def hipcc():
 EXTRA = {'mlp.hip': ['-mllvm', '-amdgpu-sched-strategy=max-ilp']}
 
 
-def _compile(src: Path) -> Path:
-    obj = OBJ / (src.stem + '.o')
-    cmd = [hipcc(), *HIPFLAGS, *EXTRA.get(src.name, []), '-c', str(src), '-o', str(obj)]
+# host-side AddressSanitizer + UndefinedBehaviorSanitizer for the C-ABI layer (argument checks, error messages,
+# struct handling); the device code is built as usual (GPU sanitizers are not used)
+SANITIZE = ['-Xarch_host', '-fsanitize=address', '-Xarch_host', '-fsanitize=undefined',
+            '-Xarch_host', '-fno-omit-frame-pointer', '-Xarch_host', '-fno-sanitize-recover=all']
+
+
+def _compile(src: Path, obj_dir: Path = OBJ, extra=()) -> Path:
+    obj = obj_dir / (src.stem + '.o')
+    cmd = [hipcc(), *HIPFLAGS, *EXTRA.get(src.name, []), *extra, '-c', str(src), '-o', str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f'hipcc failed on {src.name}:\n{res.stderr[-8000:]}')
@@ -60,6 +66,33 @@ def build(verbose: bool = False) -> Path:
     if verbose:
         print(f'built {OUT} from {len(sources)} sources', file=sys.stderr)
     return OUT
+
+
+def build_sanitized(out_dir: Path) -> Path:
+    """The library with the host code under ASan + UBSan, into out_dir (for tests that drive the C ABI's host
+    layer on the CPU; load it with the sanitizer runtime preloaded: sanitizer_runtime())."""
+    out_dir = Path(out_dir)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    sources = sorted(CSRC.glob('*.hip'))
+    workers = min(len(sources), int(os.environ.get('MAX_JOBS', '8')), 8)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=max(1, workers)) as pool:
+        objs = list(pool.map(lambda src: _compile(src, out_dir, SANITIZE), sources))
+    out = out_dir / 'libnoise_amd_sanitized.so'
+    cmd = [hipcc(), f'--offload-arch={ARCH}', '-shared', '-fPIC', *SANITIZE, '-o', str(out), *map(str, objs)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f'link failed:\n{res.stderr[-8000:]}')
+    return out
+
+
+def sanitizer_runtime() -> Path:
+    """The shared ASan runtime of the HIP toolchain's clang (to LD_PRELOAD into a host process)."""
+    exe = Path(hipcc()).resolve()
+    for root in (exe.parents[1] / 'llvm', exe.parents[1] / 'lib' / 'llvm', exe.parents[1]):
+        hits = sorted(root.glob('lib/clang/*/lib/linux/libclang_rt.asan-x86_64.so'))
+        if hits:
+            return hits[-1]
+    raise RuntimeError('libclang_rt.asan-x86_64.so not found next to hipcc')
 
 
 if __name__ == '__main__':

@@ -509,6 +509,23 @@ def lowrank_embed_eager(weight, a, b, idx, sign, dir_div=1):
     return out
 
 
+def member_plan(pairs, sequences, rank=0, world=1, chunk=512):
+    """The member bookkeeping of eggroll.py:133-146 for one rank: the population has max(2 pairs, 2 sequences)
+    members, every sequence hosting the same number (per_seq); rank r evaluates members [r per_rank,
+    (r + 1) per_rank) in chunks of `chunk` (an even count; a chunk takes the sequence of its first member,
+    as the reference's chunk loop does), member g on direction (g mod 2 pairs) // 2 with sign +sigma for even
+    g. Returns [(start, n, first direction, sequence)] per chunk, on the host (no device work)."""
+    members = max(2 * pairs, 2 * sequences)
+    per_seq, per_rank = members // sequences, members // world
+    if chunk % 2 or per_rank % 2:
+        raise ValueError(f'member_plan: chunk ({chunk}) and members per rank ({per_rank}) must be even')
+    plan = []
+    for start in range(rank * per_rank, (rank + 1) * per_rank, chunk):
+        n = min(chunk, (rank + 1) * per_rank - start)
+        plan.append((start, n, (start % (2 * pairs)) // 2, start // per_seq))
+    return plan
+
+
 class Eggroll:
     """EGGROLL's perturbation bookkeeping (eggroll.py:106-128) over the virtual noise buffer.
 
@@ -543,23 +560,21 @@ class Eggroll:
         +sigma for even g and -sigma for odd g, sequence g // per_seq. names restricts which parameters
         are perturbed (None: all, as the reference)."""
         pairs = self.pairs
-        members = max(2 * pairs, 2 * len(x))
-        per_seq, per_rank = members // len(x), members // self.world
         offsets = self.offsets(step)
         if names is not None:
             offsets = {n: o for n, o in offsets.items() if n in names}
         W = weights if weights is not None else Weights(self.params, fp32_head=fp32_head)
+        plan = member_plan(pairs, len(x), self.rank, self.world, chunk)
+        per_rank = sum(c[1] for c in plan)
         losses = torch.empty(per_rank, device=self.device)
-        for start in range(self.rank * per_rank, (self.rank + 1) * per_rank, chunk):
-            n = min(chunk, (self.rank + 1) * per_rank - start)
-            directions = torch.arange(start, start + n, 2, device=self.device) % (2 * pairs) // 2
+        for start, n, _, seq in plan:
+            directions = (torch.arange(start, start + n, 2, device=self.device) % (2 * pairs)) // 2
             noise = {}
             for name, o in offsets.items():
                 p = self.params[name]
                 rows = self.buffer.gather(o, sum(p.shape), rows=directions)
                 noise[name] = tuple(rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
             sign = _pair_signs(n // 2, SIGMA, self.device)
-            seq = start // per_seq
             losses[start - self.rank * per_rank:start - self.rank * per_rank + n] = population_forward(
                 W, noise, sign, x[seq], y[seq], dir_div=2)
         return losses

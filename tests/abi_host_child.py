@@ -1,0 +1,82 @@
+"""Drives the C ABI's host layer of a libnoise_amd build without a GPU (run by test_abi_sanitized_cpu.py in a child
+process with the ASan runtime preloaded): every entry point with all-zero arguments, targeted invalid arguments,
+long error messages, and concurrent calls from several threads (the error message is per host thread). Loads
+noise_amd/abi.py by path, so that torch is never imported into the sanitized process."""
+import ctypes
+import importlib.util
+import sys
+import threading
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+spec = importlib.util.spec_from_file_location('noise_abi', ROOT / 'noise_amd' / 'abi.py')
+abi = importlib.util.module_from_spec(spec)
+spec.loader.exec_module(abi)
+
+lib = abi.bind(ctypes.CDLL(sys.argv[1]))
+QUERIES = {'noise_abi_version', 'noise_last_error', 'noise_dust_block_workspace_bytes',
+           'noise_dust_block_static_max_bytes', 'noise_update_workspace_bytes'}
+
+
+def zero(t):
+    return abi.View(None, 0, 0) if t == 'View' else (None if t is ctypes.c_void_p else t(0))
+
+
+def message():
+    return lib.noise_last_error().decode()
+
+
+assert lib.noise_abi_version() == 2
+rejected = 0
+for name, argtypes in abi.SIGNATURES.items():
+    fn = getattr(lib, name)
+    st = fn(*[zero(t) for t in argtypes])
+    if name in QUERIES:
+        continue
+    assert st != 0, f'{name} accepted all-zero arguments'
+    assert message(), f'{name} returned {st} without a message'
+    rejected += 1
+print(f'all-zero arguments: {rejected} entry points rejected them with a message', flush=True)
+
+# targeted invalid arguments (values that pass the NULL checks)
+pop = abi.Population(2, 300, None, 2, 0)
+assert lib.noise_pop_block(ctypes.byref(pop), abi.View(16, 0, 512), 16, None, None, 0, abi.View(16, 0, 512), 16, None,
+                           16, None, 16, 0, None, None, None, None, 0, abi.View(None, 0, 0), 16, 0, None, 0, None,
+                           None) == -1
+assert 'multiple of' in message()
+big = abi.Population(1 << 40, 1 << 40, None, 1, 0)
+assert lib.noise_member_mean(16, 1 << 40, 1 << 40, 16, None) != 0
+assert lib.noise_rank1_expand(ctypes.byref(big), 16, 4, 16, 0, None, 16, 1, None) == -1
+r1 = abi.Rank1(16, None, 4, 0)
+pop4 = abi.Population(4, 8, 16, 3, 0)
+assert lib.noise_rank1_expand(ctypes.byref(pop4), 16, 4, 16, 1, ctypes.byref(r1), 16, 1, None) == -1
+assert 'directions' in message()  # dots_stride 1 < 2 directions: the %lld message formatting
+assert lib.noise_attention_fwd(16, 16, 16, 16, 1, 1, 64, 32, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 10, 0.1, None, 0, 1,
+                               None, None) == -1
+assert 'head_dim' in message()
+print('targeted invalid arguments: rejected', flush=True)
+
+# concurrent calls: each thread's message is its own call's
+errors = []
+
+
+def worker(k):
+    try:
+        for _ in range(200):
+            p = abi.Population(2, 300 + 2 * k, None, 2, 0)
+            st = lib.noise_pop_block(ctypes.byref(p), abi.View(16, 0, 512), 16, None, None, 0, abi.View(16, 0, 512), 16,
+                                     None, 16, None, 16, 0, None, None, None, None, 0, abi.View(None, 0, 0), 16, 0,
+                                     None, 0, None, None)
+            assert st == -1 and f'({300 + 2 * k})' in message(), message()
+    except AssertionError as e:
+        errors.append(str(e))
+
+
+threads = [threading.Thread(target=worker, args=(k,)) for k in range(8)]
+for t in threads:
+    t.start()
+for t in threads:
+    t.join()
+assert not errors, errors[:3]
+print('threads: per-thread messages intact', flush=True)
+print('ok', flush=True)

@@ -107,15 +107,16 @@ def config5():
 
 
 def test_config5_population_vs_oracle(config5):
-    """Members 0-3 and 2044-2047 of the full 2048-member run against the fp32 CPU oracle within 1e-3;
-    the same members evaluated alone give bit-identical losses (members are independent)."""
+    """Members 0, 1, 1022-1025 (the two sides of the 1024-member chunk boundary) and 2046, 2047 of the full
+    2048-member run against the fp32 CPU oracle within 1e-3; the same members evaluated alone give
+    bit-identical losses (members are independent)."""
     from noise_amd.eggroll import orthogonal_population
     from oracle import model as om
     from oracle.orthogonal import orthogonal_directions as oracle_dirs
     P, shapes, noise, W, x, y, losses = config5
     assert losses.shape == (2048,) and torch.isfinite(losses).all()
-    dirs = torch.tensor([0, 1, 1022, 1023])
-    members = torch.tensor([0, 1, 2, 3, 2044, 2045, 2046, 2047])
+    dirs = torch.tensor([0, 511, 512, 1023])
+    members = torch.tensor([0, 1, 1022, 1023, 1024, 1025, 2046, 2047])
     sub = orthogonal_population(W, noise, x, y, sigma=0.002, directions=dirs)
     assert torch.equal(sub, losses[members.to(DEV)])
     # the oracle draws its own directions (bit-exact twin), then the fp32 population loss
