@@ -181,14 +181,22 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
 #pragma unroll
         for (int kb = 0; kb < 16; ++kb) xf[kb] = load_bf16x8(yr + 32 * kb);
     }
+    // the products accumulate onto the residual rows (x_mid = x + y W_o^T + rank-1): their loads fly together
+    // with the y rows and the first W_o step (block ob, register r holds feature 16 ob + 4 g + r)
+    f32x4 out[32];
+    {
+        const float *xr = p.xres + m * p.xr_m + (int64_t)tok * p.xr_t + 4 * g;
+#pragma unroll
+        for (int ob = 0; ob < 32; ++ob) {
+            const float4 v = ld4(xr + 16 * ob);
+            out[ob] = f32x4{v.x, v.y, v.z, v.w};
+        }
+    }
     vm_wait<0>();
     __syncthreads();
 
     // ---- attn.c_proj: out[ob] = W_o[16 ob ..] . y^T in 8 steps of two k blocks (unrolled: xf is indexed by
     // the step)
-    f32x4 out[32];
-#pragma unroll
-    for (int ob = 0; ob < 32; ++ob) out[ob] = f32x4{};
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         if (s + 1 < 8) issue_o(s + 1);  // its buffer was last read in step s - 1, before the barrier below
@@ -213,31 +221,23 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
     issue_stage(1);
     issue_stage(2);
 
-    // ---- x_mid = x + (product + sign (y . b_o) a_o); h = bf16(norm(x_mid)) into xf; c_fc's h . b from fp32
+    // ---- x_mid = (x + product) + sign (y . b_o) a_o; h = bf16(norm(x_mid)) into xf; c_fc's h . b from fp32
     float corr_fc = 0.f;
     {
         float osum = 0.f;
         if (p.ao)
             for (int k = 0; k < p.odots_n; ++k) osum += p.odots[row * p.odots_n + k];
         const float corr_o = sgn * osum;
-        const float *xr = p.xres + m * p.xr_m + (int64_t)tok * p.xr_t + 4 * g;
         const float *ao = reinterpret_cast<const float *>(lds + kVAo) + 4 * g;
         float ssq = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {  // 8 output blocks at a time: their residual loads in flight together
-            float4 xv[8];
+        for (int ob = 0; ob < 32; ++ob) {
+            const float4 a4 = ld4(ao + 16 * ob);
 #pragma unroll
-            for (int i = 0; i < 8; ++i) xv[i] = ld4(xr + 16 * (8 * q + i));
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int ob = 8 * q + i;
-                const float4 a4 = ld4(ao + 16 * ob);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const float v = f4get(xv[i], r) + (out[ob][r] + corr_o * f4get(a4, r));
-                    out[ob][r] = v;
-                    ssq += v * v;
-                }
+            for (int r = 0; r < 4; ++r) {
+                const float v = out[ob][r] + corr_o * f4get(a4, r);
+                out[ob][r] = v;
+                ssq += v * v;
             }
         }
         const float rstd = rsqrtf(token_sum(ssq) * (1.0f / kModel) + kBlkEps);
