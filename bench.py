@@ -51,6 +51,8 @@ def kernel_flops_per_launch(name, label, members, T):
         return 2 * 2 * 512 * 2048 * rows
     if name in ('noise_pop_attn_mlp', 'noise_pop_block'):
         return 2 * (512 * 512 + 2 * 512 * 2048) * rows
+    if name == 'noise_pop_block_qkv':
+        return 2 * (512 * 512 + 2 * 512 * 2048 + 512 * 1536) * rows
     if name == 'noise_pop_head_ce':
         return 2 * 512 * 4096 * rows
     if name == 'noise_attention_fwd':
@@ -60,9 +62,11 @@ def kernel_flops_per_launch(name, label, members, T):
 
 
 PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', 'population_forward_1024x2048.md')
-# entry point (bench label) -> the kernel name in the committed trace of the default workload
+# entry point (bench label) -> the kernel name in the committed trace of the default workload (the block
+# kernels that form the next block's q/k/v: 4 of their 7 launches carry value embeddings)
 ROCPROF_NAME = {'noise_pop_qkv': 'qkv16_kernel<false>', 'noise_pop_head_ce': 'head_x_kernel<false, false>',
-                'noise_pop_block[block]': 'block_kernel<true, 3, false>'}
+                'noise_pop_block_qkv[block]': 'block_kernel<true, 3, false, 2>',
+                'noise_pop_block[block]': 'block_kernel<false, 0, false, 0>'}
 
 
 def profiled_traffic(kernel):

@@ -282,6 +282,24 @@ int noise_pop_block(const noise_population_t *pop, noise_view_t y, const void *w
                     void *hout, int split3, const noise_rank1_t *next, int64_t nnext, float *next_dots,
                     noise_stream_t stream);
 
+/* noise_pop_block followed, in the same kernel, by the next block's noise_pop_gate and noise_pop_qkv on
+ * h = bf16(norm(xout)) (eggroll.py:92-94, then 81-90 of the next block): h and the next dots never reach HBM.
+ * The first 19 arguments as noise_pop_block (xout required; no hout); then noise_pop_qkv's w, r1 (their b rows
+ * replace noise_pop_block's next vectors: the dots of every perturbed matrix are formed from the fp32 norm),
+ * rotary tables, ve, vocab, idx, idx_sm and ve_noise, with the value-embedding gate's weights gate_w
+ * ([8][32] fp32) and noise (noise_pop_gate's gate_noise) in place of precomputed gates. w_qkv in the column
+ * order noise_block_weight_layout writes; outputs 16 B aligned. q, k, v as noise_pop_qkv writes them (up to the
+ * products' summation order); the gates bit for bit as noise_pop_gate's. No counterpart in the reference beyond
+ * the call sites it replaces. */
+int noise_pop_block_qkv(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
+                        const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
+                        const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout,
+                        int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+                        int64_t eps_stride, noise_view_t x0, const void *const w_qkv[3], const noise_rank1_t r_qkv[3],
+                        const void *rope_cos, const void *rope_sin, const float *ve, int64_t vocab,
+                        const int64_t *idx, int64_t idx_sm, const float *gate_w, const noise_rank1_t *gate_noise,
+                        const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream);
+
 /* w [rows][cols] bf16 -> the column order noise_pop_block reads: within every 32 columns, position 8g + j
  * (g < 4) holds column 4g + j for j < 4 and 16 + 4g + (j - 4) for j >= 4. cols a multiple of 32. */
 int noise_block_weight_layout(const void *w, void *out, int64_t rows, int64_t cols, noise_stream_t stream);

@@ -31,6 +31,8 @@ SIGNATURES = {
                            'View', _p, _i32, _p, _i64, _p, _p],
     'noise_pop_block': [_p, 'View', _p, _p, _p, _i64, 'View', _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _i64,
                         'View', _p, _i32, _p, _i64, _p, _p],
+    'noise_pop_block_qkv': [_p, 'View', _p, _p, _p, _i64, 'View', _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _i64,
+                            'View', _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _p, _p, _p, _p],
     'noise_block_weight_layout': [_p, _p, _i64, _i64, _p],
     'noise_mlp_proj_layout': [_p, _p, _i64, _p],
     'noise_pop_linear': [_p, 'View', _p, _i64, _i64, _p, _p, _p, _i32, _i64, _i64, _p],

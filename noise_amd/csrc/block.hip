@@ -27,8 +27,15 @@
 //   - a token's 512 features are spread over the four lanes l % 16 + 16 g: RMSNorm and the dots need two
 //     exchanges (lane ^ 16, lane ^ 32).
 // The second wave on each SIMD issues while the other waits on its fragment reads, its ReLU^2 or the barrier.
+//
+// noise_pop_block_qkv runs the next block's value-embedding gates and q/k/v (qkv_phase.hpp) after the tail in
+// the same workgroup: h = bf16(norm(y)) goes from the accumulators into the phase's B operand in the permuted
+// k order (c_q, c_k, c_v come permuted like c_fc), the next dots stay in registers as the phase's rank-1
+// scales, and neither h nor the dots reach HBM; the phase's stage buffers reuse the step buffers once every
+// wave has stored its residual rows.
 #include "common.hpp"
 #include "mfma.hpp"
+#include "qkv_phase.hpp"
 #include "tile.hpp"
 
 namespace noise {
@@ -60,6 +67,7 @@ constexpr int kVAo = kVNb + 3 * kModel * 4;      // attn.c_proj's a [512]
 constexpr int kVBfc = kVAo + kModel * 4;         // c_fc's b       [512]
 constexpr int kBlkLds = kVBfc + kModel * 4;      // 156 KiB
 static_assert(kBlkLds <= 160 * 1024, "LDS of one CU");
+constexpr int kBlkQkvLds = kBlkLds > kQLds ? kBlkLds : kQLds;  // with the next block's q/k/v phase
 
 struct BlockArgs {
     int members, tokens, dir_div;
@@ -89,6 +97,7 @@ struct BlockArgs {
     const float *nb[3];
     int64_t nb_stride[3];
     float *ndots;                          // [rows][NNEXT]
+    QkvRowsArgs q;                         // the next block's q/k/v (QKV): its x is h, its dots come from the epilogue
 };
 
 // sum over the four lanes holding one token's features (l % 16 + 16 g)
@@ -97,9 +106,11 @@ __device__ __forceinline__ float token_sum(float v) {
     return v + __shfl_xor(v, 32, 64);
 }
 
-template <bool MIX, int NNEXT, bool SPLIT3>
+// QKV: 0, or the next block's q/k/v after the tail (1; 2 with its value embeddings) in place of the hout and
+// next_dots stores
+template <bool MIX, int NNEXT, bool SPLIT3, int QKV>
 __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
-    __shared__ __attribute__((aligned(16))) char lds[kBlkLds];
+    __shared__ __attribute__((aligned(16))) char lds[QKV ? kBlkQkvLds : kBlkLds];
     const int T = p.tokens, tiles_t = T / kBlkTok;
     const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * kBlkTok;
     const int tid = threadIdx.x, lane = tid & 63, tl = lane & 15, g = lane >> 4;
@@ -121,7 +132,8 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         vcopy(p.apj ? p.bpj + dir * p.bpj_stride : nullptr, kVBpj, kHidden);
         vcopy(p.apj ? p.apj + dir * p.apj_stride : nullptr, kVApj, kModel);
 #pragma unroll
-        for (int k = 0; k < NNEXT; ++k) vcopy(p.nb[k] + dir * p.nb_stride[k], kVNb + k * kModel * 4, kModel);
+        for (int k = 0; k < NNEXT; ++k)
+            vcopy(p.nb[k] ? p.nb[k] + dir * p.nb_stride[k] : nullptr, kVNb + k * kModel * 4, kModel);
         vcopy(p.ao ? p.ao + dir * p.ao_stride : nullptr, kVAo, kModel);
         vcopy(p.afc ? p.bfc + dir * p.bfc_stride : nullptr, kVBfc, kModel);
     }
@@ -371,6 +383,7 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         }
     }
     const float rstd = rsqrtf(token_sum(ssq) * (1.0f / kModel) + kBlkEps);
+    float dq[3] = {0.f, 0.f, 0.f};  // QKV: sign * (h . b) of the next c_q, c_k, c_v from the fp32 norm
 #pragma unroll
     for (int k = 0; k < NNEXT; ++k) {
         const float *nb = reinterpret_cast<const float *>(lds + kVNb + k * kModel * 4) + 4 * g;
@@ -382,7 +395,10 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
             for (int r = 0; r < 4; ++r) d += out[ob][r] * f4get(b4, r);
         }
         d = token_sum(d);
-        if (g == 0) p.ndots[row * NNEXT + k] = rstd * d;
+        if constexpr (QKV != 0)
+            dq[k] = p.q.a[k] ? sgn * (rstd * d) : 0.f;
+        else if (g == 0)
+            p.ndots[row * NNEXT + k] = rstd * d;
     }
     // whole-line stores through the wave's 16 KiB of the (free) step buffers: rows of 1 KiB, 16 B chunk c of
     // row t at position c ^ t
@@ -404,6 +420,28 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
                     *reinterpret_cast<const float4 *>(stg + it * 1024 + ((lane ^ it) << 4)));
             wave_lds_sync();  // the staging rows are rewritten next
         }
+    }
+    if constexpr (QKV != 0) {
+        // the next block's q/k/v from h = bf16(norm(y)), packed as the B operand in the permuted k order (c_q, c_k
+        // and c_v come with their columns permuted as c_fc's)
+#pragma unroll
+        for (int kb = 0; kb < 16; ++kb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                xf[kb][r] = (__bf16)(out[2 * kb][r] * rstd);
+                xf[kb][4 + r] = (__bf16)(out[2 * kb + 1][r] * rstd);
+            }
+        __syncthreads();  // every wave has read back its staged rows: the stage buffers are free
+#pragma unroll
+        for (int k = 0; k < 3; ++k) qkv_issue(p.q, lbase, wave, lane, k);
+        QkvLane L;
+        L.m = m; L.t0 = t0; L.tok = tok; L.wave = wave; L.lane = lane; L.tid = tid; L.dir = dir; L.row = row;
+        L.sgn = sgn; L.dq0 = dq[0]; L.dq1 = dq[1]; L.dq2 = dq[2];
+        qkv_token_scalars<QKV == 2>(p.q, L);
+        vm_wait<0>();  // the three stages and the scalars landed
+        __syncthreads();
+        qkv_phase<QKV == 2, true>(p.q, lds, xf, L);
+        return;
     }
     // bf16 rows (hi, and lo for the split3 head input): 1 KiB rows, 16 B chunk c of row t at c ^ t
     const int width = SPLIT3 ? 3 * kModel : kModel;
@@ -452,9 +490,9 @@ __global__ __launch_bounds__(256) void block_layout_kernel(const __bf16 *w, __bf
 template <bool MIX, int NNEXT>
 void launch_block_n(const BlockArgs &a, bool split3, dim3 grid, hipStream_t s) {
     if (split3)
-        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, true>), grid, dim3(kBlkThreads), 0, s, a);
+        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, true, 0>), grid, dim3(kBlkThreads), 0, s, a);
     else
-        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, false>), grid, dim3(kBlkThreads), 0, s, a);
+        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, false, 0>), grid, dim3(kBlkThreads), 0, s, a);
 }
 
 template <bool MIX>
@@ -465,6 +503,23 @@ void launch_block(const BlockArgs &a, int nnext, bool split3, dim3 grid, hipStre
         case 2: launch_block_n<MIX, 2>(a, split3, grid, s); break;
         default: launch_block_n<MIX, 3>(a, split3, grid, s); break;
     }
+}
+
+// with the next block's q/k/v: its dots for all three matrices or none
+template <bool MIX, int NNEXT>
+void launch_block_qkv_n(const BlockArgs &a, bool ve, dim3 grid, hipStream_t s) {
+    if (ve)
+        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, false, 2>), grid, dim3(kBlkThreads), 0, s, a);
+    else
+        hipLaunchKernelGGL((block_kernel<MIX, NNEXT, false, 1>), grid, dim3(kBlkThreads), 0, s, a);
+}
+
+template <bool MIX>
+void launch_block_qkv(const BlockArgs &a, int nnext, bool ve, dim3 grid, hipStream_t s) {
+    if (nnext)
+        launch_block_qkv_n<MIX, 3>(a, ve, grid, s);
+    else
+        launch_block_qkv_n<MIX, 0>(a, ve, grid, s);
 }
 
 }  // namespace
@@ -482,14 +537,15 @@ extern "C" int noise_block_weight_layout(const void *w, void *out, int64_t rows,
     return launch_status("noise_block_weight_layout");
 }
 
-extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
-                               const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
-                               const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout,
-                               int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
-                               int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
-                               int64_t nnext, float *next_dots, noise_stream_t stream) {
-    clear_error();
-    const char *fn = "noise_pop_block";
+namespace noise {
+namespace {
+
+// checks and arguments of the block's tail, shared by the two block entry points
+int block_args(const char *fn, BlockArgs &a, const noise_population_t *pop, noise_view_t y, const void *w_o,
+               const noise_rank1_t *r_o, const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
+               const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout, int mix,
+               const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x, int64_t eps_stride,
+               noise_view_t x0, const noise_rank1_t *next, int64_t nnext) {
     NOISE_CHECK_ARG(pop && pop->members > 0 && pop->tokens > 0 && pop->dir_div >= 1, "%s: bad population", fn);
     NOISE_CHECK_ARG(pop->tokens % kBlkTok == 0, "%s: tokens (%lld) must be a multiple of %d", fn,
                     (long long)pop->tokens, kBlkTok);
@@ -503,8 +559,7 @@ extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, co
     NOISE_CHECK_ARG(!mix || (x0.ptr && aligned(x0.ptr, 16) && x0.sm % 4 == 0 && x0.st % 4 == 0 && lam_r && lam_x),
                     "%s: mixing needs x0 and the mixing scalars", fn);
     NOISE_CHECK_ARG(!(eps_r || eps_x) || (mix && pop->sign), "%s: mixing-scalar noise needs mix and sign", fn);
-    NOISE_CHECK_ARG(hout && aligned(hout, 16), "%s: hout NULL or misaligned", fn);
-    NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || (next && next_dots)), "%s: bad next-dot request", fn);
+    NOISE_CHECK_ARG(nnext >= 0 && nnext <= 3 && (nnext == 0 || next), "%s: bad next-dot request", fn);
     const bool po = r_o && r_o->a, pfc = r_fc && r_fc->a, ppj = r_proj && r_proj->a;
     NOISE_CHECK_ARG(!po || (pop->sign && o_dots && o_dots_n >= 1 && aligned(r_o->a, 16) && r_o->a_stride % 4 == 0),
                     "%s: attn.c_proj noise needs sign, dots and 16 B aligned a rows", fn);
@@ -514,7 +569,7 @@ extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, co
     NOISE_CHECK_ARG(!ppj || (pop->sign && r_proj->b && aligned(r_proj->a, 16) && aligned(r_proj->b, 16) &&
                              r_proj->a_stride % 4 == 0 && r_proj->b_stride % 4 == 0),
                     "%s: mlp.c_proj noise needs sign and 16 B aligned a, b rows", fn);
-    BlockArgs a{};
+    a = BlockArgs{};
     a.members = (int)pop->members; a.tokens = (int)pop->tokens; a.dir_div = (int)pop->dir_div; a.sign = pop->sign;
     a.y = (const __bf16 *)y.ptr; a.ys_m = y.sm; a.ys_t = y.st;
     a.wo = (const __bf16 *)w_o;
@@ -530,7 +585,6 @@ extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, co
     a.xout = xout;
     a.lam_r = lam_r; a.lam_x = lam_x; a.eps_r = eps_r; a.eps_x = eps_x; a.eps_stride = eps_stride;
     a.x0 = (const float *)x0.ptr; a.x0_m = x0.sm; a.x0_t = x0.st;
-    a.hout = (__bf16 *)hout;
     for (int k = 0; k < 3; ++k) {
         a.nb[k] = k < nnext ? next[k].b : nullptr;
         a.nb_stride[k] = k < nnext ? next[k].b_stride : 0;
@@ -538,11 +592,86 @@ extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, co
             NOISE_CHECK_ARG(next[k].b && aligned(next[k].b, 16) && next[k].b_stride % 4 == 0,
                             "%s: next b %d NULL or misaligned", fn, k);
     }
+    return NOISE_OK;
+}
+
+}  // namespace
+}  // namespace noise
+
+extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
+                               const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
+                               const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout,
+                               int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+                               int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
+                               int64_t nnext, float *next_dots, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_block";
+    BlockArgs a;
+    const int st = block_args(fn, a, pop, y, w_o, r_o, o_dots, o_dots_n, xres, w_fc, r_fc, w_proj, r_proj, xout, mix,
+                              lam_r, lam_x, eps_r, eps_x, eps_stride, x0, next, nnext);
+    if (st != NOISE_OK) return st;
+    NOISE_CHECK_ARG(hout && aligned(hout, 16), "%s: hout NULL or misaligned", fn);
+    NOISE_CHECK_ARG(nnext == 0 || next_dots, "%s: next dots need an output", fn);
+    a.hout = (__bf16 *)hout;
     a.ndots = next_dots;
     const dim3 grid((unsigned)(pop->members * (pop->tokens / kBlkTok)));
     if (mix)
         launch_block<true>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
     else
         launch_block<false>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
+    return launch_status(fn);
+}
+
+extern "C" int noise_pop_block_qkv(const noise_population_t *pop, noise_view_t y, const void *w_o,
+                                   const noise_rank1_t *r_o, const float *o_dots, int64_t o_dots_n, noise_view_t xres,
+                                   const void *w_fc, const noise_rank1_t *r_fc, const void *w_proj,
+                                   const noise_rank1_t *r_proj, float *xout, int mix, const float *lam_r,
+                                   const float *lam_x, const float *eps_r, const float *eps_x, int64_t eps_stride,
+                                   noise_view_t x0, const void *const w_qkv[3], const noise_rank1_t r_qkv[3],
+                                   const void *rope_cos, const void *rope_sin, const float *ve, int64_t vocab,
+                                   const int64_t *idx, int64_t idx_sm, const float *gate_w,
+                                   const noise_rank1_t *gate_noise, const noise_rank1_t *ve_noise, void *const out[3],
+                                   noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_pop_block_qkv";
+    const bool pq = r_qkv && (r_qkv[0].a || r_qkv[1].a || r_qkv[2].a);
+    BlockArgs a;
+    const int st = block_args(fn, a, pop, y, w_o, r_o, o_dots, o_dots_n, xres, w_fc, r_fc, w_proj, r_proj, xout, mix,
+                              lam_r, lam_x, eps_r, eps_x, eps_stride, x0, nullptr, 0);
+    if (st != NOISE_OK) return st;
+    NOISE_CHECK_ARG(xout, "%s: xout (the next block's residual) must not be NULL", fn);
+    // the dots of the perturbed matrices (an unperturbed one's b reads as zeros)
+    for (int k = 0; k < 3 && pq; ++k) {
+        if (!r_qkv[k].a) continue;
+        NOISE_CHECK_ARG(r_qkv[k].b && aligned(r_qkv[k].b, 16) && r_qkv[k].b_stride % 4 == 0,
+                        "%s: q/k/v noise b %d NULL or misaligned", fn, k);
+        a.nb[k] = r_qkv[k].b;
+        a.nb_stride[k] = r_qkv[k].b_stride;
+    }
+    NOISE_CHECK_ARG(w_qkv && out && rope_cos && rope_sin && aligned(rope_cos, 16) && aligned(rope_sin, 16),
+                    "%s: NULL q/k/v weight or output array, or rotary tables not 16 B aligned", fn);
+    for (int i = 0; i < 3; ++i) {
+        NOISE_CHECK_ARG(w_qkv[i] && out[i] && aligned(w_qkv[i], 16) && aligned(out[i], 16),
+                        "%s: q/k/v weight or output %d NULL or not 16 B aligned", fn, i);
+        NOISE_CHECK_ARG(!pq || !r_qkv[i].a || (pop->sign && aligned(r_qkv[i].a, 16) && r_qkv[i].a_stride % 4 == 0),
+                        "%s: perturbed matrix %d needs sign and 16 B aligned a rows", fn, i);
+    }
+    NOISE_CHECK_ARG(!ve || (idx && gate_w && vocab > 0), "%s: value embeddings need idx, gate weights and vocab", fn);
+    NOISE_CHECK_ARG(idx_sm == 0 || idx_sm >= pop->tokens, "%s: idx_sm must be 0 or >= tokens", fn);
+    const bool gn = ve && gate_noise && gate_noise->a;
+    NOISE_CHECK_ARG(!gn || (pop->sign && gate_noise->b), "%s: gate noise needs sign and b", fn);
+    const bool vn = ve && ve_noise && ve_noise->a;
+    NOISE_CHECK_ARG(!vn || (pop->sign && ve_noise->b && aligned(ve_noise->b, 16) && ve_noise->b_stride % 4 == 0),
+                    "%s: value-embedding noise needs sign and 16 B aligned b rows", fn);
+    a.q = qkv_rows_args(pop, noise_view_t{nullptr, 0, 0}, w_qkv, r_qkv, nullptr, rope_cos, rope_sin, ve, vocab, idx,
+                        idx_sm, nullptr, ve_noise, out);
+    a.q.gate_w = gate_w;
+    a.q.gate_a = gn ? gate_noise->a : nullptr; a.q.gate_b = gn ? gate_noise->b : nullptr;
+    a.q.gate_a_stride = gn ? gate_noise->a_stride : 0; a.q.gate_b_stride = gn ? gate_noise->b_stride : 0;
+    const dim3 grid((unsigned)(pop->members * (pop->tokens / kBlkTok)));
+    if (mix)
+        launch_block_qkv<true>(a, pq ? 3 : 0, ve != nullptr, grid, (hipStream_t)stream);
+    else
+        launch_block_qkv<false>(a, pq ? 3 : 0, ve != nullptr, grid, (hipStream_t)stream);
     return launch_status(fn);
 }

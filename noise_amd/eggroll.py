@@ -139,8 +139,12 @@ class Weights:
             blk = dict(q=bf(pre + 'attn.c_q.weight'), k=bf(pre + 'attn.c_k.weight'), v=bf(pre + 'attn.c_v.weight'),
                        o=bf(pre + 'attn.c_proj.weight'), fc=bf(pre + 'mlp.c_fc.weight'),
                        mp=bf(pre + 'mlp.c_proj.weight'))
-            # mlp.c_fc and mlp.c_proj in the block kernel's column order (within every 32 columns)
-            for src, dst in (('mp', 'mp_blk'), ('fc', 'fc_blk')):
+            # mlp.c_fc and mlp.c_proj in the block kernel's column order (within every 32 columns); so are c_q, c_k
+            # and c_v of the blocks whose q/k/v the previous block's kernel forms
+            perm = [('mp', 'mp_blk'), ('fc', 'fc_blk')]
+            if i:
+                perm += [('q', 'q_blk'), ('k', 'k_blk'), ('v', 'v_blk')]
+            for src, dst in perm:
                 blk[dst] = torch.empty_like(blk[src])
                 _lib.call('noise_block_weight_layout', blk[src].data_ptr(), blk[dst].data_ptr(), blk[src].shape[0],
                           blk[src].shape[1], _lib.stream_ptr(dev))
@@ -198,7 +202,7 @@ def _zero_b(dev, width):
 
 
 def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffers=None, per_token=False,
-                       rounding=_lib.ROUNDING_FUSED):
+                       rounding=_lib.ROUNDING_FUSED, fuse_qkv=True):
     """Per-member mean cross-entropy [m] of the perturbed models (eggroll.py:66-103 semantics).
 
     W: Weights. noise: name -> (a [dirs, out], b [dirs, in]) fp32 row views for matrices and embeddings,
@@ -209,7 +213,9 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     (default: rotary_tables(T)). per_token: return the [m, T] per-token losses (0 at targets < 0) instead
     of the member means (a view of the buffers' storage). rounding: ROUNDING_FUSED (the compiled training
     forward) or ROUNDING_EAGER (the scorer's eager autocast forward, bf16 residual stream; noise must be
-    empty)."""
+    empty). fuse_qkv: with fused rounding, each block's kernel also forms the next block's gates and q/k/v
+    (noise_pop_block_qkv); False launches them on their own (same results up to the products' summation
+    order)."""
     dev = W.device
     m, T = sign.shape[0], idx.shape[-1]
     if T % 256:
@@ -276,6 +282,7 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
         _call('noise_member_dots', popp, _view(B.h0, sm_e, E), E, dot_vecs(n0, E), 3, B.d_qkv.data_ptr(), stream)
 
     qkv_out = (ctypes.c_void_p * 3)(*(B.qkv[i].data_ptr() for i in range(3)))
+    qkv_ready = False
     for i in range(L):
         pre = f'transformer.h.{i}.'
         blk = W.blocks[i]
@@ -283,24 +290,27 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
         x_in = _view(B.h0, sm_e, E) if i == 0 else _view(B.h, T * E, E)
         ws = (ctypes.c_void_p * 3)(blk['q'].data_ptr(), blk['k'].data_ptr(), blk['v'].data_ptr())
         ve_r1 = _rank1(nz(f'value_embeds.{i}.weight'))
-        if 've' in blk:
-            gate_r1 = _rank1(nz(pre + 'attn.ve_gate.weight'))
-            _call('noise_pop_gate', popp, x_in, blk['gate'].data_ptr(), ctypes.byref(gate_r1), B.gates.data_ptr(),
-                  stream)
-        if i == 0 and B.qkv_base is not None and 've' not in blk and rounding == _lib.ROUNDING_FUSED:
-            # every member reads the same block input: its product with c_q, c_k, c_v is computed once and
-            # each member adds its rank-1 terms before rotary and norm
-            one = _lib.Population(1, T, None, 1, _lib.ROUNDING_FUSED)
-            for j in range(3):
-                _call('noise_pop_linear', ctypes.byref(one), x_in, ws[j], E, E, None, None,
-                      B.qkv_base.data_ptr() + 4 * E * j, 1, T * 3 * E, 3 * E, stream)
-            _call('noise_pop_qkv_shared', popp, B.qkv_base.data_ptr(), _rank1_array(nq), B.d_qkv.data_ptr(),
-                  cos_t.data_ptr(), sin_t.data_ptr(), qkv_out, stream)
+        if qkv_ready:
+            qkv_ready = False  # the previous block's kernel formed this block's gates and q/k/v
         else:
-            _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
-                  sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None,
-                  blk['ve'].shape[0] if 've' in blk else 0, idx.data_ptr(), idx_sm,
-                  B.gates.data_ptr() if 've' in blk else None, ctypes.byref(ve_r1), qkv_out, stream)
+            if 've' in blk:
+                gate_r1 = _rank1(nz(pre + 'attn.ve_gate.weight'))
+                _call('noise_pop_gate', popp, x_in, blk['gate'].data_ptr(), ctypes.byref(gate_r1), B.gates.data_ptr(),
+                      stream)
+            if i == 0 and B.qkv_base is not None and 've' not in blk and rounding == _lib.ROUNDING_FUSED:
+                # every member reads the same block input: its product with c_q, c_k, c_v is computed once and
+                # each member adds its rank-1 terms before rotary and norm
+                one = _lib.Population(1, T, None, 1, _lib.ROUNDING_FUSED)
+                for j in range(3):
+                    _call('noise_pop_linear', ctypes.byref(one), x_in, ws[j], E, E, None, None,
+                          B.qkv_base.data_ptr() + 4 * E * j, 1, T * 3 * E, 3 * E, stream)
+                _call('noise_pop_qkv_shared', popp, B.qkv_base.data_ptr(), _rank1_array(nq), B.d_qkv.data_ptr(),
+                      cos_t.data_ptr(), sin_t.data_ptr(), qkv_out, stream)
+            else:
+                _call('noise_pop_qkv', popp, x_in, ws, _rank1_array(nq), B.d_qkv.data_ptr(), cos_t.data_ptr(),
+                      sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None,
+                      blk['ve'].shape[0] if 've' in blk else 0, idx.data_ptr(), idx_sm,
+                      B.gates.data_ptr() if 've' in blk else None, ctypes.byref(ve_r1), qkv_out, stream)
         # attention; its epilogue also forms y . b_o per head for c_proj's rank-1 term
         no = nz(pre + 'attn.c_proj.weight')
         q4, k4 = (B.qkv[j].transpose(1, 2) for j in range(2))  # [m, T, H, D] views of [m, H, T, D]
@@ -334,6 +344,21 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
                 nxt, nnext, ndots = (dot_vecs([nh], E), 1, B.d_head.data_ptr()) if nh is not None else (None, 0, None)
                 hout, split3 = (B.h3, 1) if W.fp32_head else (B.h, 0)
                 mixargs = (0, None, None, None, None, 0)
+            if not last and fuse_qkv:
+                # ... and the next block's gates and q/k/v from its normalised input, which stays in registers
+                nblk, npre = W.blocks[i + 1], f'transformer.h.{i + 1}.'
+                nws = (ctypes.c_void_p * 3)(nblk['q_blk'].data_ptr(), nblk['k_blk'].data_ptr(),
+                                            nblk['v_blk'].data_ptr())
+                n_ve, n_gate = _rank1(nz(f'value_embeds.{i + 1}.weight')), _rank1(nz(npre + 'attn.ve_gate.weight'))
+                _call('noise_pop_block_qkv', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), ctypes.byref(o_r1),
+                      B.d_attn.data_ptr(), N_HEAD, xres, blk['fc_blk'].data_ptr(), ctypes.byref(fc_r1),
+                      blk['mp_blk'].data_ptr(), ctypes.byref(mp_r1), B.resid.data_ptr(), *mixargs,
+                      _view(B.x0, sm_e, E), nws, _rank1_array(nn), cos_t.data_ptr(), sin_t.data_ptr(),
+                      nblk['ve'].data_ptr() if 've' in nblk else None, nblk['ve'].shape[0] if 've' in nblk else 0,
+                      idx.data_ptr(), idx_sm, nblk['gate'].data_ptr() if 've' in nblk else None,
+                      ctypes.byref(n_gate), ctypes.byref(n_ve), qkv_out, stream, label='block')
+                qkv_ready = True
+                continue
             _call('noise_pop_block', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), ctypes.byref(o_r1),
                   B.d_attn.data_ptr(), N_HEAD, xres, blk['fc_blk'].data_ptr(), ctypes.byref(fc_r1),
                   blk['mp_blk'].data_ptr(), ctypes.byref(mp_r1), None if last else B.resid.data_ptr(), *mixargs,

@@ -44,6 +44,10 @@ assert lib.noise_pop_block(ctypes.byref(pop), abi.View(16, 0, 512), 16, None, No
                            16, None, 16, 0, None, None, None, None, 0, abi.View(None, 0, 0), 16, 0, None, 0, None,
                            None) == -1
 assert 'multiple of' in message()
+assert lib.noise_pop_block_qkv(ctypes.byref(pop), abi.View(16, 0, 512), 16, None, None, 0, abi.View(16, 0, 512), 16,
+                               None, 16, None, 16, 0, None, None, None, None, 0, abi.View(None, 0, 0), None, None, None,
+                               None, None, 0, None, 0, None, None, None, None, None) == -1
+assert 'multiple of' in message()
 big = abi.Population(1 << 40, 1 << 40, None, 1, 0)
 assert lib.noise_member_mean(16, 1 << 40, 1 << 40, 16, None) != 0
 assert lib.noise_rank1_expand(ctypes.byref(big), 16, 4, 16, 0, None, 16, 1, None) == -1
