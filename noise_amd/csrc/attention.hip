@@ -279,7 +279,10 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
 // v_cvt_pk_bf16_f32. BOUNDED: the caller guarantees q and k rows of RMS <= 1 (RMSNorm outputs, as
 // utils/model.py:94 applies to both), so |score * scale * log2 e| <= D * scale * log2 e (+ bf16 rounding)
 // = shift, and exp2(score * scale * log2 e - shift) <= 1 needs no running maximum (softmax is
-// shift-invariant; fp32 and bf16 keep full relative precision down to 2^-126).
+// shift-invariant; fp32 and bf16 keep full relative precision down to 2^-126). There q is pre-scaled by
+// scale * log2 e and the products accumulate onto -shift, so each score leaves the MFMA as its exponent, and
+// the row sum is taken from the bf16 weights that P V uses (v_dot2_f32_bf16): one exp, half a pack and a
+// quarter dot per score.
 // ------------------------------------------------------------------------------------------------
 constexpr int kStage = 2 * 64 * 128;  // K [64 keys][64 d] then V^T [64 d][64 keys], 128 B rows
 constexpr int kVtQT = 256;  // queries per workgroup of the transposed-V kernel
@@ -331,6 +334,17 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     // the query fragments land before any tile copy is issued: the compiler's own wait for them inside the
     // tile loop would otherwise be a vmcnt that also drains the copies in flight
     vm_wait<0>();
+    if constexpr (BOUNDED) {
+        // q pre-scaled by scale * log2 e (one more bf16 rounding of q, within the shift's margin): with the
+        // products accumulated onto -shift, a score leaves the MFMA as its softmax exponent
+        const float c = a.scale_log2;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int s = 0; s < 4; ++s)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qf[qb][s][e] = (__bf16)((float)qf[qb][s][e] * c);
+    }
 
     // copies: per stage 16 of 1 KB (8 rows); A wave w issues copies c = 4 i + w, rows 8 (c % 8) .. of K (c < 8)
     // or V^T. Row R's slot P holds chunk P ^ ((R >> 1) & 7); for this lane R = 8 c' + lane / 8, so the chunk
@@ -381,13 +395,18 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     bf16x8 pf[QB][4];
     auto tile_k0 = [&](int t) { return (kv_first + t) * kBKV; };
     auto active = [&](int t) { return tile_k0(t) <= wq_hi && tile_k0(t) + kBKV - 1 >= wq_lo - W; };
-    // S = K Q^T of tile t (slot t % NS)
+    // S = K Q^T of tile t (slot t % NS); BOUNDED: K (c2 Q)^T - shift, the exponents
     auto qk = [&](int t) {
         const char *st = lds + (t % NS) * kStage;
+        f32x16 init = f32x16{};
+        if constexpr (BOUNDED) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) init[r] = -shift;
+        }
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = f32x16{};
+            for (int qb = 0; qb < QB; ++qb) sc[kb][qb] = init;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -448,18 +467,25 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                 for (int r = 0; r < 16; ++r) {
-                    const float p = exp2_fast(__builtin_fmaf(sc[kb][qb][r], c2, -mb));
+                    const float p = BOUNDED ? exp2_fast(sc[kb][qb][r]) : exp2_fast(__builtin_fmaf(sc[kb][qb][r], c2, -mb));
                     sc[kb][qb][r] = p;
-                    rs += p;
+                    if constexpr (!BOUNDED) rs += p;
                 }
-            l[qb] += rs;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
                 bf16x8 v;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = (__bf16)sc[s >> 1][qb][8 * (s & 1) + e];
                 pf[qb][s] = v;
+                if constexpr (BOUNDED) {
+                    // the row sum of the bf16 weights P^T carries into O^T, two per dot
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2)
+                        rs = __builtin_amdgcn_fdot2_f32_bf16(bf16x2{v[e], v[e + 1]}, bf16x2{(__bf16)1.0f, (__bf16)1.0f},
+                                                             rs, false);
+                }
             }
+            l[qb] += rs;
         }
     };
     // O += V^T P^T of tile t
