@@ -204,6 +204,11 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
             out[ob] = f32x4{v.x, v.y, v.z, v.w};
         }
     }
+    // y . b_o from the attention kernel's per-head partial sums, read with the rows (read after the MLP's first
+    // copies, they would wait for those too)
+    float osum = 0.f;
+    if (p.ao)
+        for (int k = 0; k < p.odots_n; ++k) osum += p.odots[row * p.odots_n + k];
     vm_wait<0>();
     __syncthreads();
 
@@ -236,9 +241,6 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
     // ---- x_mid = (x + product) + sign (y . b_o) a_o; h = bf16(norm(x_mid)) into xf; c_fc's h . b from fp32
     float corr_fc = 0.f;
     {
-        float osum = 0.f;
-        if (p.ao)
-            for (int k = 0; k < p.odots_n; ++k) osum += p.odots[row * p.odots_n + k];
         const float corr_o = sgn * osum;
         const float *ao = reinterpret_cast<const float *>(lds + kVAo) + 4 * g;
         float ssq = 0.f;
