@@ -36,6 +36,11 @@ __device__ __forceinline__ bf16x4 load_bf16x4(const __bf16 *p) { return *reinter
 
 __device__ __forceinline__ void store_bf16x8(__bf16 *p, bf16x8 v) { *reinterpret_cast<bf16x8 *>(p) = v; }
 
+// a streaming store (nt): output that no later work in the kernel reads, kept from displacing cached weights
+__device__ __forceinline__ void store_bf16x8_nt(__bf16 *p, bf16x8 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<bf16x8 *>(p));
+}
+
 __device__ __forceinline__ void store_bf16x4(__bf16 *p, bf16x4 v) { *reinterpret_cast<bf16x4 *>(p) = v; }
 
 __device__ __forceinline__ bf16x8 cat(bf16x4 lo, bf16x4 hi) {

@@ -193,7 +193,7 @@ __device__ __forceinline__ void qkv_phase(const QkvRowsArgs &p, char *lds, const
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
             const int c = it * 64 + lane, r = c >> 3, ch = c & 7;
-            store_bf16x8(dst + r * 64 + ch * 8,
+            store_bf16x8_nt(dst + r * 64 + ch * 8,
                          *reinterpret_cast<const bf16x8 *>(qk_stg + r * 128 + ((ch ^ (r & 7)) << 4)));
         }
     };
@@ -203,7 +203,7 @@ __device__ __forceinline__ void qkv_phase(const QkvRowsArgs &p, char *lds, const
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
             const int c = it * 512 + tid, d = c >> 4, ch = c & 15;
-            store_bf16x8(dst + (int64_t)d * T + 8 * ch,
+            store_bf16x8_nt(dst + (int64_t)d * T + 8 * ch,
                          *reinterpret_cast<const bf16x8 *>(vt_stg + d * 256 + ((ch ^ ((d >> 2) & 15)) << 4)));
         }
     };
