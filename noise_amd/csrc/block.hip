@@ -418,7 +418,7 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
             wave_lds_sync();
 #pragma unroll
             for (int it = 0; it < 16; ++it)
-                st4(p.xout + (row0 + it) * kModel + 256 * half + 4 * lane,
+                st4_nt(p.xout + (row0 + it) * kModel + 256 * half + 4 * lane,
                     *reinterpret_cast<const float4 *>(stg + it * 1024 + ((lane ^ it) << 4)));
             wave_lds_sync();  // the staging rows are rewritten next
         }
