@@ -352,8 +352,8 @@ __global__ __launch_bounds__(256) void qkv_shared_kernel(QkvSharedArgs p) {
                 hi[i] = (__bf16)(x2[i] * rstd);
             }
             __bf16 *o = p.out[mat] + hrow * 64;
-            store_bf16x8(o + 8 * part, lo);
-            store_bf16x8(o + 32 + 8 * part, hi);
+            store_bf16x8_nt(o + 8 * part, lo);
+            store_bf16x8_nt(o + 32 + 8 * part, hi);
         } else {
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void qkv_shared_kernel(QkvSharedArgs p) {
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
         const int c = it * 256 + tid, d = c >> 3, ch = c & 7;
-        store_bf16x8(ov + (int64_t)d * T + ch * 8, load_bf16x8(&vt[d][ch * 8]));
+        store_bf16x8_nt(ov + (int64_t)d * T + ch * 8, load_bf16x8(&vt[d][ch * 8]));
     }
 }
 
