@@ -93,7 +93,7 @@ def profiled_mfma_busy(kernel):
         return None
     for line in open(PROFILE):
         cells = [c.strip() for c in line.strip().strip('|').split('|')]
-        if len(cells) == 10 and cells[0] == name:
+        if len(cells) == 11 and cells[0] == name:
             try:
                 return float(cells[2])
             except ValueError:
