@@ -114,6 +114,80 @@ struct DotsArgs {
     float *out;
 };
 
+// The same dots when every member reads the same rows (x member stride 0): each (token, direction) pair once,
+// 32 tokens x 64 directions per workgroup (4 x 4 per thread, fp32 FMAs over k in order), x and the b rows
+// staged through LDS in k chunks of 32; each result goes to the dir_div members of its direction.
+constexpr int kSdT = 32, kSdD = 64, kSdK = 32, kSdThreads = 128;
+__global__ __launch_bounds__(kSdThreads) void shared_dots_kernel(DotsArgs p, int dirs) {
+    __shared__ float xs[kSdK][kSdT + 4];
+    __shared__ float bs[3][kSdK][kSdD + 4];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int t0 = blockIdx.x * kSdT, d0 = blockIdx.y * kSdD;
+    float acc[3][4][4];
+#pragma unroll
+    for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[k][i][j] = 0.f;
+    for (int n0 = 0; n0 < p.width; n0 += kSdK) {
+        {
+            // x: token tid / 4, k 8 (tid % 4) .. + 8 (zeros past the last token)
+            const int t = tid >> 2, k8 = (tid & 3) * 8;
+            bf16x8 v = bf16x8{};
+            if (t0 + t < p.tokens) v = load_bf16x8(p.x + (int64_t)(t0 + t) * p.xs_t + n0 + k8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) xs[k8 + e][t] = (float)v[e];
+        }
+#pragma unroll
+        for (int kk = 0; kk < 3; ++kk) {
+            if (kk < p.nk) {
+#pragma unroll
+                for (int it = 0; it < 4; ++it) {
+                    const int c = it * kSdThreads + tid, d = c >> 3, k4 = (c & 7) * 4;
+                    float4 v = float4{0.f, 0.f, 0.f, 0.f};
+                    if (d0 + d < dirs) v = ld4(p.b[kk] + (int64_t)(d0 + d) * p.b_stride[kk] + n0 + k4);
+                    bs[kk][k4][d] = v.x; bs[kk][k4 + 1][d] = v.y; bs[kk][k4 + 2][d] = v.z; bs[kk][k4 + 3][d] = v.w;
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll 4
+        for (int k = 0; k < kSdK; ++k) {
+            const float4 xv = *reinterpret_cast<const float4 *>(&xs[k][4 * ty]);
+#pragma unroll
+            for (int kk = 0; kk < 3; ++kk) {
+                if (kk < p.nk) {
+                    const float4 bv = *reinterpret_cast<const float4 *>(&bs[kk][k][4 * tx]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) acc[kk][i][j] += f4get(xv, i) * f4get(bv, j);
+                }
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int t = t0 + 4 * ty + i;
+        if (t >= p.tokens) continue;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int d = d0 + 4 * tx + j;
+            if (d >= dirs) continue;
+            for (int r = 0; r < p.dir_div; ++r) {
+                const int m = d * p.dir_div + r;
+                if (m >= p.members) break;
+                float *o = p.out + ((int64_t)m * p.tokens + t) * p.nk;
+#pragma unroll
+                for (int kk = 0; kk < 3; ++kk)
+                    if (kk < p.nk) o[kk] = acc[kk][i][j];
+            }
+        }
+    }
+}
+
 __global__ __launch_bounds__(256) void dots_kernel(DotsArgs p) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -248,7 +322,17 @@ extern "C" int noise_member_dots(const noise_population_t *pop, noise_view_t x, 
         if (k < nk) NOISE_CHECK_ARG(vecs[k].b && aligned(vecs[k].b, 16), "%s: b %d NULL or misaligned", fn, k);
     }
     a.out = out;
-    hipLaunchKernelGGL(dots_kernel, dim3(rows_grid(pop->members * pop->tokens)), dim3(256), 0, (hipStream_t)stream, a);
+    if (x.sm == 0 && pop->members > 1) {
+        // rows shared by every member: one dot per (token, direction)
+        for (int k = 0; k < nk; ++k)
+            NOISE_CHECK_ARG(vecs[k].b_stride % 4 == 0, "%s: b %d rows must be 16 B aligned", fn, k);
+        const int64_t dirs = (pop->members + pop->dir_div - 1) / pop->dir_div;
+        const dim3 grid((unsigned)((pop->tokens + kSdT - 1) / kSdT), (unsigned)((dirs + kSdD - 1) / kSdD));
+        hipLaunchKernelGGL(shared_dots_kernel, grid, dim3(kSdThreads), 0, (hipStream_t)stream, a, (int)dirs);
+    } else {
+        hipLaunchKernelGGL(dots_kernel, dim3(rows_grid(pop->members * pop->tokens)), dim3(256), 0, (hipStream_t)stream,
+                           a);
+    }
     return launch_status(fn);
 }
 

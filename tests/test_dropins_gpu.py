@@ -213,3 +213,40 @@ def test_config3_antithetic_linear_full_size():
         i = mbr // 2
         ref = base + sign[mbr] * xb[:, i, None] * a[i][None, :]
         assert ((y[mbr] - ref).abs().max() / scale).item() <= 2.0 ** -7, mbr
+
+
+@pytest.mark.parametrize('members,tokens,dir_div,nk,width', [(1024, 256, 2, 3, 512), (7, 100, 2, 2, 1024),
+                                                             (5, 64, 1, 1, 512)])
+def test_member_dots_shared_rows(members, tokens, dir_div, nk, width):
+    """noise_member_dots with rows every member shares (member stride 0: one dot per token and direction,
+    written to each member of the direction) against float64 sums and against the per-member kernel on the
+    same rows repeated per member; ragged token and direction counts included."""
+    import ctypes
+    from noise_amd import _lib
+    print(f'member dots: {members} members x {tokens} tokens, dir_div {dir_div}, {nk} vectors, width {width}',
+          flush=True)
+    g = torch.Generator().manual_seed(members + tokens)
+    dirs = -(-members // dir_div)
+    x = torch.randn(tokens, width, generator=g).bfloat16()
+    bs = [torch.randn(dirs, width + 4, generator=g)[:, :width] for _ in range(nk)]  # strided rows
+    sign = torch.ones(members)
+    xd, sd = x.to(DEV), sign.to(DEV)
+    bd = [b.to(DEV) for b in bs]
+    vecs = (_lib.Rank1 * 3)(*[_lib.Rank1(None, b.data_ptr(), 0, b.stride(0)) for b in bd])
+    pop = _lib.Population(members, tokens, sd.data_ptr(), dir_div, _lib.ROUNDING_FUSED)
+    stream = _lib.stream_ptr(DEV)
+    out = torch.full((members * tokens, nk), float('nan'), device=DEV)
+    _lib.call('noise_member_dots', ctypes.byref(pop), _lib.View(xd.data_ptr(), 0, width), width, vecs, nk,
+              out.data_ptr(), stream)
+    xr = xd.unsqueeze(0).expand(members, tokens, width).contiguous()
+    ref_k = torch.full_like(out, float('nan'))
+    _lib.call('noise_member_dots', ctypes.byref(pop), _lib.View(xr.data_ptr(), tokens * width, width), width, vecs, nk,
+              ref_k.data_ptr(), stream)
+    torch.cuda.synchronize()
+    got = out.cpu().view(members, tokens, nk)
+    mdir = torch.arange(members) // dir_div
+    ref = torch.stack([x.double() @ b.double().t() for b in bs], -1)[:, mdir].permute(1, 0, 2)  # [m, T, nk]
+    scale = ref.abs().max().item()
+    assert torch.isfinite(got).all()
+    assert (got.double() - ref).abs().max().item() <= 1e-5 * scale
+    assert (got - ref_k.cpu().view(members, tokens, nk)).abs().max().item() <= 1e-5 * scale
