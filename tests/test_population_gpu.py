@@ -249,3 +249,36 @@ def test_config4_full_population(params, head_scale):
               f'{f2:.3e} (x{f1 / f2:.2f}) when sigma halves', flush=True)
         assert 1.8 < f1 / f2 < 2.2
         assert 3.0 < s1 / s2 < 4.8   # quadratic; a sign mix-up within pairs would make it linear (x2)
+
+
+def test_fused_next_qkv_matches_separate_launches(params):
+    """population_forward with each block kernel forming the next block's gates and q/k/v (the default) against
+    the same forward with them launched on their own (fuse_qkv=False), every parameter perturbed (value
+    embeddings and their gates included, non-zero gates) and one token row per member. The two differ only in
+    the summation order of the q/k/v products (one bf16 ulp in ~0.01% of q, k, v), which later bf16 roundings
+    carry into most tokens: per-token losses differ by up to ~1e-2 with the head scaled x30, per-member means
+    by ~2e-4 (measured), as much as either path differs from the fp32 oracle. A wiring mistake (another
+    block's weights or noise, the gates) moves the means and the antithetic fitness by orders more."""
+    from noise_amd.eggroll import Weights, population_forward
+    P = dict(scaled_head(params, 30.0))
+    for i in (1, 3, 5, 7):
+        P[f'transformer.h.{i}.attn.ve_gate.weight'] = torch.randn(8, 32, generator=torch.Generator().manual_seed(i)) * 0.3
+    m, T = 4, 512
+    g = torch.Generator().manual_seed(7)
+    tables = make_noise(P, [n for n in P if 'wte' not in n and 'lambdas' not in n], m // 2, 4)
+    seq = torch.randint(0, 4096, (m, T + 1), generator=g)
+    sign = torch.tensor([0.01, -0.01]).repeat(m // 2).to(DEV)
+    W = Weights({k: v.to(DEV) for k, v in P.items()})
+    noise = split(P, tables, DEV)
+    x, y = seq[:, :-1].to(DEV), seq[:, 1:].to(DEV)
+    fused = population_forward(W, noise, sign, x, y, dir_div=2, per_token=True).clone()
+    separate = population_forward(W, noise, sign, x, y, dir_div=2, per_token=True, fuse_qkv=False).clone()
+    assert torch.isfinite(fused).all() and torch.isfinite(separate).all()
+    err = (fused - separate).abs().max().item()
+    merr = (fused.mean(1) - separate.mean(1)).abs().max().item()
+    print(f'fused vs separate q/k/v: max per-token loss difference {err:.2e}, per-member mean {merr:.2e}, '
+          f'tokens differing {(fused != separate).float().mean().item():.3f}, mean loss {fused.mean().item():.4f}')
+    fit = lambda L: L.mean(1)[1::2] - L.mean(1)[0::2]
+    assert err <= 5e-2
+    assert merr <= 5e-4
+    assert (fit(fused) - fit(separate)).abs().max().item() <= 5e-4
