@@ -36,6 +36,45 @@ def test_every_declared_symbol_has_a_ctypes_signature():
     assert not missing, missing
 
 
+def declarations():
+    """name -> [parameter type] for every entry point of include/noise_amd.h (parameter names dropped)."""
+    text = (ROOT / 'include' / 'noise_amd.h').read_text()
+    text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
+    out = {}
+    for name, args in re.findall(r'\b(noise_[a-z0-9_]+)\s*\(([^;()]*)\)\s*;', text, flags=re.S):
+        params = []
+        for a in args.split(','):
+            a = ' '.join(a.split())
+            if not a or a == 'void':
+                continue
+            m = re.match(r'(.*?)(\w+)(\s*\[\d*\])?$', a)
+            params.append(m.group(1).strip() + (' []' if m.group(3) else ''))
+        out[name] = params
+    return out
+
+
+def test_ctypes_signatures_match_the_header():
+    """Each entry point's ctypes argtypes agree with its C declaration parameter by parameter (a ctypes call
+    with a wrong argument list would not fail; it would pass the wrong bits)."""
+    import ctypes
+    import importlib.util
+    spec = importlib.util.spec_from_file_location('noise_abi', ROOT / 'noise_amd' / 'abi.py')
+    abi = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(abi)
+
+    def expected(t):
+        if '*' in t or t.endswith('[]') or t == 'noise_stream_t':
+            return ctypes.c_void_p
+        return {'noise_view_t': 'View', 'int64_t': ctypes.c_int64, 'uint64_t': ctypes.c_uint64, 'int': ctypes.c_int,
+                'float': ctypes.c_float}[t]
+
+    decl = declarations()
+    assert set(decl) == set(abi.SIGNATURES), set(decl) ^ set(abi.SIGNATURES)
+    for name, params in decl.items():
+        want = [expected(t) for t in params]
+        assert abi.SIGNATURES[name] == want, f'{name}: header {params}, ctypes {abi.SIGNATURES[name]}'
+
+
 def test_abi_version(lib):
     assert lib.noise_abi_version() == 2
 
