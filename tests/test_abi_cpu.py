@@ -75,6 +75,39 @@ def test_ctypes_signatures_match_the_header():
         assert abi.SIGNATURES[name] == want, f'{name}: header {params}, ctypes {abi.SIGNATURES[name]}'
 
 
+def test_struct_layouts_match_the_header(tmp_path):
+    """The ctypes mirrors of noise_view_t, noise_rank1_t, noise_population_t and noise_update_param_t have the
+    sizes and field offsets a C compiler gives the header's structs (gcc on include/noise_amd.h)."""
+    import ctypes
+    import shutil
+    import subprocess
+    import importlib.util
+    gcc = shutil.which('gcc')
+    if gcc is None:
+        pytest.skip('gcc not available')
+    spec = importlib.util.spec_from_file_location('noise_abi', ROOT / 'noise_amd' / 'abi.py')
+    abi = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(abi)
+    structs = {'noise_view_t': abi.View, 'noise_rank1_t': abi.Rank1, 'noise_population_t': abi.Population,
+               'noise_update_param_t': abi.UpdateParam}
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "noise_amd.h"', 'int main(void) {']
+    for c_name, py in structs.items():
+        lines.append(f'    printf("{c_name} size %zu\\n", sizeof({c_name}));')
+        for field, _ in py._fields_:
+            lines.append(f'    printf("{c_name} {field} %zu\\n", offsetof({c_name}, {field}));')
+    lines += ['    return 0;', '}']
+    src = tmp_path / 'layout.c'
+    src.write_text('\n'.join(lines) + '\n')
+    exe = tmp_path / 'layout'
+    subprocess.run([gcc, '-std=c99', '-I', str(ROOT / 'include'), str(src), '-o', str(exe)], check=True)
+    got = dict(line.rsplit(' ', 1) for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                               check=True).stdout.splitlines())
+    for c_name, py in structs.items():
+        assert int(got[f'{c_name} size']) == ctypes.sizeof(py), c_name
+        for field, _ in py._fields_:
+            assert int(got[f'{c_name} {field}']) == getattr(py, field).offset, f'{c_name}.{field}'
+
+
 def test_abi_version(lib):
     assert lib.noise_abi_version() == 2
 
