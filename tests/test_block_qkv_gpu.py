@@ -22,7 +22,7 @@ VOCAB = 300
 
 def _case(m, T, seed, qkv_noise, ve, ve_noise, per_member_idx, block_noise=True):
     g = torch.Generator().manual_seed(seed)
-    dirs = m // 2
+    dirs = -(-m // 2)
     u = lambda *s, scale: ((torch.rand(*s, generator=g) * 2 - 1) * scale)
     c = dict(m=m, T=T)
     c['y'] = torch.randn(m, T, 512, generator=g).bfloat16()
@@ -55,7 +55,7 @@ def _case(m, T, seed, qkv_noise, ve, ve_noise, per_member_idx, block_noise=True)
     idx = torch.randint(0, VOCAB, (m, T) if per_member_idx else (T,), generator=g)
     idx.view(-1)[7] = VOCAB + 5  # outside the table
     c['idx'] = idx
-    c['sign'] = torch.tensor([0.05, -0.05]).repeat(dirs)
+    c['sign'] = torch.tensor([0.05, -0.05]).repeat(dirs)[:m]
 
     def dev(v):
         if v is None:
@@ -165,10 +165,12 @@ CASES = {
 }
 
 
-@pytest.mark.parametrize('name', list(CASES))
-def test_block_qkv_matches_separate_launches(name):
-    print(f'block + next q/k/v: 4 members x 256 tokens, case {name}', flush=True)
-    c = _case(4, 256, 11, **CASES[name])
+@pytest.mark.parametrize('name,m,T', [(n, 4, 256) for n in CASES] + [('ve-noisy', 3, 256)],
+                         ids=list(CASES) + ['ve-noisy-3-members'])
+def test_block_qkv_matches_separate_launches(name, m, T):
+    """Every case at 4 members x 256 tokens, and an odd member count (the last direction has one member)."""
+    print(f'block + next q/k/v: {m} members x {T} tokens, case {name}', flush=True)
+    c = _case(m, T, 11, **CASES[name])
     xo_s, qkv_s = _separate(c)
     status, xo_f, qkv_f = _fused(c)
     assert status == 0
