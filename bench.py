@@ -199,7 +199,7 @@ def main():
         print(json.dumps(dict(copy_bytes=2 ** 30)))
         return
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
-        print('bench.py measures one GPU: this build has no multi-GPU path (members would shard across GPUs with '
+        print('bench.py measures one GPU: the library has no multi-GPU path (members would shard across GPUs with '
               'one all_gather of the per-member losses). Run with --gpus 1.', file=sys.stderr)
         sys.exit(2)
 

@@ -653,7 +653,7 @@ class Eggroll:
         """eggroll.py:131-168 on one GPU: evaluate the population, rebuild the update, step the optimizer;
         returns the mean loss."""
         if self.world != 1:
-            raise NotImplementedError('Eggroll.step gathers losses across ranks in the reference; this build '
+            raise NotImplementedError('Eggroll.step gathers losses across ranks in the reference; this library '
                                       'runs one GPU (call population() per rank and gather the losses first)')
         losses = self.population(step, x, y, chunk=chunk)
         grads = self.update(losses, self.offsets(step), chunk=update_chunk)

@@ -1,6 +1,6 @@
 """ORACLE -- test infrastructure only.
 
-CPU restatements of the reference's population-forward path, used as the checker by tests/,
+CPU restatements of the reference's population-forward path, used to check the product by tests/,
 __graft_entry__.smoke() and bench.py's cpu_baseline leg. The product (noise_amd/) never imports, links or
 runs anything here; there is no CPU fallback in the product.
 
