@@ -1,6 +1,6 @@
 /*
  * ORACLE -- test infrastructure only. Nothing in the product (noise_amd/) may link, load or call this
- * file; tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it as the checker.
+ * file; tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it to check the product.
  *
  * CPU restatement of the noise that the reference draws from torch's device generator:
  *   - eggroll.py:114   buffer = torch.randn(2**28, generator=Generator('cuda').manual_seed(SEED))
