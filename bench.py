@@ -127,10 +127,24 @@ def host_cpu():
     return info
 
 
+CPU_RUNS = 5  # timed runs of each CPU baseline after one warmup run; the median is reported
+
+
+def _median_time(fn, runs=CPU_RUNS):
+    """One warmup call, then the median wall time of `runs` calls (and the last call's result)."""
+    out = fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        out = fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2], out
+
+
 def cpu_forward_config1(threads=None):
     """The reference's CPU plumbing case: the fixed model's fp32 forward + mean next-token CE (the oracle's
     restatement of utils/model.py:193-209) on a batch of 4 x 2048 tokens ~ U[0, 4096) from a CPU generator
-    seeded 0, shifted by one (eggroll.py:217-229). One warmup, then the median of 3 runs."""
+    seeded 0, shifted by one (eggroll.py:217-229). One warmup, then the median of 5 runs."""
     import torch
     from noise_amd.model import make_model
     from oracle import model as om
@@ -140,19 +154,15 @@ def cpu_forward_config1(threads=None):
     batch = torch.randint(0, 4096, (4, TOKENS + 1), generator=torch.Generator().manual_seed(0))
     x, y = batch[:, :-1], batch[:, 1:]
     with torch.no_grad():
-        loss = om.gpt_forward(P, x, y)
-        times = []
-        for _ in range(3):
-            t0 = time.perf_counter()
-            loss = om.gpt_forward(P, x, y)
-            times.append(time.perf_counter() - t0)
-    dt = sorted(times)[1]
+        dt, loss = _median_time(lambda: om.gpt_forward(P, x, y))
     return dict(value=round(x.numel() / dt, 1), unit='tokens/s', loss=round(float(loss), 6), seconds=round(dt, 3),
-                threads=torch.get_num_threads(), batch='4 x 2048 tokens ~ U[0, 4096), seed 0')
+                threads=torch.get_num_threads(), runs=f'1 warmup + median of {CPU_RUNS}',
+                batch='4 x 2048 tokens ~ U[0, 4096), seed 0')
 
 
 def cpu_baseline(P, tables, x, y, members):
-    """The oracle forward (fp32, torch CPU) on `members` members of the same workload."""
+    """The oracle forward (fp32, torch CPU) on `members` members of the same workload: one warmup run, then
+    the median of 5 timed runs."""
     import torch
     from oracle import model as om
     threads = torch.get_num_threads()
@@ -161,13 +171,12 @@ def cpu_baseline(P, tables, x, y, members):
         noise[n] = (a[:members // 2].cpu().repeat_interleave(2, 0), b[:members // 2].cpu().repeat_interleave(2, 0))
     sign = torch.tensor([SIGMA, -SIGMA]).repeat(members // 2)
     Pc = {k: v.cpu().float() for k, v in P.items()}
-    om.population_loss(Pc, {n: (a[:2], b[:2]) for n, (a, b) in noise.items()}, sign[:2], x.cpu()[:256], y.cpu()[:256])
-    t0 = time.perf_counter()
-    losses = om.population_loss(Pc, noise, sign, x.cpu(), y.cpu(), members_per_chunk=2)
-    dt = time.perf_counter() - t0
+    with torch.no_grad():
+        dt, losses = _median_time(lambda: om.population_loss(Pc, noise, sign, x.cpu(), y.cpu(), members_per_chunk=2))
     return dict(value=members * x.numel() / dt, unit='member-tokens/s', cores=threads, kind='port',
-                sample=f'{members} members x {x.numel()} tokens, fp32 oracle forward (oracle/model.py), '
-                       f'{dt:.1f} s on {threads} threads', host=host_cpu()), losses
+                sample=f'{members} members x {x.numel()} tokens, fp32 oracle forward (oracle/model.py), one warmup '
+                       f'run then the median of {CPU_RUNS} runs ({dt:.1f} s each) on {threads} threads',
+                host=host_cpu()), losses
 
 
 def main():
@@ -183,8 +192,8 @@ def main():
     ap.add_argument('--update-chunk', type=int, default=8192, help='update workload: directions per GEMM pass')
     ap.add_argument('--members', type=int, default=None,
                     help='population size (default 1024; 2048 for orthogonal-fp32-head)')
-    ap.add_argument('--cpu-members', type=int, default=32,
-                    help='members of the CPU-baseline sample, about 15 s of CPU work (0: skip)')
+    ap.add_argument('--cpu-members', type=int, default=8,
+                    help='members of the CPU-baseline sample, timed 6 times: about 20 s of CPU work (0: skip)')
     ap.add_argument('--profile-steps', type=int, default=1, help='extra timed steps with per-kernel events')
     ap.add_argument('--copy-calibration', action='store_true',
                     help='only copy 1 GiB device to device (scale reference for rocprofv3 FETCH_SIZE / WRITE_SIZE)')

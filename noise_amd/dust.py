@@ -4,14 +4,18 @@
   block_forward(x, w, ve, cos, sin, window, o, attn, fc, mlp)   run.py:102-117
   rerun(dust, n, entry, jitter)             run.py:256-279 (DUST.rerun)
   draw_errors(errors, reward, a, sigma)     run.py:351-355 (direct_errors' estimate update)
+  direct_errors(dust, sites, draws, sigma, entry, gamma, retrieved)   run.py:332-378 (DUST.direct_errors)
+  chunk_size(draws, cap), reward_to_go(reward, gamma)                 run.py:76-86
   coordinate_differences(raw, y, sigma)     run.py:121-137
   head_error(logits, y, vocab, sigma)       run.py:380-389
   hadamard(d, device, dtype)                run.py:143-152
   OrthogonalDraws                           run.py:218-238 (signs, orthogonal_noise)
 """
 import ctypes
+import math
 
 import torch
+import torch.nn.functional as F
 
 from . import _lib
 from .noise import DeviceGenerator
@@ -20,6 +24,12 @@ F32, BF16 = torch.float32, torch.bfloat16
 
 
 def head_loss(x, weight, targets, vocab):
+    """run.py:89-94 `head_loss(x, weight, targets, vocab)` through the registered op torch.ops.noise_amd.head_loss
+    (the reference compiles it, run.py:89): per-token soft-capped cross-entropy of the fp32 head, [numel(targets)]."""
+    return torch.ops.noise_amd.head_loss(x, weight, targets, int(vocab))
+
+
+def head_loss_eager(x, weight, targets, vocab):
     """Final norm, fp32 head, soft cap and per-token cross-entropy (ignore_index -1), reduction none.
 
     x [..., T, 512] fp32, weight [V, 512], targets [..., T] -> [numel(targets)]. The reference runs the
@@ -197,5 +207,97 @@ def rerun(dust, n, entry, jitter):
         ve = None if ve is None else ve.detach().repeat(n, 1, 1)
         sites = {key: jitter.get(site.format(i)) for key, site in SITES.items()} if i == entry else {}
         x = block_forward_eager(x, dust.weights[i], ve, cos, sin, model.window_sizes[i][0], **sites)
-    loss = head_loss(x, model.lm_head.weight.detach().float(), dust.y.repeat(n, 1), model.config.vocab_size)
+    loss = head_loss_eager(x, model.lm_head.weight.detach().float(), dust.y.repeat(n, 1), model.config.vocab_size)
     return loss.view(n, b, T)
+
+
+def chunk_size(draws, cap):
+    """run.py:76-78: the draws per rerun, the largest divisor of `draws` that is at most `cap`."""
+    if draws < 1 or cap < 1:
+        raise ValueError(f'chunk_size needs positive draws and cap, not {draws} and {cap}')
+    return max(n for n in range(1, min(cap, draws) + 1) if draws % n == 0)
+
+
+def reward_to_go(reward, gamma):
+    """run.py:81-86: each token's reward plus the rewards of the later tokens of its sequence, the token k places
+    later weighted gamma^k, over the lags whose weight reaches 1e-6. reward [..., t] (the last dim is the
+    sequence). A correlation with the weight row gamma^0 .. gamma^(lags - 1) over the right-padded rows."""
+    lags = math.ceil(math.log(1e-6) / math.log(gamma))
+    weight = torch.pow(torch.tensor(gamma, dtype=reward.dtype, device=reward.device),
+                       torch.arange(lags, device=reward.device, dtype=reward.dtype))
+    rows = reward.reshape(-1, 1, reward.shape[-1])
+    return F.conv1d(F.pad(rows, (0, lags - 1)), weight.view(1, 1, lags)).view(reward.shape)
+
+
+def _site_width(dust, site):
+    """run.py:338: an attention-output site o@i is n_embd wide; any other site as wide as its captured output."""
+    return dust.model.config.n_embd if site.startswith('o@') else dust.outputs[site].shape[-1]
+
+
+def direct_errors(dust, sites, draws, sigma, entry=None, gamma=0.0, retrieved=None):
+    """DUST.direct_errors (run.py:332-378) over this library's rerun: each site's output error per token,
+    estimated from n orthogonal draws per rerun (n = chunk_size(draws, dust.recipe.nrep)), returned as
+    {site: fp32 [batch, length, width]}.
+
+    Per chunk of n draws: the draws a of every site in the draw dtype (dust.orthogonal_noise, run.py:223-238;
+    an mlp.c_fc site keeps only its live units, those whose captured output is > 0), the rerun of n jittered
+    copies of the batch from block `entry` with sigma * a added at every site (rerun, run.py:256-279), the
+    reward clean_loss - perturbed loss per draw and token, centred over the chunk's draws when n > 1, discounted
+    over later tokens when gamma > 0 (reward_to_go), corrected by the priors' predicted loss drop when
+    `retrieved` holds memory retrievals (prior = alpha[site] * retrieval, masked like the draws), and folded
+    into the estimates by noise_draw_errors (bf16 reward times the draws, summed over the chunk's draws, / sigma).
+    Finally each estimate is divided by `draws` and the prior, scaled by the centring's 1 - 1/n, added back.
+
+    `dust` carries the reference DUST's state: model, batch, length, outputs, blocks, x0, y, weights, clean_loss
+    [batch, length] fp32, dtype (the draws' dtype: bf16 on a GPU), recipe.nrep, alpha, estimates, fits,
+    prior_sites and orthogonal_noise(site, draws, chunk, n, b, t, d). Like the reference, it records the
+    estimates of prior sites in dust.estimates and, per retrieved site, the least-squares fit statistics
+    (<retrieval, unshrunk estimate>, |retrieval|^2) in dust.fits."""
+    retrieved = retrieved or {}
+    dtype = dust.dtype
+    priors = {s: dust.alpha[s] * r for s, r in retrieved.items() if s in dust.alpha}
+    n, b, t = chunk_size(draws, dust.recipe.nrep), dust.batch, dust.length
+    dev = dust.clean_loss.device
+    width = {s: _site_width(dust, s) for s in sites}
+    errors = {s: torch.zeros(b, t, width[s], dtype=F32, device=dev) for s in sites}
+    # an mlp.c_fc site is jittered at its live units only (ReLU is flat below 0); its prior is masked alike
+    live = {s: (dust.outputs[s] > 0).to(dtype) for s in sites if s.endswith('mlp.c_fc')}
+    for s, mask in live.items():
+        if s in priors:
+            priors[s] = priors[s] * mask.float()
+    mu = {s: p.to(dtype).float() for s, p in priors.items()}  # the priors as the draws' bf16 products see them
+
+    for chunk in range(draws // n):
+        a = {}
+        for s in sites:
+            draw = dust.orthogonal_noise(s, draws, chunk, n, b, t, width[s])
+            if s in live:
+                draw = draw * live[s]
+            a[s] = draw.reshape(n * b, t, width[s])
+        loss = rerun(dust, n, entry, {s: sigma * draw for s, draw in a.items()})
+        reward = dust.clean_loss.unsqueeze(0) - loss
+        if n > 1:
+            reward = reward - reward.mean(0, keepdim=True)
+        if gamma:
+            reward = reward_to_go(reward, gamma)
+        if priors:
+            # the loss drop the priors predict, sigma a.mu summed over sites: each site's product rounded to the
+            # draw dtype, the sum over sites in it too, then fp32 (run.py:359-363)
+            predicted = None
+            for s, m in mu.items():
+                dot = (a[s].view(n, b, t, -1).float() * m).sum(-1).to(dtype)
+                predicted = dot if predicted is None else predicted + dot
+            predicted = sigma * predicted.float()
+            reward = reward + (predicted - predicted.mean(0, keepdim=True) if n > 1 else predicted)
+        for s in sites:
+            draw_errors(errors[s], reward, a[s], sigma)
+
+    kept = 1 - 1 / n if n > 1 else 1.0
+    out = {}
+    for s, e in errors.items():
+        out[s] = e / draws + kept * priors[s] if s in priors else e / draws
+    dust.estimates.update({s: e for s, e in out.items() if s in dust.prior_sites})
+    for s, r in retrieved.items():
+        unshrunk = out[s] / kept
+        dust.fits[s] = torch.stack([(r * unshrunk).sum(), (r * r).sum()])
+    return out

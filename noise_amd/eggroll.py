@@ -121,7 +121,10 @@ class Weights:
         self.device, self.n_layer = dev, n_layer
         g = lambda n: p[n].detach().to(dev)
         bf = lambda n: g(n).to(BF16).contiguous()
-        self.wte = g('transformer.wte.weight').to(F32).contiguous()
+        # fp32 tables and scalars are copied even when the parameter is already fp32 on the device: a Weights
+        # is a snapshot of one update's parameters, never a view of the live ones
+        snap = lambda n: g(n).to(F32, copy=True).contiguous()
+        self.wte = snap('transformer.wte.weight')
         self.lm_head = bf('lm_head.weight')
         self.fp32_head = fp32_head
         if fp32_head:
@@ -131,8 +134,8 @@ class Weights:
                       _lib.stream_ptr(dev))
         # the mixing scalars stay on the device: the kernels read them there (a host copy would wait for the
         # stream at every update)
-        self.resid_lambdas = g('resid_lambdas').to(F32).contiguous()
-        self.x0_lambdas = g('x0_lambdas').to(F32).contiguous()
+        self.resid_lambdas = snap('resid_lambdas')
+        self.x0_lambdas = snap('x0_lambdas')
         self.blocks = []
         for i in range(n_layer):
             pre = f'transformer.h.{i}.'
@@ -151,7 +154,7 @@ class Weights:
             if has_ve(i, n_layer):
                 # the gate's product runs under autocast: its weights enter rounded to bf16
                 blk['gate'] = bf(pre + 'attn.ve_gate.weight').to(F32).contiguous()
-                blk['ve'] = g(f'value_embeds.{i}.weight').to(F32).contiguous()
+                blk['ve'] = snap(f'value_embeds.{i}.weight')
             self.blocks.append(blk)
         self.windows = window_sizes(n_layer)
 

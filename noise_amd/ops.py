@@ -16,7 +16,7 @@ Ops take flat tensor lists where the reference passes dicts: population_loss's p
 become one list per field in the order of `names` (newline-separated parameter names), with the noise of
 a 1-D parameter (the mixing scalars' eps) in noise_a and None in noise_b; block_forward's weight dict is
 the list (q, k, v, gate or None, proj, fc, out). The reference-signature wrappers that pack them are
-noise_amd.eggroll.population_loss and noise_amd.dust.block_forward / coordinate_differences.
+noise_amd.eggroll.population_loss and noise_amd.dust.head_loss / block_forward / coordinate_differences.
 """
 from typing import List, Optional
 
@@ -83,7 +83,7 @@ def _population_loss_fake(names, params, noise_a, noise_b, sign, idx, targets, n
 
 @custom_op('noise_amd::head_loss', mutates_args=())
 def head_loss(x: Tensor, weight: Tensor, targets: Tensor, vocab: int) -> Tensor:
-    return dust.head_loss(x, weight, targets, vocab)
+    return dust.head_loss_eager(x, weight, targets, vocab)
 
 
 @head_loss.register_fake

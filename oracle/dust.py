@@ -1,9 +1,12 @@
-"""ORACLE (test infrastructure only): DUST's head error, block_forward, capture cache and rerun on the CPU.
+"""ORACLE (test infrastructure only): DUST's head error, block_forward, capture cache, rerun and direct errors
+on the CPU.
 
 Restates train/val/run.py:121-137 (coordinate_differences) and run.py:380-389 (head_error) in float64
 numpy: z = 15 tanh(raw / 15), the moved logits z' = cap(raw +- sigma), w = softmax(z), and
     change_j = log1p(w_j expm1(up_j - z_j)) - log1p(w_j expm1(down_j - z_j)) - [j = y] (up_j - down_j)
-divided by 2 sigma, zero where y < 0.
+divided by 2 sigma, zero where y < 0. run.py:102-117 (block_forward), 247-254 (capture), 256-279 (rerun) in fp32
+torch CPU ops; run.py:76-86 (chunk_size, reward_to_go) and 332-378 (direct_errors) in float64 numpy with the
+reference's bf16 roundings (the reward and each chunk's estimate sum, the priors' predicted drop).
 """
 import numpy as np
 
@@ -31,10 +34,12 @@ def head_error(logits, y, vocab, sigma=0.1):
     return out
 
 
-def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=None):
+def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=None, taps=None):
     """run.py:102-117 in the dtype of x (fp32 or fp64 torch, CPU): Block.forward with the jitter added at o
     (attention output), attn (c_proj product), fc (c_fc product, before ReLU^2) and mlp (mlp.c_proj product).
-    w: q, k, v, gate (or None), proj, fc, out; cos, sin [T, 32]."""
+    w: q, k, v, gate (or None), proj, fc, out; cos, sin [T, 32]. taps: a dict that, when given, receives the
+    three products 'attn' (attn.c_proj), 'fc' (mlp.c_fc) and 'mlp' (mlp.c_proj) as the module outputs a
+    forward hook sees (run.py:196-200)."""
     import torch
     import torch.nn.functional as F
     from .model import norm, apply_rotary_emb, attention, N_HEAD, HEAD_DIM
@@ -49,9 +54,13 @@ def block_forward(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=No
         v = v + gate.unsqueeze(-1) * ve.to(dt).view(B, T, N_HEAD, HEAD_DIM)
     q, k = norm(apply_rotary_emb(q, cos.to(dt), sin.to(dt))), norm(apply_rotary_emb(k, cos.to(dt), sin.to(dt)))
     y = add(attention(q, k, v, window).to(dt).reshape(B, T, C), o)
-    x = x + add(y @ W['proj'].t(), attn)
-    hidden = add(norm(x) @ W['fc'].t(), fc)
-    return x + add(F.relu(hidden).square() @ W['out'].t(), mlp)
+    proj = y @ W['proj'].t()
+    x = x + add(proj, attn)
+    hidden = norm(x) @ W['fc'].t()
+    out = F.relu(add(hidden, fc)).square() @ W['out'].t()
+    if taps is not None:
+        taps.update(attn=proj, fc=hidden, mlp=out)
+    return x + add(out, mlp)
 
 
 def draw_errors(errors, reward, a, sigma):
@@ -66,8 +75,9 @@ def draw_errors(errors, reward, a, sigma):
 
 def capture(P, idx):
     """What DUST.capture (run.py:247-254) caches from the clean forward of GPT.forward (utils/model.py:193-209),
-    in fp32 on the CPU: the embedding output, every block's input (after its mixing), x0 = norm(embedding) and
-    the value-embedding outputs. idx [b, T]."""
+    in fp32 on the CPU: the embedding output, every block's input (after its mixing), x0 = norm(embedding), the
+    value-embedding outputs and each block's attn.c_proj, mlp.c_fc and mlp.c_proj outputs (by module name, as
+    the output hooks record them). idx [b, T]."""
     from .model import norm, has_ve, rotary_tables, window_sizes, N_LAYER
     T = idx.shape[1]
     cos, sin = rotary_tables(T)
@@ -82,7 +92,11 @@ def capture(P, idx):
         ve = P[f'value_embeds.{i}.weight'][idx].float() if has_ve(i) else None
         if ve is not None:
             outputs[f'value_embeds.{i}'] = ve
-        x = block_forward(x, block_weights(P, i), ve, cos, sin, wins[i])
+        taps = {}
+        x = block_forward(x, block_weights(P, i), ve, cos, sin, wins[i], taps=taps)
+        for key, site in SITES.items():
+            if key in taps:
+                outputs[site.format(i)] = taps[key]
     return dict(outputs=outputs, blocks=blocks, x0=x0)
 
 
@@ -118,3 +132,77 @@ def rerun(P, cache, y, n, entry, jitter):
         x = block_forward(x, block_weights(P, i), None if ve is None else ve.repeat(n, 1, 1), cos, sin, wins[i],
                           **sites)
     return head_loss(x, P['lm_head.weight'], y.repeat(n, 1)).view(n, b, T)
+
+
+def chunk_size(draws, cap):
+    """run.py:76-78: largest divisor of draws that does not exceed cap."""
+    n = min(cap, draws)
+    while draws % n:
+        n -= 1
+    return n
+
+
+def reward_to_go(reward, gamma):
+    """run.py:81-86 by its definition: out[..., i] = sum_{k < lags, i + k < t} gamma^k reward[..., i + k],
+    lags = ceil(log(1e-6) / log(gamma)); float64."""
+    r = np.asarray(reward, dtype=np.float64)
+    lags = int(np.ceil(np.log(1e-6) / np.log(gamma)))
+    t = r.shape[-1]
+    out = np.zeros_like(r)
+    for k in range(min(lags, t)):
+        out[..., :t - k] += gamma ** k * r[..., k:]
+    return out
+
+
+def _bf16(v):
+    import torch
+    return torch.as_tensor(np.asarray(v, dtype=np.float32)).bfloat16().double().numpy()
+
+
+def direct_errors(draw, rerun_fn, clean_loss, live, sites, widths, draws, sigma, nrep, gamma=0.0, priors=None):
+    """DUST.direct_errors (run.py:332-378) in float64 with the reference's bf16 roundings.
+
+    draw(site, draws, chunk, n, b, t, d) -> [n, b, t, d] of +-1 (OrthogonalDrawsOracle); rerun_fn(n, jitter) ->
+    per-token losses [n, b, t] with jitter site -> bf16 torch tensor [n * b, t, d] holding bf16(sigma) * draw;
+    clean_loss [b, t]; live: site -> 0/1 mask [b, t, d] (the mlp.c_fc sites); widths: site -> d; priors: site ->
+    alpha * retrieval [b, t, d] or None.
+
+    Per chunk of n = chunk_size(draws, nrep) draws: reward = clean_loss - loss, centred over the draws when n > 1,
+    discounted when gamma > 0, plus sigma * sum_s bf16(a_s . bf16(prior_s)) (bf16 sums over sites; centred when
+    n > 1), then each site's estimate -= bf16(sum_i bf16(reward_i) a_i) / sigma. Returns (estimates, record):
+    estimates site -> error / draws + (1 - 1/n) prior, record per chunk the rewards, predicted drops and the
+    chunk sums (for rounding bounds)."""
+    import torch
+    priors = {s: np.asarray(p, dtype=np.float64) * live.get(s, 1.0) for s, p in (priors or {}).items()}
+    clean_loss = np.asarray(clean_loss, dtype=np.float64)
+    b, t = clean_loss.shape
+    n = chunk_size(draws, nrep)
+    est = {s: np.zeros((b, t, widths[s])) for s in sites}
+    record = []
+    sig_bf = float(torch.tensor(sigma).bfloat16())   # the jitter sigma * a rounds sigma to bf16
+    for chunk in range(draws // n):
+        a = {s: np.asarray(draw(s, draws, chunk, n, b, t, widths[s]), dtype=np.float64) * live.get(s, 1.0)
+             for s in sites}
+        jitter = {s: torch.from_numpy((sig_bf * v).reshape(n * b, t, -1).astype(np.float32)).bfloat16()
+                  for s, v in a.items()}
+        loss = np.asarray(rerun_fn(n, jitter), dtype=np.float64)
+        reward = clean_loss[None] - loss
+        if n > 1:
+            reward = reward - reward.mean(0, keepdims=True)
+        if gamma:
+            reward = reward_to_go(reward, gamma)
+        predicted = None
+        if priors:
+            total = None
+            for s, p in priors.items():
+                dot = _bf16(np.einsum('nbtd,btd->nbt', a[s], _bf16(p)))
+                total = dot if total is None else _bf16(total + dot)
+            predicted = sigma * total
+            reward = reward + (predicted - predicted.mean(0, keepdims=True) if n > 1 else predicted)
+        sums = {}
+        for s in sites:
+            sums[s] = _bf16(np.einsum('nbt,nbtd->btd', _bf16(reward), a[s]))
+            est[s] = est[s] - sums[s] / sigma
+        record.append(dict(loss=loss, reward=reward, predicted=predicted, sums=sums, a=a))
+    kept = 1 - 1 / n if n > 1 else 1.0
+    return {s: e / draws + kept * priors.get(s, 0.0) for s, e in est.items()}, record

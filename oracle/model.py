@@ -167,32 +167,43 @@ def lowrank_embed(weight, a, b, idx, sign):
     return weight[idx].unsqueeze(0) + sign[:, None, None] * a[:, idx].unsqueeze(-1) * b[:, None, :]
 
 
-def population_loss(P, noise, sign, idx, targets, members_per_chunk=None):
+class CpuOps:
+    """The perturbed-linear, perturbed-embedding and attention ops population_loss composes; these are the
+    oracle's own fp32 CPU forms. A caller may pass another set with the same signatures (the drop-ins), so the
+    composition below doubles as a caller of the reference's shape: every weight matrix through lowrank, every
+    table through lowrank_embed, attention on [B, T, H, D] views."""
+    lowrank = staticmethod(lowrank)
+    lowrank_embed = staticmethod(lowrank_embed)
+    attention = staticmethod(attention)
+
+
+def population_loss(P, noise, sign, idx, targets, members_per_chunk=None, ops=CpuOps):
     """eggroll.py:66-103 in fp32: mean CE [m] of m perturbed models on one sequence.
 
     noise: name -> (a [m, out], b [m, in]) for perturbed matrices/embeddings, or eps [m, L] for the mixing
-    scalars; names absent from `noise` are unperturbed. members_per_chunk splits m to bound memory."""
+    scalars; names absent from `noise` are unperturbed. members_per_chunk splits m to bound memory. ops: the
+    lowrank / lowrank_embed / attention implementations (CpuOps: the oracle's)."""
     m = sign.shape[0]
     if members_per_chunk and m > members_per_chunk:
         parts = []
         for c in range(0, m, members_per_chunk):
             sl = slice(c, c + members_per_chunk)
             sub = {n: (tuple(t[sl] for t in v) if isinstance(v, tuple) else v[sl]) for n, v in noise.items()}
-            parts.append(population_loss(P, sub, sign[sl], idx, targets))
+            parts.append(population_loss(P, sub, sign[sl], idx, targets, ops=ops))
         return torch.cat(parts)
     length = idx.shape[0]
-    cos, sin = rotary_tables(length)
+    cos, sin = (t.to(idx.device) for t in rotary_tables(length))
     windows = window_sizes()
     s = sign[:, None, None]
 
     def lin(name, inp):
         if name in noise:
-            return lowrank(inp, P[name], *noise[name], sign)
+            return ops.lowrank(inp, P[name], *noise[name], sign)
         return inp @ P[name].t()
 
     def emb(name):
         if name in noise:
-            return lowrank_embed(P[name].float(), *noise[name], idx, sign)
+            return ops.lowrank_embed(P[name].float(), *noise[name], idx, sign)
         return P[name][idx].float().unsqueeze(0).expand(m, length, -1)
 
     def scalar(name, i):
@@ -214,7 +225,7 @@ def population_loss(P, noise, sign, idx, targets, members_per_chunk=None):
             gate = 2 * torch.sigmoid(lin(pre + 'attn.ve_gate.weight', h[..., :32]))
             v = v + gate.unsqueeze(-1) * ve
         q, k = norm(apply_rotary_emb(q, cos, sin)), norm(apply_rotary_emb(k, cos, sin))
-        y = attention(q, k, v, windows[i]).reshape(m, length, -1)
+        y = ops.attention(q, k, v, windows[i]).reshape(m, length, -1)
         x = x + lin(pre + 'attn.c_proj.weight', y)
         x = x + lin(pre + 'mlp.c_proj.weight', F.relu(lin(pre + 'mlp.c_fc.weight', norm(x))).square())
     h = norm(x)

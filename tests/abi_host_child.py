@@ -58,6 +58,12 @@ assert 'directions' in message()  # dots_stride 1 < 2 directions: the %lld messa
 assert lib.noise_attention_fwd(16, 16, 16, 16, 1, 1, 64, 32, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 0, 10, 0.1, None, 0, 1,
                                None, None) == -1
 assert 'head_dim' in message()
+# the allocation-free DUST block: a shape beyond its static scratch is rejected before any HIP call
+cap, need = lib.noise_dust_block_static_max_bytes(), lib.noise_dust_block_workspace_bytes(64, 2048, 1)
+assert need > cap
+w7 = (ctypes.c_void_p * 7)(*([16] * 7))
+assert lib.noise_dust_block_static(16, 16, 64, 2048, w7, 16, 16, 16, 1024, None, None, None, None, None) == -1
+assert 'static array holds' in message()
 print('targeted invalid arguments: rejected', flush=True)
 
 # concurrent calls: each thread's message is its own call's

@@ -1,14 +1,14 @@
 """The drop-in boundary at the reference's own call sites, on the GPU.
 
-- EGGROLL's chunk loop (eggroll.py:133-146) as the reference writes it: per-member noise after
-  repeat_interleave(2), all 60 parameters perturbed, the population loss behind torch.compile and autocast
-  (eggroll.py:115, 144). Run twice: with the fused population_loss drop-in, and with the reference's
-  population_loss body (eggroll.py:66-103) composed from the lowrank / lowrank_embed / attention drop-ins,
-  so every linear call site -- the value-embedding gate's lowrank on h[..., :32] included -- goes through
-  this library. Both stay within 1e-3 of the fp32 oracle for every member.
+- A compiled caller of the reference's shape (eggroll.py:115, 133-146): a population evaluated chunk by chunk
+  under torch.compile and bf16 autocast, per-member noise of all 60 parameters, member g on direction
+  (g mod 2P) // 2 with sign +-sigma. Run twice: with the fused population_loss drop-in, and with a population
+  forward composed from the lowrank / lowrank_embed / attention drop-ins (the oracle's composition, given the
+  drop-ins as its ops), so every linear call site -- the value-embedding gate's lowrank on h[..., :32]
+  included -- goes through this library. Both stay within 1e-3 of the fp32 oracle for every member.
 - Eggroll.population's member -> direction, sign and sequence mapping (eggroll.py:134-146) with 8
-  sequences, three chunks per rank and two rank slices, against the oracle on noise gathered by the
-  reference's formula.
+  sequences, three chunks per rank and two rank slices, against the oracle on noise gathered per member
+  from the mapping's closed form.
 - lowrank in autocast's form for every shape (eggroll.py:56-58 under eggroll.py:144), block_forward and
   coordinate_differences behind torch.compile (run.py:102, 120), token ids outside the vocabulary, and
   the device make_model's bf16 embedding storage (utils/model.py:171-175).
@@ -51,76 +51,61 @@ def _cpu_noise(noise):
     return {n: (tuple(t.cpu() for t in v) if isinstance(v, tuple) else v.cpu()) for n, v in noise.items()}
 
 
-def _reference_population_loss(model, p, noise, sign, idx, targets):
-    """eggroll.py:66-103 line by line, with its lowrank, lowrank_embed and attention calls going to this
-    library's drop-ins (torch.ops.noise_amd.*) and the elementwise steps left to torch, as in the reference."""
-    from noise_amd.eggroll import lowrank, lowrank_embed
-    from noise_amd.model import has_ve, rotary_tables
-    cfg = model.config
-    heads, dim = cfg.n_head, cfg.n_embd // cfg.n_head
-    m, length = sign.shape[0], idx.shape[0]
-    cos, sin = (t[None, :, None, :].to(idx.device) for t in rotary_tables(length))
-    s = sign[:, None, None]
+class DropIns:
+    """The library's drop-ins in the roles the composed population forward gives its ops (oracle/model.py
+    population_loss takes lowrank, lowrank_embed and attention as arguments): with these, every linear call
+    site of a population forward -- the value-embedding gate's lowrank on h[..., :32] included -- and every
+    attention runs through libnoise_amd, while the elementwise steps stay torch's, as in the reference."""
 
-    def norm(x):
-        return F.rms_norm(x, (x.size(-1),))
+    @staticmethod
+    def lowrank(x, weight, a, b, sign):
+        from noise_amd.eggroll import lowrank
+        return lowrank(x, weight, a, b, sign)
 
-    def rotary(x):
-        d = x.shape[3] // 2
-        x1, x2 = x[..., :d], x[..., d:]
-        return torch.cat([x1 * cos + x2 * sin, x1 * (-sin) + x2 * cos], 3)
+    @staticmethod
+    def lowrank_embed(weight, a, b, idx, sign):
+        from noise_amd.eggroll import lowrank_embed
+        return lowrank_embed(weight, a, b, idx, sign)
 
-    x = x0 = norm(lowrank_embed(p['transformer.wte.weight'], *noise['transformer.wte.weight'], idx, sign))
-    for i in range(cfg.n_layer):
-        pre = f'transformer.h.{i}.'
-        resid = p['resid_lambdas'][i] + s * noise['resid_lambdas'][:, i, None, None]
-        mix = p['x0_lambdas'][i] + s * noise['x0_lambdas'][:, i, None, None]
-        x = resid * x + mix * x0
-
-        def linear(name, inp):
-            return lowrank(inp, p[pre + name], *noise[pre + name], sign)
-
-        h = norm(x)
-        q = linear('attn.c_q.weight', h).view(m, length, heads, dim)
-        k = linear('attn.c_k.weight', h).view(m, length, heads, dim)
-        v = linear('attn.c_v.weight', h).view(m, length, heads, dim)
-        if has_ve(i, cfg.n_layer):
-            name = f'value_embeds.{i}.weight'
-            ve = lowrank_embed(p[name], *noise[name], idx, sign).view(m, length, heads, dim)
-            gate = 2 * torch.sigmoid(linear('attn.ve_gate.weight', h[..., :32]))
-            v = v + gate.unsqueeze(-1) * ve
-        q, k = norm(rotary(q)), norm(rotary(k))
-        y = torch.ops.noise_amd.attention(q, k, v, model.window_sizes[i][0]).reshape(m, length, -1)
-        x = x + linear('attn.c_proj.weight', y)
-        x = x + linear('mlp.c_proj.weight', F.relu(linear('mlp.c_fc.weight', norm(x))).square())
-    h = norm(x)
-    logits = lowrank(h, p['lm_head.weight'], *noise['lm_head.weight'], sign)[..., :cfg.vocab_size].float()
-    logits = 15 * torch.tanh(logits / 15)
-    ce = F.cross_entropy(logits.flatten(0, 1), targets.repeat(m), reduction='none')
-    return ce.view(-1, length).mean(-1)
+    @staticmethod
+    def attention(q, k, v, window):
+        return torch.ops.noise_amd.attention(q, k, v, window)
 
 
-def _chunk_loop(model, loss_fn, pairs, chunk, x, y, step=0, sigma=0.002):
-    """eggroll.py:133-146 as the reference writes it (one rank): losses [members] and, per chunk, the
-    (start, directions, per-member noise, sign, sequence) it evaluated."""
+def composed_population_loss(model, p, noise, sign, idx, targets):
+    """A population_loss of the reference's signature composed from the drop-ins (the oracle's composition run
+    with DropIns as its ops, on the device tensors)."""
+    return om.population_loss(p, noise, sign, idx, targets, ops=DropIns)
+
+
+def member_noise(es, offsets, members, pairs):
+    """Per-member noise, signs and directions for the member ids `members` of a population of `pairs` antithetic
+    pairs: member g perturbs along direction (g mod 2 pairs) // 2, by +sigma when g is even and -sigma when it
+    is odd (eggroll.py:134-142). The rows are gathered per member directly (a direction drawn once per member
+    that uses it), so no pair expansion is needed."""
+    from noise_amd.eggroll import SIGMA
+    direction = (members % (2 * pairs)) // 2
+    sign = torch.where(members % 2 == 0, SIGMA, -SIGMA).float()
+    return es.noise(offsets, direction), sign, direction
+
+
+def run_population(model, loss_fn, pairs, chunk, x, y, step=0):
+    """One rank's whole population through `loss_fn(model, params, noise, sign, idx, targets)` under bf16 autocast,
+    `2 * chunk` members per call; each call's members score the sequence of their first member (per_seq members
+    per sequence, eggroll.py:143). Returns the member losses and, per call, (first member, noise, sign, sequence)."""
     from noise_amd.eggroll import Eggroll
     es = Eggroll(model, pairs)
-    members = max(2 * pairs, 2 * len(x))
-    per_seq = members // len(x)
+    total = max(2 * pairs, 2 * len(x))
+    per_seq = total // len(x)
     offsets = es.offsets(step)
-    losses = torch.empty(members, device=DEV)
-    sign = torch.tensor([sigma, -sigma], device=DEV).repeat(chunk)
-    seen = []
-    for start in range(0, members, 2 * chunk):
-        directions = torch.arange(start, start + 2 * chunk, 2, device=DEV) % (2 * pairs) // 2
-        noise = {n: tuple(t.repeat_interleave(2, 0) for t in v) if isinstance(v, tuple) else v.repeat_interleave(2, 0)
-                 for n, v in es.noise(offsets, directions).items()}
-        seq = start // per_seq
+    parts, calls = [], []
+    for first in range(0, total, 2 * chunk):
+        noise, sign, _ = member_noise(es, offsets, torch.arange(first, first + 2 * chunk, device=DEV), pairs)
+        seq = first // per_seq
         with torch.autocast('cuda', dtype=torch.bfloat16):
-            part = loss_fn(model, es.params, noise, sign, x[seq], y[seq])
-        losses[start:start + 2 * chunk] = part
-        seen.append((start, noise, sign, seq))
-    return losses, seen
+            parts.append(loss_fn(model, es.params, noise, sign, x[seq], y[seq]))
+        calls.append((first, noise, sign, seq))
+    return torch.cat(parts), calls
 
 
 def _tokens(batch, T, seed):
@@ -129,10 +114,10 @@ def _tokens(batch, T, seed):
     return rows[:, :-1].to(DEV), rows[:, 1:].to(DEV)
 
 
-def _check_against_oracle(model, losses, seen, x, y, chunk):
+def _check_against_oracle(model, losses, calls, x, y, chunk):
     P = _cpu_params(model)
     worst = 0.0
-    for start, noise, sign, seq in seen:
+    for start, noise, sign, seq in calls:
         ref = om.population_loss(P, _cpu_noise(noise), sign.cpu(), x[seq].cpu(), y[seq].cpu(), members_per_chunk=4)
         got = losses[start:start + 2 * chunk].cpu()
         assert torch.isfinite(got).all()
@@ -146,13 +131,13 @@ def test_reference_chunk_loop_under_compile(model, composed):
     pairs, chunk = 8, 4                      # two chunks of 8 members
     x, y = _tokens(2, 256, 5)                # two sequences: members 0-7 on one, 8-15 on the other
     if composed:
-        fn = torch.compile(_reference_population_loss, backend='aot_eager', fullgraph=True)
+        fn = torch.compile(composed_population_loss, backend='aot_eager', fullgraph=True)
     else:
         fn = torch.compile(population_loss, fullgraph=True)
     print(f'chunk loop under torch.compile ({"composed" if composed else "fused"}): 16 members x 256 tokens, '
           f'all 60 parameters perturbed', flush=True)
-    losses, seen = _chunk_loop(model, fn, pairs, chunk, x, y)
-    worst = _check_against_oracle(model, losses, seen, x, y, chunk)
+    losses, calls = run_population(model, fn, pairs, chunk, x, y)
+    worst = _check_against_oracle(model, losses, calls, x, y, chunk)
     print(f'worst |loss - oracle| = {worst:.3e}', flush=True)
     assert worst <= TOL
     # the perturbations must matter at this tolerance: a pair's losses differ
@@ -164,8 +149,8 @@ def test_fused_and_composed_agree(model):
     losses (both compiled, same noise), within the bar."""
     from noise_amd.eggroll import population_loss
     x, y = _tokens(1, 256, 6)
-    fused, _ = _chunk_loop(model, torch.compile(population_loss), 4, 4, x, y, step=1)
-    comp, _ = _chunk_loop(model, torch.compile(_reference_population_loss, backend='aot_eager'), 4, 4, x, y, step=1)
+    fused, _ = run_population(model, torch.compile(population_loss), 4, 4, x, y, step=1)
+    comp, _ = run_population(model, torch.compile(composed_population_loss, backend='aot_eager'), 4, 4, x, y, step=1)
     assert (fused - comp).abs().max().item() <= TOL
 
 
@@ -173,9 +158,8 @@ def test_population_member_mapping_ranks_and_chunks(model):
     """Eggroll.population (eggroll.py:134-146): 24 pairs = 48 members over 8 sequences (6 each), two ranks
     of 24 members, chunks of 8 members (three per rank; a chunk's sequence is its first member's,
     start // per_seq, as the reference takes it). Every member of both ranks is checked against the oracle
-    on noise gathered by the reference's formula (directions (g mod 2P) // 2, repeat_interleave(2),
-    signs +sigma, -sigma)."""
-    from noise_amd.eggroll import SIGMA, Eggroll
+    on noise gathered member by member from the mapping's closed form (member_noise)."""
+    from noise_amd.eggroll import Eggroll
     pairs, batch, world, chunk = 24, 8, 2, 8
     x, y = _tokens(batch, 256, 7)
     step = 2
@@ -191,12 +175,10 @@ def test_population_member_mapping_ranks_and_chunks(model):
         assert got.shape == (per_rank,)
         offsets = es.offsets(step)
         for start in range(rank * per_rank, (rank + 1) * per_rank, chunk):
-            directions = torch.arange(start, start + chunk, 2, device=DEV) % (2 * pairs) // 2
-            noise = {n: tuple(t.repeat_interleave(2, 0) for t in v) if isinstance(v, tuple)
-                     else v.repeat_interleave(2, 0) for n, v in es.noise(offsets, directions).items()}
-            sign = torch.tensor([SIGMA, -SIGMA]).repeat(chunk // 2)
+            noise, sign, _ = member_noise(es, offsets, torch.arange(start, start + chunk, device=DEV), pairs)
             seq = start // per_seq
-            ref = om.population_loss(P, _cpu_noise(noise), sign, x[seq].cpu(), y[seq].cpu(), members_per_chunk=4)
+            ref = om.population_loss(P, _cpu_noise(noise), sign.cpu(), x[seq].cpu(), y[seq].cpu(),
+                                     members_per_chunk=4)
             part = got[start - rank * per_rank:start - rank * per_rank + chunk]
             worst = max(worst, (part - ref).abs().max().item())
     print(f'population mapping: worst |loss - oracle| = {worst:.3e}', flush=True)
@@ -246,9 +228,9 @@ def test_lowrank_gate_call_site_compiled():
 
 
 def test_block_forward_and_coordinate_differences_compiled():
-    """run.py:102 and :120 compile block_forward and coordinate_differences: both trace through the
-    registered ops (fullgraph) and equal the eager drop-ins bit for bit."""
-    from noise_amd.dust import block_forward, coordinate_differences
+    """run.py:89, :102 and :120 compile head_loss, block_forward and coordinate_differences: all three trace
+    through the registered ops (fullgraph) and equal the eager drop-ins bit for bit."""
+    from noise_amd.dust import block_forward, coordinate_differences, head_loss, head_loss_eager
     from noise_amd.model import make_model, rotary_tables
     P = {k: v.to(DEV) for k, v in make_model('cpu', 0).state_dict().items()}
     pre = 'transformer.h.1.'
@@ -270,6 +252,12 @@ def test_block_forward_and_coordinate_differences_compiled():
     yy = torch.randint(-1, 4096, (2, 256), generator=g).to(DEV)
     cd = torch.compile(lambda r, t: coordinate_differences(r, t, 0.1), fullgraph=True, backend='aot_eager')
     assert torch.equal(cd(raw, yy), coordinate_differences(raw, yy, 0.1))
+    # run.py:89 compiles head_loss too: the fp32 head traces through torch.ops.noise_amd.head_loss
+    xs = torch.randn(2, 256, 512, generator=g).to(DEV)
+    head = P['lm_head.weight'].float() * 30
+    hl = torch.compile(lambda x_, w_, t_: head_loss(x_, w_, t_, 4096), fullgraph=True, backend='aot_eager')
+    got = hl(xs, head, yy)
+    assert got.shape == (2 * 256,) and torch.equal(got, head_loss_eager(xs, head, yy, 4096))
 
 
 def test_out_of_range_token_ids_give_nan():

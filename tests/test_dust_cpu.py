@@ -176,3 +176,92 @@ def test_rerun_oracle_reduces_to_the_clean_forward():
     jit = {'o@5': 0.05 * torch.randn(n * 2, 256, 512, generator=g)}
     moved = odust.rerun(P, cache, y, n, 5, jit)
     assert (moved - clean).abs().max().item() > 1e-3
+
+
+def test_chunk_size_is_the_largest_divisor():
+    """run.py:76-78 by brute force: the largest n <= cap dividing draws; the product's and the oracle's agree."""
+    from noise_amd.dust import chunk_size
+    for draws in range(1, 65):
+        for cap in range(1, 20):
+            want = max(n for n in range(1, cap + 1) if draws % n == 0 and n <= draws)
+            assert chunk_size(draws, cap) == want == odust.chunk_size(draws, cap), (draws, cap)
+    with pytest.raises(ValueError):
+        chunk_size(0, 4)
+
+
+@pytest.mark.parametrize('gamma', [0.5, 0.9, 0.99])
+def test_reward_to_go_closed_forms(gamma):
+    """run.py:81-86: a unit impulse at token j gives gamma^(j - i) at every token i <= j within the lags (and 0
+    elsewhere); a constant reward gives the truncated geometric sum (1 - gamma^m) / (1 - gamma),
+    m = min(lags, t - i). The product's conv1d form (torch CPU) and the oracle's loop both match."""
+    import math
+    import torch
+    from noise_amd.dust import reward_to_go
+    t = 300
+    lags = math.ceil(math.log(1e-6) / math.log(gamma))
+    imp = np.zeros((2, 3, t))
+    imp[1, 2, 250] = 1.0
+    ones = np.ones((2, 3, t))
+    i = np.arange(t)
+    want_imp = np.where((i <= 250) & (250 - i < lags), gamma ** np.clip(250 - i, 0, None), 0.0)
+    m = np.minimum(lags, t - i)
+    want_ones = (1 - gamma ** m) / (1 - gamma)
+    for fn, tol in ((odust.reward_to_go, 1e-12), (lambda r, g: reward_to_go(torch.from_numpy(r), g).numpy(), 1e-9)):
+        got_imp, got_ones = fn(imp, gamma), fn(ones, gamma)
+        assert np.abs(got_imp[1, 2] - want_imp).max() <= tol
+        assert np.abs(got_imp[0]).max() == 0 and np.abs(got_imp[1, :2]).max() == 0
+        assert np.abs(got_ones - want_ones).max() <= tol * lags
+
+
+def _linear_case(d, draws, nrep, offset=0.0, prior_scale=None, mask=False, seed=0):
+    """A loss that is linear in the jitter: loss_i = clean + sigma_bf a_i . g at every token (g per token), the
+    oracle's direct_errors over its orthogonal draws (one site of width d). Returns (estimate, g, mask)."""
+    import torch
+    from oracle.orthogonal import OrthogonalDrawsOracle
+    rng = np.random.default_rng(seed)
+    b, t, sigma = 2, 8, 0.1
+    g = rng.normal(size=(b, t, d))
+    clean = rng.normal(size=(b, t)) + 8.0
+    live = {}
+    if mask:
+        live['s'] = (rng.random((b, t, d)) > 0.5).astype(np.float64)
+    draw = OrthogonalDrawsOracle(seed=seed)
+
+    def rerun_fn(n, jitter):
+        j = jitter['s'].double().numpy().reshape(n, b, t, d)
+        return clean[None] + offset + np.einsum('nbtd,btd->nbt', j, g)
+
+    priors = {'s': prior_scale * g} if prior_scale is not None else None
+    est, _ = odust.direct_errors(draw, rerun_fn, clean, live, ['s'], {'s': d}, draws, sigma, nrep, priors=priors)
+    return est['s'], g, live.get('s'), float(torch.tensor(sigma).bfloat16()) / sigma
+
+
+def test_direct_errors_oracle_recovers_a_linear_gradient():
+    """One full cycle of d orthogonal draws, one draw per rerun (no centring): sum_i a_i a_i^T = d I, so the
+    estimate of a linear loss is its gradient g exactly, up to the bf16 rounding of each reward (2^-8 relative)
+    and sigma's own bf16 rounding in the jitter (a fixed factor). With half of the units dead (masked), the dead
+    units' estimates are exactly 0 and the live units' are the gradient of the masked loss."""
+    for mask in (False, True):
+        est, g, live, ratio = _linear_case(64, 64, 1, mask=mask)
+        want = g * ratio * (live if mask else 1.0)
+        err = np.abs(est - want).max()
+        assert err <= 2 ** -7 * np.abs(g).sum(-1).max() / 8 + 1e-9, err
+        if mask:
+            assert np.all(est[live == 0] == 0)
+
+
+def test_direct_errors_oracle_priors_and_centring():
+    """A perfect prior (mu = g at sigma's bf16 ratio) leaves a zero residual reward, so the estimate is the prior
+    itself; half a prior is completed by the draws. With n > 1 draws per rerun, a constant added to every
+    perturbed loss cancels in the centring; with n = 1 it does not."""
+    est, g, _, ratio = _linear_case(64, 64, 1, prior_scale=None)
+    full, _, _, _ = _linear_case(64, 64, 1, prior_scale=ratio)
+    assert np.abs(full - g * ratio).max() <= 2 ** -7 * np.abs(g).max() * 4
+    half, _, _, _ = _linear_case(64, 64, 1, prior_scale=0.5 * ratio)
+    assert np.abs(half - g * ratio).max() <= 2 ** -7 * np.abs(g).sum(-1).max() / 4 + 1e-9
+    c0, _, _, _ = _linear_case(64, 64, 4)
+    c1, _, _, _ = _linear_case(64, 64, 4, offset=0.37)
+    assert np.abs(c1 - c0).max() <= 2 ** -6 * np.abs(c0).max()
+    u0, _, _, _ = _linear_case(64, 64, 1)
+    u1, _, _, _ = _linear_case(64, 64, 1, offset=0.37)
+    assert np.abs(u1 - u0).max() > 0.01

@@ -188,3 +188,123 @@ def test_rerun_matches_oracle(entry, site, width):
     assert eff <= 1e-3
     effect = (ref - ref0).mean(-1).abs().max().item()
     assert effect > max(1e-4, 10 * eff), 'the jitter must move the losses well beyond the error'
+
+
+@pytest.mark.parametrize('entry,sites,prior_sites,gamma', [
+    (6, ['transformer.h.6.mlp.c_fc', 'o@6'], ['o@6'], 0.0),
+    (3, ['transformer.h.3.mlp.c_fc', 'transformer.h.3.attn.c_proj'], ['transformer.h.3.mlp.c_fc'], 0.0),
+    (None, ['transformer.wte'], [], 0.9)], ids=['late-fc-o-prior', 'fc-prior-attn', 'embedding-gamma'])
+def test_direct_errors_matches_oracle(monkeypatch, entry, sites, prior_sites, gamma):
+    """DUST.direct_errors (run.py:332-378) end to end on the device -- orthogonal draws per site, the live-unit
+    mask of an mlp.c_fc site, 2 chunks of n = 4 draws (draws 8, nrep 4) rerun from block `entry`, the reward
+    centred over each chunk (the clean loss is offset by 0.05 so that an uncentred reward would show), priors from
+    a retrieval (alpha 0.5), reward-to-go, the bf16 estimate update -- against the oracle composition
+    (oracle/dust.py direct_errors over OrthogonalDrawsOracle, the oracle's rerun and the bf16 roundings).
+
+    Bounds. (1) The device draws equal the oracle's bit for bit. (2) Fed the device rerun's own losses, the
+    oracle composition agrees with the device estimate to the rounding of the bf16 steps: per chunk a one-ulp
+    flip (2^-7 relative) of each draw's bf16 reward and of the chunk sum, / (sigma draws). (3) The device rerun's
+    losses are within the rerun's bar of the fp32 oracle's (per-draw mean 1e-3, per token 3e-2), and the
+    end-to-end estimate differs from the oracle's by at most the propagated reward difference
+    sum_i |delta r_i| |a_i| / (sigma draws) plus (2). (4) Dead units of an mlp.c_fc site without a prior are
+    exactly 0; estimates of prior sites and the fits of retrieved sites are recorded as the reference does."""
+    from types import SimpleNamespace
+    import noise_amd.dust as ndust
+    from noise_amd.model import make_model
+    from noise_amd.noise import OrthogonalDraws
+    from oracle.orthogonal import OrthogonalDrawsOracle
+    model = make_model('cpu', 0)
+    with torch.no_grad():
+        model.lm_head.weight.mul_(30)
+    P = {k: v.detach().float().clone() for k, v in model.named_parameters()}
+    g = torch.Generator().manual_seed(41)
+    b, T, draws, nrep, sigma = 2, 256, 8, 4, 0.1
+    rows = torch.randint(0, 4096, (b, T + 1), generator=g)
+    x, y = rows[:, :-1], rows[:, 1:]
+    cache = odust.capture(P, x)
+    clean = odust.rerun(P, cache, y, 1, 6, {})[0] + 0.05
+    dev = torch.device('cuda', 0)
+    to = lambda d: {k: v.to(dev) for k, v in d.items()}
+    widths = {s: 512 if s.startswith('o@') else cache['outputs'][s].shape[-1] for s in sites}
+    retrieved = {s: (torch.randn(b, T, widths[s], generator=g) * 0.2) for s in prior_sites}
+    alpha = {s: 0.5 for s in prior_sites}
+    print(f'direct_errors: entry {entry}, sites {sites}, priors {prior_sites}, gamma {gamma}, {draws} draws in '
+          f'chunks of {nrep}, {b} x {T} tokens', flush=True)
+
+    draws_dev = OrthogonalDraws(seed=0, device=dev)
+    seen_draws, seen_losses = [], []
+
+    def orthogonal_noise(site, draws_, chunk, n, b_, t_, d):
+        a = draws_dev(site, draws_, chunk, n, b_, t_, d, dtype=torch.bfloat16)
+        seen_draws.append((site, chunk, a.cpu()))
+        return a
+
+    real_rerun = ndust.rerun
+
+    def recording_rerun(dust_, n, entry_, jitter):
+        loss = real_rerun(dust_, n, entry_, jitter)
+        seen_losses.append(loss.cpu().double().numpy())
+        return loss
+
+    monkeypatch.setattr(ndust, 'rerun', recording_rerun)
+    m = model.to(dev)
+    dust = SimpleNamespace(
+        model=m, length=T, batch=b, outputs=to(cache['outputs']), blocks=to(cache['blocks']), x0=cache['x0'].to(dev),
+        y=y.to(dev), clean_loss=clean.to(dev), dtype=torch.bfloat16, recipe=SimpleNamespace(nrep=nrep),
+        weights=[{k: (None if v is None else v.to(dev)) for k, v in odust.block_weights(P, i).items()} for i in range(8)],
+        alpha=alpha, estimates={}, fits={}, prior_sites=list(prior_sites), orthogonal_noise=orthogonal_noise)
+    got = ndust.direct_errors(dust, sites, draws, sigma, entry=entry, gamma=gamma, retrieved=to(retrieved))
+    got = {s: e.cpu().double().numpy() for s, e in got.items()}
+
+    live = {s: (cache['outputs'][s] > 0).double().numpy() for s in sites if s.endswith('mlp.c_fc')}
+    priors = {s: 0.5 * retrieved[s].double().numpy() for s in prior_sites}
+    oracle_draws = OrthogonalDrawsOracle(seed=0)
+    draw = lambda *args: oracle_draws(*args)
+    replay = iter(seen_losses)
+    ref_g, rec_g = odust.direct_errors(draw, lambda n, j: next(replay), clean.numpy(), live, sites, widths, draws,
+                                       sigma, nrep, gamma=gamma, priors=priors)
+    oracle_draws = OrthogonalDrawsOracle(seed=0)
+    ref, rec = odust.direct_errors(draw, lambda n, j: odust.rerun(P, cache, y, n, entry, j).numpy(), clean.numpy(),
+                                   live, sites, widths, draws, sigma, nrep, gamma=gamma, priors=priors)
+
+    # (1) the draws (the composition masks an mlp.c_fc site's draws by its live units)
+    assert len(seen_draws) == len(sites) * (draws // nrep)
+    for site, chunk, a in seen_draws:
+        assert np.array_equal(a.double().numpy() * live.get(site, 1.0), rec_g[chunk]['a'][site]), (site, chunk)
+    # (2) the composition over the device losses, to the bf16 steps' rounding
+    ulp = 2.0 ** -7
+    worst = {}
+    for s in sites:
+        bound = sum(ulp * (np.abs(r['sums'][s]) + np.einsum('nbt,nbtd->btd', np.abs(r['reward']), np.abs(r['a'][s])))
+                    for r in rec_g) / (sigma * draws) + 1e-6
+        diff = np.abs(got[s] - ref_g[s])
+        worst[s] = float((diff / bound).max())
+        assert np.all(diff <= bound), (s, worst[s])
+    # (3) the end-to-end estimate against the fp32 oracle rerun
+    dev_loss, ora_loss = np.stack(seen_losses), np.stack([r['loss'] for r in rec])
+    tok = np.abs(dev_loss - ora_loss).max()
+    mean = np.abs(dev_loss.mean(-1) - ora_loss.mean(-1)).max()
+    assert tok <= 3e-2 and mean <= 1e-3, (tok, mean)
+    for s in sites:
+        prop = sum(np.einsum('nbt,nbtd->btd', np.abs(rg['reward'] - ro['reward']), np.abs(ro['a'][s]))
+                   for rg, ro in zip(rec_g, rec)) / (sigma * draws)
+        bound = prop + sum(ulp * (np.abs(r['sums'][s]) + np.einsum('nbt,nbtd->btd', np.abs(r['reward']),
+                                                                   np.abs(r['a'][s]))) for r in rec_g + rec) \
+            / (sigma * draws) + 1e-6
+        rel = float(np.linalg.norm(got[s] - ref[s]) / np.linalg.norm(ref[s]))
+        print(f'  {s}: composition {worst[s]:.2f} of its rounding bound; end to end rel {rel:.2e}, '
+              f'|estimate| rms {float(np.sqrt((ref[s] ** 2).mean())):.3e}', flush=True)
+        assert np.all(np.abs(got[s] - ref[s]) <= bound), s
+    print(f'  rerun: per-token {tok:.2e}, per-draw mean {mean:.2e}', flush=True)
+    # (4) dead units, recorded estimates and fits
+    for s, mask in live.items():
+        if s not in prior_sites:
+            assert np.all(got[s][mask == 0] == 0)
+    assert set(dust.estimates) == set(prior_sites)
+    for s in prior_sites:
+        kept = 1 - 1 / 4
+        r = retrieved[s].double().numpy()
+        dot, rr = dust.fits[s].cpu().double().numpy()
+        assert abs(rr - (r * r).sum()) <= 1e-4 * (r * r).sum()
+        assert abs(dot - (r * got[s] / kept).sum()) <= 1e-3 * np.abs(r * got[s] / kept).sum()
+

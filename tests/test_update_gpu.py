@@ -1,6 +1,6 @@
 """EGGROLL's update reassembly on the GPU (noise_update_weights / noise_update_gradients through the C ABI)
-against the oracle (oracle/update.py) and against the reference's own loop (eggroll.py:151-165) run with
-torch ops over Eggroll.noise's device slices.
+against the oracle (oracle/update.py) and against a float64 contraction over Eggroll.noise's device slices
+(the update of eggroll.py:151-165: -(1/F) sum_d w_d a_d b_d^T per matrix, -(1/F) sum_d w_d eps_d per 1-D scalar).
 
 Tolerance: the gradients are fp32 sums over the directions; the device forms the matrices' products as
 split-bf16x3 MFMA GEMMs (each value hi + lo to 2^-16), so entries agree with the float64 oracle to 1e-4 of
@@ -38,6 +38,16 @@ class _Params(torch.nn.Module):
         self.lam = torch.nn.Parameter(torch.zeros(8))
 
 
+def _direction_weights(losses, pairs):
+    """Per-direction weights of the update, float64: member pair i holds losses (L[2i], L[2i+1]) and scores
+    L[2i+1] - L[2i]; the scores are divided by their sample standard deviation (+1e-8) and summed per direction
+    i mod pairs."""
+    L = losses.double().cpu().numpy().reshape(-1, 2)
+    score = L[:, 1] - L[:, 0]
+    score = score / (score.std(ddof=1) + 1e-8)
+    return score.reshape(-1, pairs).sum(0)
+
+
 def _oracle(es, losses, offsets):
     d = es.buffer
     shapes = {n: tuple(p.shape) for n, p in es.params.items()}
@@ -51,9 +61,7 @@ def test_weights_match_torch():
         losses = _losses(members, seed=members)
         w = torch.empty(pairs, device='cuda')
         _lib.call('noise_update_weights', _lib.ptr(losses), members, pairs, _lib.ptr(w), _lib.stream_ptr())
-        fitness = losses[1::2] - losses[0::2]
-        fitness = fitness / (fitness.std() + 1e-8)
-        ref = torch.zeros(pairs, device='cuda').index_add_(0, torch.arange(len(fitness), device='cuda') % pairs, fitness)
+        ref = torch.from_numpy(_direction_weights(losses, pairs)).float().cuda()
         torch.cuda.synchronize()
         print(f'weights members {members} pairs {pairs}', flush=True)
         assert torch.allclose(w, ref, rtol=1e-5, atol=1e-6)
@@ -75,30 +83,28 @@ def test_full_model_matches_oracle():
     assert worst[0] <= TOL
 
 
-def test_chunks_accumulate_and_match_the_reference_loop():
+def test_chunks_accumulate_and_match_the_contraction():
     # pairs 600 in chunks of 256: three GEMM passes (the last partial), 1-D and small parameters alongside
     from noise_amd.eggroll import Eggroll
     es = Eggroll(_Params().cuda(), 600)
     offsets = es.offsets(11)
     losses = _losses(1200, seed=1)
     grads = es.update(losses, offsets, chunk=256)
-    # eggroll.py:151-165 literally, over the device slices (fp32 torch matmuls, CHUNK = 256)
-    fitness = losses[1::2] - losses[0::2]
-    fitness = fitness / (fitness.std() + 1e-8)
-    weight = torch.zeros(600, device='cuda').index_add_(0, torch.arange(len(fitness), device='cuda') % 600, fitness)
-    gradients = {n: torch.zeros_like(p) for n, p in es.params.items()}
-    for start in range(0, 600, 256):
-        directions = torch.arange(start, min(600, start + 256), device='cuda')
-        w = weight[directions]
-        for name, n in es.noise(offsets, directions).items():
-            if isinstance(n, tuple):
-                gradients[name] -= (w[:, None] * n[0]).t() @ n[1]
-            else:
-                gradients[name] -= w @ n
+    # the same gradients as one float64 contraction over all directions at once, on the device slices
+    w = _direction_weights(losses, 600)
+    n_pairs = losses.numel() // 2
+    drawn = es.noise(offsets, torch.arange(600, device='cuda'))
+    torch_grads = {}
+    for name, n in drawn.items():
+        if isinstance(n, tuple):
+            A, B = (t.double().cpu().numpy() for t in n)
+            torch_grads[name] = -((A * w[:, None]).T @ B) / n_pairs
+        else:
+            torch_grads[name] = -(w @ n.double().cpu().numpy()) / n_pairs
     ref = _oracle(es, losses, offsets)
     for name in es.params:
         got = grads[name].cpu().numpy()
-        torch_ref = (gradients[name] / len(fitness)).cpu().numpy()
+        torch_ref = torch_grads[name]
         print(name, _rel(got, ref[name]), _rel(got, torch_ref), flush=True)
         assert got.shape == tuple(es.params[name].shape)
         assert _rel(got, ref[name]) <= TOL

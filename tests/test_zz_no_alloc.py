@@ -71,15 +71,26 @@ def test_static_matches_workspace_entry_two_calls():
 
 
 def test_static_rejects_inputs_beyond_the_scratch():
+    """64 sequences x 2048 tokens need more scratch than the static array holds: rejected on the host before any
+    launch. Every pointer is a real device buffer of the full shape (inputs, output, value rows, weights, rotary
+    tables), so only the scratch size is at stake in this call."""
     from noise_amd import _lib
     lib = _lib.lib()
+    S, T = 64, 2048
     cap = _fn(lib, 'noise_dust_block_static_max_bytes', [], ctypes.c_int64)()
     need = _fn(lib, 'noise_dust_block_workspace_bytes', [ctypes.c_int64, ctypes.c_int64, ctypes.c_int],
-               ctypes.c_int64)(64, 2048, 1)
+               ctypes.c_int64)(S, T, 1)
     assert need > cap
+    _, w, _, cos, sin, _, _ = _inputs(1, T, True, 3)
+    x = torch.zeros(S, T, 512, device=DEV)
+    out = torch.full((S, T, 512), float('nan'), device=DEV)
+    ve = torch.zeros(S, T, 512, dtype=torch.bfloat16, device=DEV)
     p = ctypes.c_void_p
     f = _fn(lib, 'noise_dust_block_static', [p, p, ctypes.c_int64, ctypes.c_int64, p, p, p, p, ctypes.c_int64, p, p,
                                               p, p, p])
-    w = (ctypes.c_void_p * 7)(*([16] * 7))
-    st = f(16, 16, 64, 2048, w, 16, 16, 16, 1024, None, None, None, None, None)
+    wp = (ctypes.c_void_p * 7)(*[t.data_ptr() for t in w])
+    st = f(x.data_ptr(), out.data_ptr(), S, T, wp, ve.data_ptr(), cos.data_ptr(), sin.data_ptr(), 1024, None, None,
+           None, None, _lib.stream_ptr(DEV))
     assert st == -1 and 'static array holds' in lib.noise_last_error().decode()
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all(), 'a rejected call must not have launched'
