@@ -185,7 +185,7 @@ def main():
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
     ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update', 'head-error', 'dust-block',
-                                           'attention', 'lowrank', 'cpu-forward'),
+                                           'dust-rerun', 'attention', 'lowrank', 'cpu-forward'),
                     default='population')
     ap.add_argument('--pairs', type=int, default=None,
                     help='update workload: antithetic pairs (default 512; the reference trains with 131072)')
@@ -218,6 +218,8 @@ def main():
         return bench_head_error(args)
     if args.workload == 'dust-block':
         return bench_dust_block(args)
+    if args.workload == 'dust-rerun':
+        return bench_dust_rerun(args)
     if args.workload == 'attention':
         return bench_attention(args)
     if args.workload == 'lowrank':
@@ -246,6 +248,8 @@ def main():
     directions = torch.arange(0, members, 2, device=dev) % (2 * pairs) // 2
     shapes = {n: tuple(P[n].shape) for n in names}
 
+    gather_events = None   # (start, end) events around the noise-slice regeneration, in the profiling steps
+
     def step():
         if orthogonal:
             tables = eg.orthogonal_directions(shapes, pairs, seed=0, device=dev)
@@ -253,10 +257,16 @@ def main():
             return eg.orthogonal_population(W, tables, x, y, sigma=SIGMA, chunk=chunk), tables
         offsets = es.offsets(0)
         tables = {}
+        if gather_events is not None:
+            ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            ev[0].record()
         for n in names:
             p = es.params[n]
             rows = es.buffer.gather(offsets[n], sum(p.shape), rows=directions)
             tables[n] = tuple(rows.split(list(p.shape), dim=1))
+        if gather_events is not None:
+            ev[1].record()
+            gather_events.append(ev)
         W = eg.Weights(P)
         return eg.population_forward(W, tables, sign, x, y, dir_div=2, rope=rope), tables
 
@@ -273,6 +283,7 @@ def main():
     # per-kernel HIP events (torch's current stream = the launch stream) over extra timed steps
     timer = eg.KernelTimer()
     eg.set_timer(timer)
+    gather_events = []
     for _ in range(args.profile_steps):
         step()
     torch.cuda.synchronize()
@@ -286,6 +297,14 @@ def main():
             tf = flops * n / (ms * 1e-3)
             entry.update(tflops=round(tf / 1e12, 1), mfma_frac=round(tf / BF16_PEAK, 4))
         kernels[key] = entry
+    if gather_events:
+        # the noise regeneration replacing the reference's buffer gather (eggroll.py:114, 126-127): one
+        # noise_gather_slices launch per perturbed matrix, writing its directions' a and b rows in fp32
+        ms = sum(s_.elapsed_time(e_) for s_, e_ in gather_events) / len(gather_events)
+        written = 4 * len(directions) * sum(sum(shapes[n]) for n in names)
+        kernels['noise_gather_slices'] = dict(launches=len(names), ms_per_step=round(ms, 4), bytes_written=written,
+                                              gbps=round(written / ms / 1e6, 1),
+                                              hbm_frac=round(written / ms / 1e6 / (HBM_PEAK / 1e9), 4))
     timed = [k for k in kernels if 'tflops' in kernels[k]]
     roofline = None
     if timed:
@@ -443,6 +462,73 @@ def bench_dust_block(args):
         roofline=dict(bound='mfma', achieved=round(flops / ms / 1e9, 1), peak=BF16_PEAK / 1e12, unit='TFLOP/s',
                       frac=round(flops / ms / 1e9 / (BF16_PEAK / 1e12), 4), traffic=None),
         finite=bool(torch.isfinite(out).all().item()))), flush=True)
+
+
+def bench_dust_rerun(args):
+    """DUST.rerun (run.py:256-279) as direct_errors calls it: 16 draws x 8 sequences x 2048 tokens rerun from block
+    0 with bf16 jitter (+-0.1) at its mlp.c_fc, then blocks 1-7, the final norm and the fp32 head with per-token CE.
+    The capture state (block 0's input, x0, the embedding and value-embedding outputs) is formed with torch from
+    the seed-0 model and uniform tokens. Timed: `rerun` (the blocks after the jittered one on the population
+    kernels) and, for comparison, `rerun_tiled` (every block on noise_dust_block)."""
+    import torch
+    import torch.nn.functional as F
+    from types import SimpleNamespace
+    from noise_amd import dust as ndust
+    from noise_amd.model import make_model, window_sizes
+    dev = torch.device('cuda', 0)
+    n, b, T = 16, 8, TOKENS
+    model = make_model('cpu', 0).to(dev)
+    g = torch.Generator().manual_seed(0)
+    rows = torch.randint(0, 4096, (b, T + 1), generator=g).to(dev)
+    x, y = rows[:, :-1].contiguous(), rows[:, 1:].contiguous()
+    with torch.no_grad():
+        emb = model.transformer.wte.weight[x].float()
+        x0 = F.rms_norm(emb, (512,))
+        block0 = model.resid_lambdas[0] * x0 + model.x0_lambdas[0] * x0
+        outputs = {'transformer.wte': emb}
+        for key, table in model.value_embeds.items():
+            outputs[f'value_embeds.{key}'] = table.weight[x].float()
+    weights = [dict(q=blk.attn.c_q.weight, k=blk.attn.c_k.weight, v=blk.attn.c_v.weight,
+                    gate=blk.attn.ve_gate.weight if blk.attn.ve_gate is not None else None,
+                    proj=blk.attn.c_proj.weight, fc=blk.mlp.c_fc.weight, out=blk.mlp.c_proj.weight)
+               for blk in model.transformer.h]
+    state = SimpleNamespace(model=model, length=T, batch=b, outputs=outputs, blocks={0: block0}, x0=x0, x=x, y=y,
+                            weights=weights)
+    jit = {'transformer.h.0.mlp.c_fc': (0.1 * (torch.randint(0, 2, (n * b, T, 2048), generator=g) * 2 - 1))
+           .bfloat16().to(dev)}
+    timings = {}
+    for name in ('rerun', 'rerun_tiled'):
+        fn = getattr(ndust, name)
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                loss = fn(state, n, 0, jit)
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record()
+            for _ in range(args.steps):
+                loss = fn(state, n, 0, jit)
+            e.record()
+            torch.cuda.synchronize()
+        timings[name] = (s.elapsed_time(e) / args.steps, loss.clone())
+    ms, loss = timings['rerun']
+    wins = window_sizes(8)
+    gemm = 2 * (512 * 1536 + 512 * 512 + 2 * 512 * 2048)
+    flops = sum(gemm + 4 * 64 * 8 * visible_pairs(T, w) / T for w in wins) + 2 * 512 * 4096
+    flops *= n * b * T
+    tiled_ms, tiled_loss = timings['rerun_tiled']
+    print(json.dumps(dict(
+        metric='DUST rerun throughput from block 0 (jitter at mlp.c_fc, 8 blocks + fp32 head), sequence-tokens/s',
+        value=round(n * b * T / ms * 1e3), unit='tokens/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 3), higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
+        data='synthetic', config=dict(workload=f'{n} draws x {b} sequences x {T} tokens from block 0 of the fixed '
+                                               '37.7M GPT, fp32 head'),
+        ms_per_block=round(ms / 8, 3), tiled_ms_per_step=round(tiled_ms, 3), tiled_ms_per_block=round(tiled_ms / 8, 3),
+        speedup_vs_tiled=round(tiled_ms / ms, 3),
+        roofline=dict(bound='mfma', achieved=round(flops / ms / 1e9, 1), peak=BF16_PEAK / 1e12, unit='TFLOP/s',
+                      frac=round(flops / ms / 1e9 / (BF16_PEAK / 1e12), 4), traffic=None),
+        mean_loss=round(loss.mean().item(), 6), max_abs_vs_tiled=float((loss - tiled_loss).abs().max()),
+        mean_abs_vs_tiled=float((loss.mean(-1) - tiled_loss.mean(-1)).abs().max()),
+        finite=bool(torch.isfinite(loss).all().item()))), flush=True)
 
 
 def bench_attention(args):

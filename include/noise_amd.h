@@ -368,6 +368,12 @@ int noise_draw_errors(const float *reward, const void *a, int64_t n, int64_t row
 int noise_rerun_rows(const float *x, int64_t x_rows, const void *add, const float *x0, int64_t x0_rows,
                      const float *lam_r, const float *lam_x, int64_t rows, float *out, noise_stream_t stream);
 
+/* DUST.rerun's mixing into a block that runs on the population kernels (run.py:266-268, then the block's
+ * norm(x), utils/model.py:117): out[r] = rl * x[r mod x_rows] + ml * x0[r mod x0_rows] (fp32, rl = *lam_r,
+ * ml = *lam_x on the device) and h[r] = bf16(norm(out[r])) (bf16 [rows][512]), the block's normalised input. */
+int noise_rerun_mix_norm(const float *x, int64_t x_rows, const float *x0, int64_t x0_rows, const float *lam_r,
+                         const float *lam_x, int64_t rows, float *out, void *h, noise_stream_t stream);
+
 /* DUST's block_forward (run.py:102-117) over `sequences` rows of `tokens` (a multiple of 256) tokens: the fixed
  * model's block (utils/model.py:103-110) on x fp32 [sequences][tokens][512] -> x_out fp32 (same layout), with
  * the weights unperturbed and optional jitter, bf16 [sequences][tokens][width] or NULL, added where the

@@ -45,6 +45,7 @@ SIGNATURES = {
     'noise_coordinate_differences': [_p, _i32, _i64, _i64, _i64, _p, _f32, _p, _i64, _i64, _p],
     'noise_draw_errors': [_p, _p, _i64, _i64, _i64, _f32, _p, _p],
     'noise_rerun_rows': [_p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _p],
+    'noise_rerun_mix_norm': [_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _p],
     'noise_dust_block_workspace_bytes': [_i64, _i64, _i32],
     'noise_dust_block': [_p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p],
     'noise_dust_block_static_max_bytes': [],

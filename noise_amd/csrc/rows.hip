@@ -624,10 +624,12 @@ namespace {
 // DUST.rerun's glue between blocks (run.py:262-268), over rows of 512 (one wave per row):
 //   entry (x0 == NULL): out[r] = norm(e[r % e_rows] (+ add[r]))      the jittered embedding entry
 //   mix   (x0 != NULL): out[r] = rl * x[r] + ml * x0[r % x0_rows]     the next block's mixing scalars
-// e / x fp32, add bf16 or NULL, x0 fp32; rl, ml read on the device.
+// e / x fp32, add bf16 or NULL, x0 fp32; rl, ml read on the device. With h, the mixed row's norm is also
+// stored as bf16 (the normalised input of the block the row enters, utils/model.py:117).
 __global__ __launch_bounds__(256) void rerun_rows_kernel(const float *x, int64_t x_rows, const __bf16 *add,
                                                          const float *x0, int64_t x0_rows, const float *lam_r,
-                                                         const float *lam_x, int64_t rows, float *out) {
+                                                         const float *lam_x, int64_t rows, float *out,
+                                                         __bf16 *h) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -653,6 +655,16 @@ __global__ __launch_bounds__(256) void rerun_rows_kernel(const float *x, int64_t
         for (int i = 0; i < 8; ++i) v[i] *= r;
     }
     st8(out + row * 512 + lane * 8, v);
+    if (h) {
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+        const float r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
+        bf16x8 hb;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) hb[i] = (__bf16)(v[i] * r);
+        store_bf16x8(h + row * 512 + lane * 8, hb);
+    }
 }
 
 }  // namespace
@@ -668,6 +680,20 @@ extern "C" int noise_rerun_rows(const float *x, int64_t x_rows, const void *add,
     NOISE_CHECK_ARG(!x0 || (x0_rows > 0 && aligned(x0, 16) && lam_r && lam_x && !add),
                     "%s: mixing needs x0 rows, both lambdas and no add", fn);
     hipLaunchKernelGGL(rerun_rows_kernel, dim3(rows_grid(rows)), dim3(256), 0, (hipStream_t)stream, x, x_rows,
-                       (const __bf16 *)add, x0, x0_rows, lam_r, lam_x, rows, out);
+                       (const __bf16 *)add, x0, x0_rows, lam_r, lam_x, rows, out, nullptr);
+    return launch_status(fn);
+}
+
+extern "C" int noise_rerun_mix_norm(const float *x, int64_t x_rows, const float *x0, int64_t x0_rows,
+                                    const float *lam_r, const float *lam_x, int64_t rows, float *out, void *h,
+                                    noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_rerun_mix_norm";
+    NOISE_CHECK_ARG(x && out && h && rows > 0 && x_rows > 0 && aligned(x, 16) && aligned(out, 16) && aligned(h, 16),
+                    "%s: bad x / out / h", fn);
+    NOISE_CHECK_ARG(x0 && x0_rows > 0 && aligned(x0, 16) && lam_r && lam_x, "%s: mixing needs x0 rows and both lambdas",
+                    fn);
+    hipLaunchKernelGGL(rerun_rows_kernel, dim3(rows_grid(rows)), dim3(256), 0, (hipStream_t)stream, x, x_rows,
+                       (const __bf16 *)nullptr, x0, x0_rows, lam_r, lam_x, rows, out, (__bf16 *)h);
     return launch_status(fn);
 }

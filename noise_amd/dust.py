@@ -166,9 +166,83 @@ def _rotary(model, T, dev):
     return cos.bfloat16().to(dev), sin.bfloat16().to(dev)
 
 
+def _weights(dust):
+    """The population kernels' weights of dust.model (bf16 matrices in the block kernel's layouts, the fp32 head
+    as split-bf16x3), built on first use and rebuilt when a parameter has changed since (an in-place optimizer
+    step bumps the tensor's version)."""
+    from .eggroll import Weights
+    params = dict(dust.model.named_parameters())
+    key = tuple((name, p.data_ptr(), p._version) for name, p in params.items())
+    cached = getattr(dust, '_noise_amd_weights', None)
+    if cached is None or cached[0] != key:
+        dev = dust.y.device
+        W = Weights({name: p.detach() for name, p in params.items()}, device=dev, n_layer=dust.model.config.n_layer,
+                    fp32_head=True)
+        dust._noise_amd_weights = cached = (key, W)
+    return cached[1]
+
+
 def rerun(dust, n, entry, jitter):
     """DUST.rerun (run.py:256-279) with the same arguments and state: the per-token losses [n, batch, length]
     of n jittered draws, rerun from block `entry` (None: from the embedding).
+
+    `dust` carries what the reference's DUST object holds after capture: model (resid_lambdas, x0_lambdas,
+    window_sizes, lm_head, config, parameters), length, batch, outputs ('transformer.wte' and 'value_embeds.{i}'
+    outputs), blocks (block inputs by layer), x0 (the normed embedding), x and y (the batch's token ids and
+    targets, [batch, length]) and weights (the per-block dicts of run.py:172-175). jitter: site name ->
+    [n * batch, length, width] (sigma * draws).
+
+    The chain: the cached input of block `entry` repeated n times through that block with its jitter sites
+    (noise_dust_block, the block with per-token jitter epilogues), or the jittered embedding entry normed; then
+    every later block's mixing and the blocks on the population kernels (blocks_forward: n * batch members, one
+    token row each, no rank-1 terms), the final norm and the fp32 head (split-bf16x3) with the soft cap and CE.
+    A jittered last block goes straight to the head (head_loss)."""
+    from .eggroll import blocks_forward
+    model = dust.model
+    T, b = dust.length, dust.batch
+    dev = dust.y.device
+    stream = _lib.stream_ptr(dev)
+    rows = n * b * T
+    L = model.config.n_layer
+    W = _weights(dust)
+    cos, sin = _rotary(model, T, dev)
+    if entry is None:
+        emb = dust.outputs['transformer.wte'].detach().to(F32).contiguous()
+        add = jitter.get('transformer.wte')
+        add = None if add is None else add.reshape(n * b, T, -1).to(BF16).contiguous()
+        x0 = torch.empty(n * b, T, 512, dtype=F32, device=dev)
+        _lib.call('noise_rerun_rows', emb.data_ptr(), b * T, _lib.ptr(add), None, 0, None, None, rows, x0.data_ptr(),
+                  stream)
+        x_prev, first = x0, 0
+    else:
+        x = dust.blocks[entry].detach().to(F32).repeat(n, 1, 1).contiguous()
+        ve = dust.outputs.get(f'value_embeds.{entry}')
+        ve = None if ve is None else ve.detach().repeat(n, 1, 1)
+        sites = {key: jitter.get(site.format(entry)) for key, site in SITES.items()}
+        x_prev = block_forward_eager(x, dust.weights[entry], ve, cos, sin, model.window_sizes[entry][0], **sites)
+        if entry == L - 1:
+            loss = head_loss_eager(x_prev, model.lm_head.weight.detach().float(), dust.y.repeat(n, 1),
+                                   model.config.vocab_size)
+            return loss.view(n, b, T)
+        x0 = dust.x0.detach().to(F32).repeat(n, 1, 1).contiguous()
+        first = entry + 1
+    # the first block after the entry: its mixing (run.py:267-268) and norm, then the population chain
+    x_in = torch.empty(n * b, T, 512, dtype=F32, device=dev)
+    h_in = torch.empty(n * b, T, 512, dtype=BF16, device=dev)
+    _lib.call('noise_rerun_mix_norm', x_prev.data_ptr(), rows, x0.data_ptr(), rows, W.lam_r(first), W.lam_x(first),
+              rows, x_in.data_ptr(), h_in.data_ptr(), stream)
+    idx = dust.x.to(device=dev, dtype=torch.int64).repeat(n, 1).contiguous()
+    targets = dust.y.to(device=dev, dtype=torch.int64).repeat(n, 1).contiguous()
+    rope = (cos.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous(),
+            sin.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous())
+    loss = blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=rope)
+    return loss.view(n, b, T)
+
+
+def rerun_tiled(dust, n, entry, jitter):
+    """DUST.rerun (run.py:256-279) with every block on noise_dust_block (the tiled kernels): the form `rerun`
+    replaced, kept as its cross-check and as the baseline the rerun benchmark times it against. Same arguments,
+    state and result as rerun.
 
     `dust` carries what the reference's DUST object holds after capture: model (resid_lambdas, x0_lambdas,
     window_sizes, lm_head, config), length, batch, outputs ('transformer.wte' and 'value_embeds.{i}' outputs),

@@ -407,6 +407,85 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     return out
 
 
+def blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=None, buffers=None):
+    """Per-token losses [m, T] of the fixed (unperturbed) model run from block `first` on m token rows: the
+    blocks first .. L-1 on the population kernels (the same launches as population_forward's fused path), the
+    final norm and the head (fp32 as split-bf16x3 when W.fp32_head), the soft cap and CE (ignore_index -1).
+
+    x_in: fp32 [m, T, 512], block `first`'s input after its mixing; h_in: bf16 [m, T, 512] = norm(x_in); x0:
+    fp32 [m, T, 512], the normed embedding every block mixes in; idx, targets: [m, T] int64 (one token row per
+    member: the value embeddings of blocks with them, and the head's targets). DUST's rerun runs the blocks
+    after its jittered one this way (run.py:265-278)."""
+    dev = W.device
+    m, T = idx.shape
+    E = N_EMBD
+    L = W.n_layer
+    if T % 256 or targets.shape != idx.shape:
+        raise ValueError(f'blocks_forward: [members, T] rows with T a multiple of 256; got {tuple(idx.shape)}, '
+                         f'{tuple(targets.shape)}')
+    if not 0 <= first < L:
+        raise ValueError(f'blocks_forward: first block {first} outside 0 .. {L - 1}')
+    for t, dt in ((x_in, F32), (h_in, BF16), (x0, F32)):
+        if t.shape != (m, T, E) or t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f'blocks_forward: x_in, x0 fp32 and h_in bf16, contiguous [{m}, {T}, {E}]')
+    idx = idx.to(device=dev, dtype=torch.int64).contiguous()
+    targets = targets.to(device=dev, dtype=torch.int64).contiguous()
+    stream = _lib.stream_ptr(dev)
+    sign = torch.zeros(m, dtype=F32, device=dev)
+    pop = _lib.Population(m, T, sign.data_ptr(), 1, _lib.ROUNDING_FUSED)
+    popp = ctypes.byref(pop)
+    cos_t, sin_t = rope if rope is not None else _rope_tables(T, dev)
+    B = buffers if buffers is not None else _Buffers(m, T, dev, W.fp32_head, True)
+    none = _lib.Rank1(None, None, 0, 0)
+    none3 = _rank1_array([None, None, None])
+    qkv_out = (ctypes.c_void_p * 3)(*(B.qkv[i].data_ptr() for i in range(3)))
+    x0v = _view(x0, T * E, E)
+    # block `first`: its value-embedding gates and q/k/v from h_in
+    blk = W.blocks[first]
+    ws = (ctypes.c_void_p * 3)(blk['q'].data_ptr(), blk['k'].data_ptr(), blk['v'].data_ptr())
+    if 've' in blk:
+        _call('noise_pop_gate', popp, _view(h_in, T * E, E), blk['gate'].data_ptr(), ctypes.byref(none),
+              B.gates.data_ptr(), stream)
+    _call('noise_pop_qkv', popp, _view(h_in, T * E, E), ws, none3, B.d_qkv.data_ptr(), cos_t.data_ptr(),
+          sin_t.data_ptr(), blk['ve'].data_ptr() if 've' in blk else None, blk['ve'].shape[0] if 've' in blk else 0,
+          idx.data_ptr(), T, B.gates.data_ptr() if 've' in blk else None, ctypes.byref(none), qkv_out, stream)
+    for i in range(first, L):
+        blk = W.blocks[i]
+        q4, k4 = (B.qkv[j].transpose(1, 2) for j in range(2))
+        vt = B.qkv[2].view(m, N_HEAD, HEAD_DIM, T)
+        yv = B.y.view(m, T, N_HEAD, HEAD_DIM)
+        _call('noise_attention_fwd', q4.data_ptr(), k4.data_ptr(), vt.data_ptr(), yv.data_ptr(), m, N_HEAD, T,
+              HEAD_DIM, q4.stride(0), q4.stride(2), q4.stride(1), k4.stride(0), k4.stride(2), k4.stride(1),
+              vt.stride(0), vt.stride(1), vt.stride(2), ATTN_V_TRANSPOSED | ATTN_QK_NORMED,
+              yv.stride(0), yv.stride(2), yv.stride(1), W.windows[i], 1.0 / math.sqrt(HEAD_DIM), None, 0, 1, None,
+              stream, label=f'window {W.windows[i]}')
+        xres = _view(x_in, T * E, E) if i == first else _view(B.resid, T * E, E)
+        if i < L - 1:
+            # the block, then the next block's mixing, norm, gates and q/k/v (norm and dots stay in registers)
+            nblk = W.blocks[i + 1]
+            nws = (ctypes.c_void_p * 3)(nblk['q_blk'].data_ptr(), nblk['k_blk'].data_ptr(), nblk['v_blk'].data_ptr())
+            _call('noise_pop_block_qkv', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), ctypes.byref(none),
+                  B.d_attn.data_ptr(), N_HEAD, xres, blk['fc_blk'].data_ptr(), ctypes.byref(none),
+                  blk['mp_blk'].data_ptr(), ctypes.byref(none), B.resid.data_ptr(), 1, W.lam_r(i + 1),
+                  W.lam_x(i + 1), None, None, 0, x0v, nws, none3, cos_t.data_ptr(), sin_t.data_ptr(),
+                  nblk['ve'].data_ptr() if 've' in nblk else None, nblk['ve'].shape[0] if 've' in nblk else 0,
+                  idx.data_ptr(), T, nblk['gate'].data_ptr() if 've' in nblk else None, ctypes.byref(none),
+                  ctypes.byref(none), qkv_out, stream, label='block')
+        else:
+            hout, split3 = (B.h3, 1) if W.fp32_head else (B.h, 0)
+            _call('noise_pop_block', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), ctypes.byref(none),
+                  B.d_attn.data_ptr(), N_HEAD, xres, blk['fc_blk'].data_ptr(), ctypes.byref(none),
+                  blk['mp_blk'].data_ptr(), ctypes.byref(none), None, 0, None, None, None, None, 0, x0v,
+                  hout.data_ptr(), split3, None, 0, None, stream, label='block')
+    if W.fp32_head:
+        hx, hw, K = _view(B.h3, T * 3 * E, 3 * E), W.lm_head3, 3 * E
+    else:
+        hx, hw, K = _view(B.h, T * E, E), W.lm_head, E
+    _call('noise_pop_head_ce', popp, hx, hw.data_ptr(), K, VOCAB, ctypes.byref(none), B.d_head.data_ptr(),
+          targets.data_ptr(), T, B.loss_tok.data_ptr(), stream)
+    return B.loss_tok.view(m, T)
+
+
 def population_loss(model, p, noise, sign, idx, targets, dir_div=1, fp32_head=False):
     """eggroll.py:66-103 `population_loss(model, p, noise, sign, idx, targets)` on the GPU: the mean
     cross-entropy [m] of m perturbed models on one sequence.

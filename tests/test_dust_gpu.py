@@ -136,10 +136,11 @@ def test_draw_errors_matches_oracle(d):
     assert np.all(np.abs(got - ref) <= step)
 
 
+@pytest.mark.parametrize('impl', ['rerun', 'rerun_tiled'])
 @pytest.mark.parametrize('entry,site,width', [(None, 'transformer.wte', 512), (3, 'transformer.h.{}.mlp.c_fc', 2048),
                                               (6, 'o@{}', 512), (7, 'transformer.h.{}.mlp.c_proj', 512)],
                          ids=['embedding', 'fc-3', 'o-6', 'mlp-7'])
-def test_rerun_matches_oracle(entry, site, width):
+def test_rerun_matches_oracle(entry, site, width, impl):
     """DUST.rerun (run.py:256-279) end to end -- the cached input repeated n times (or the jittered embedding
     entry), the later blocks' mixing, block_forward with the entry's jitter, the final norm and fp32 head --
     against the oracle rerun composed from the pinned pieces (oracle/dust.py), per draw and per token. The
@@ -148,9 +149,11 @@ def test_rerun_matches_oracle(entry, site, width):
     within 1e-3 of the fp32 oracle, and so does the jitter's effect (rerun minus the unjittered rerun, the
     reward DUST forms) per draw. Per token, bf16 products and attention through up to 8 blocks (the
     reference's autocast numerics) put single tokens up to 2e-2 from fp32 (measured 1.95e-2 from the
-    embedding): the per-token bound is 3e-2."""
+    embedding): the per-token bound is 3e-2. Both forms: rerun (the blocks after the entry on the population
+    kernels) and rerun_tiled (every block on noise_dust_block)."""
     from types import SimpleNamespace
-    from noise_amd.dust import rerun
+    import noise_amd.dust as ndust
+    rerun = getattr(ndust, impl)
     from noise_amd.model import make_model
     model = make_model('cpu', 0)
     with torch.no_grad():
@@ -172,7 +175,7 @@ def test_rerun_matches_oracle(entry, site, width):
     m = model.to(dev)
     to = lambda d: {k: v.to(dev) for k, v in d.items()}
     dust = SimpleNamespace(model=m, length=T, batch=b, outputs=to(cache['outputs']),
-                           blocks=to(cache['blocks']), x0=cache['x0'].to(dev), y=y.to(dev),
+                           blocks=to(cache['blocks']), x0=cache['x0'].to(dev), x=x.to(dev), y=y.to(dev),
                            weights=[{k: (None if v is None else v.to(dev)) for k, v in odust.block_weights(P, i).items()}
                                     for i in range(8)])
     got = rerun(dust, n, entry, to(jitter)).cpu()
@@ -250,7 +253,7 @@ def test_direct_errors_matches_oracle(monkeypatch, entry, sites, prior_sites, ga
     m = model.to(dev)
     dust = SimpleNamespace(
         model=m, length=T, batch=b, outputs=to(cache['outputs']), blocks=to(cache['blocks']), x0=cache['x0'].to(dev),
-        y=y.to(dev), clean_loss=clean.to(dev), dtype=torch.bfloat16, recipe=SimpleNamespace(nrep=nrep),
+        x=x.to(dev), y=y.to(dev), clean_loss=clean.to(dev), dtype=torch.bfloat16, recipe=SimpleNamespace(nrep=nrep),
         weights=[{k: (None if v is None else v.to(dev)) for k, v in odust.block_weights(P, i).items()} for i in range(8)],
         alpha=alpha, estimates={}, fits={}, prior_sites=list(prior_sites), orthogonal_noise=orthogonal_noise)
     got = ndust.direct_errors(dust, sites, draws, sigma, entry=entry, gamma=gamma, retrieved=to(retrieved))
