@@ -511,6 +511,23 @@ def bench_dust_rerun(args):
             torch.cuda.synchronize()
         timings[name] = (s.elapsed_time(e) / args.steps, loss.clone())
     ms, loss = timings['rerun']
+    # per-kernel HIP events over one more call: the population kernels of the blocks after the entry (and the
+    # rest of the call: the jittered entry block, the mixing and the copies)
+    from noise_amd import eggroll as eg
+    timer = eg.KernelTimer()
+    eg.set_timer(timer)
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.no_grad():
+        s.record()
+        ndust.rerun(state, n, 0, jit)
+        e.record()
+    torch.cuda.synchronize()
+    eg.set_timer(None)
+    kernels = {}
+    for (kname, label), (cnt, kms) in timer.totals().items():
+        kernels[kname if label is None else f'{kname}[{label}]'] = dict(launches=cnt, ms=round(kms, 4))
+    kernels['other (entry block, mixing, copies)'] = dict(ms=round(s.elapsed_time(e) - sum(
+        v['ms'] for v in kernels.values()), 4))
     wins = window_sizes(8)
     gemm = 2 * (512 * 1536 + 512 * 512 + 2 * 512 * 2048)
     flops = sum(gemm + 4 * 64 * 8 * visible_pairs(T, w) / T for w in wins) + 2 * 512 * 4096
@@ -526,6 +543,7 @@ def bench_dust_rerun(args):
         speedup_vs_tiled=round(tiled_ms / ms, 3),
         roofline=dict(bound='mfma', achieved=round(flops / ms / 1e9, 1), peak=BF16_PEAK / 1e12, unit='TFLOP/s',
                       frac=round(flops / ms / 1e9 / (BF16_PEAK / 1e12), 4), traffic=None),
+        kernels=kernels,
         mean_loss=round(loss.mean().item(), 6), max_abs_vs_tiled=float((loss - tiled_loss).abs().max()),
         mean_abs_vs_tiled=float((loss.mean(-1) - tiled_loss.mean(-1)).abs().max()),
         finite=bool(torch.isfinite(loss).all().item()))), flush=True)

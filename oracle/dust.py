@@ -206,3 +206,53 @@ def direct_errors(draw, rerun_fn, clean_loss, live, sites, widths, draws, sigma,
         record.append(dict(loss=loss, reward=reward, predicted=predicted, sums=sums, a=a))
     kept = 1 - 1 / n if n > 1 else 1.0
     return {s: e / draws + kept * priors.get(s, 0.0) for s, e in est.items()}, record
+
+
+def block_forward_bf16_flow(x, w, ve, cos, sin, window, o=None, attn=None, fc=None, mlp=None):
+    """run.py:102-117 with the dtype flow the reference's compiled block_forward has on a GPU under bf16 autocast,
+    for bf16-valued x: fp32 inside every fused elementwise chain, bf16 at every linear output (weights rounded to
+    bf16) and at every tensor the graph stores (norm outputs, q and k after rotary and norm, v with its gated
+    value embedding, the attention output, x_mid, ReLU^2, the block output). fp32 CPU tensors holding bf16 values."""
+    import torch
+    import torch.nn.functional as F
+    from .model import norm, apply_rotary_emb, attention, bf16, N_HEAD, HEAD_DIM
+    add = lambda t, j: t if j is None else t + j.float()
+    B, T, C = x.shape
+    W = {k: (None if v is None else bf16(v.float())) for k, v in w.items()}
+    lin = lambda u, name: bf16(u @ W[name].t())
+    h = bf16(norm(x))
+    q, k, v = (lin(h, n).view(B, T, N_HEAD, HEAD_DIM) for n in ('q', 'k', 'v'))
+    if ve is not None:
+        gate = 2 * torch.sigmoid(lin(h[..., :W['gate'].shape[1]], 'gate'))
+        v = bf16(v + gate.unsqueeze(-1) * ve.float().view(B, T, N_HEAD, HEAD_DIM))
+    q, k = bf16(norm(apply_rotary_emb(q, cos, sin))), bf16(norm(apply_rotary_emb(k, cos, sin)))
+    y = bf16(add(bf16(attention(q, k, v, window)).reshape(B, T, C), o))
+    x = bf16(x + add(lin(y, 'proj'), attn))
+    act = bf16(F.relu(add(lin(bf16(norm(x)), 'fc'), fc)).square())
+    return bf16(x + add(lin(act, 'out'), mlp))
+
+
+def rerun_bf16_flow(P, cache, y, n, entry, jitter):
+    """DUST.rerun (run.py:256-279) with the dtype flow it has on a GPU: the model's embeddings stored in bf16
+    (utils/model.py:171-175), so the captured embedding, block inputs, x0 and value-embedding outputs are bf16;
+    the mixing between blocks in bf16 (a 0-dim fp32 lambda times a bf16 tensor rounds the lambda and each
+    product, then the sum); block_forward_bf16_flow; the final norm, head and loss in fp32. cache: capture() of
+    the model with bf16-rounded embedding tables. Per-token losses [n, b, T]."""
+    from .model import norm, bf16, rotary_tables, window_sizes, head_loss, N_LAYER
+    b, T = y.shape
+    cos, sin = rotary_tables(T)
+    wins = window_sizes()
+    mix = lambda i, u, u0: bf16(bf16(bf16(P['resid_lambdas'][i]) * u) + bf16(bf16(P['x0_lambdas'][i]) * u0))
+    if entry is None:
+        x = x0 = bf16(norm(bf16(bf16(cache['outputs']['transformer.wte']).repeat(n, 1, 1)
+                                + jitter['transformer.wte'].float())))
+    else:
+        x, x0 = bf16(cache['blocks'][entry]).repeat(n, 1, 1), bf16(cache['x0']).repeat(n, 1, 1)
+    for i in range(entry or 0, N_LAYER):
+        if entry is None or i > entry:
+            x = mix(i, x, x0)
+        ve = cache['outputs'].get(f'value_embeds.{i}')
+        sites = {k: jitter.get(s.format(i)) for k, s in SITES.items()} if i == entry else {}
+        x = block_forward_bf16_flow(x, block_weights(P, i), None if ve is None else bf16(ve).repeat(n, 1, 1), cos,
+                                    sin, wins[i], **sites)
+    return head_loss(x, P['lm_head.weight'], y.repeat(n, 1)).view(n, b, T)

@@ -265,3 +265,30 @@ def test_direct_errors_oracle_priors_and_centring():
     u0, _, _, _ = _linear_case(64, 64, 1)
     u1, _, _, _ = _linear_case(64, 64, 1, offset=0.37)
     assert np.abs(u1 - u0).max() > 0.01
+
+
+def test_rerun_bf16_flow_reduces_to_the_fp32_rerun(monkeypatch):
+    """The oracle's GPU-dtype-flow rerun (bf16 storage and stores, fp32 inside fused chains) is the fp32 rerun
+    once its bf16 rounding is the identity; with rounding, every block output it produces is bf16-valued."""
+    import torch
+    import oracle.model as om
+    from noise_amd.model import make_model
+    P = {k: v.detach().float().clone() for k, v in make_model('cpu', 0).named_parameters()}
+    P['lm_head.weight'] = P['lm_head.weight'] * 30
+    g = torch.Generator().manual_seed(3)
+    rows = torch.randint(0, 4096, (1, 257), generator=g)
+    x, y = rows[:, :-1], rows[:, 1:]
+    cache = odust.capture(P, x)
+    jit = {'transformer.h.6.mlp.c_fc': (0.1 * (torch.randint(0, 2, (2, 256, 2048), generator=g) * 2 - 1)).bfloat16()}
+    flow = odust.rerun_bf16_flow(P, cache, y, 2, 6, jit)
+    with monkeypatch.context() as mp:
+        mp.setattr(om, 'bf16', lambda t: t)
+        ident = odust.rerun_bf16_flow(P, cache, y, 2, 6, jit)
+    ref = odust.rerun(P, cache, y, 2, 6, jit)
+    assert (ident - ref).abs().max().item() <= 1e-4
+    assert (flow - ref).abs().max().item() > 1e-5        # the rounding matters
+    from oracle.model import rotary_tables, window_sizes
+    cos, sin = rotary_tables(256)
+    out = odust.block_forward_bf16_flow(cache['blocks'][6].bfloat16().float(), odust.block_weights(P, 6), None, cos,
+                                        sin, window_sizes()[6])
+    assert torch.equal(out, out.bfloat16().float())

@@ -311,3 +311,50 @@ def test_direct_errors_matches_oracle(monkeypatch, entry, sites, prior_sites, ga
         assert abs(rr - (r * r).sum()) <= 1e-4 * (r * r).sum()
         assert abs(dot - (r * got[s] / kept).sum()) <= 1e-3 * np.abs(r * got[s] / kept).sum()
 
+
+
+@pytest.mark.parametrize('entry,site,width', [(3, 'transformer.h.{}.mlp.c_fc', 2048), (6, 'o@{}', 512)],
+                         ids=['fc-3', 'o-6'])
+def test_rerun_fp32_stream_against_the_bf16_flow(entry, site, width):
+    """The reference's DUST on a GPU keeps the model's embeddings in bf16 (utils/model.py:171-175), so its cached
+    block inputs, x0 and value rows are bf16 and, under autocast, its residual stream is bf16 between blocks
+    (oracle/dust.py rerun_bf16_flow). rerun keeps the stream in fp32 (the population kernels' residual). Measured
+    here on the bf16-valued cache the reference would hold: the per-draw mean losses and the jitter's effect
+    (rerun minus the unjittered rerun: the reward direct_errors forms, centred over draws) against that flow.
+    Bounds: per-draw mean within 2e-3, the jitter's effect within 1e-3 (measured ~1e-3 and ~2e-4); the printed
+    sizes are the deviation the fp32 stream brings against the reference's own GPU numerics."""
+    from types import SimpleNamespace
+    from noise_amd.dust import rerun
+    from noise_amd.model import make_model
+    model = make_model('cpu', 0)
+    with torch.no_grad():
+        model.lm_head.weight.mul_(30)
+        for emb in [model.transformer.wte, *model.value_embeds.values()]:
+            emb.weight.copy_(emb.weight.bfloat16().float())       # bf16 storage, as on a GPU
+    P = {k: v.detach().float().clone() for k, v in model.named_parameters()}
+    g = torch.Generator().manual_seed(51)
+    b, T, n = 2, 256, 3
+    rows = torch.randint(0, 4096, (b, T + 1), generator=g)
+    x, y = rows[:, :-1], rows[:, 1:]
+    cache = odust.capture(P, x)
+    bf = lambda t: t.bfloat16()
+    name = site.format(entry)
+    jitter = {name: (0.1 * (torch.randint(0, 2, (n * b, T, width), generator=g) * 2 - 1)).bfloat16()}
+    flow = odust.rerun_bf16_flow(P, cache, y, n, entry, jitter)
+    flow0 = odust.rerun_bf16_flow(P, cache, y, n, entry, {})
+    dev = torch.device('cuda', 0)
+    m = model.to(dev)
+    dust = SimpleNamespace(model=m, length=T, batch=b, x=x.to(dev), y=y.to(dev),
+                           outputs={k: bf(v).to(dev) for k, v in cache['outputs'].items()},
+                           blocks={k: bf(v).to(dev) for k, v in cache['blocks'].items()}, x0=bf(cache['x0']).to(dev),
+                           weights=[{k: (None if v is None else v.to(dev)) for k, v in odust.block_weights(P, i).items()}
+                                    for i in range(8)])
+    got = rerun(dust, n, entry, {k: v.to(dev) for k, v in jitter.items()}).cpu()
+    got0 = rerun(dust, n, entry, {}).cpu()
+    mean = (got.mean(-1) - flow.mean(-1)).abs().max().item()
+    eff = ((got - got0).mean(-1) - (flow - flow0).mean(-1)).abs().max().item()
+    tok = (got - flow).abs().max().item()
+    size = (flow - flow0).mean(-1).abs().max().item()
+    print(f'fp32 stream vs the bf16 flow: per-draw mean {mean:.2e}, jitter effect {eff:.2e} (effect size '
+          f'{size:.2e}), per token {tok:.2e}', flush=True)
+    assert mean <= 2e-3 and eff <= 1e-3
