@@ -256,14 +256,14 @@ def main():
             W = eg.Weights(P, fp32_head=True)
             return eg.orthogonal_population(W, tables, x, y, sigma=SIGMA, chunk=chunk), tables
         offsets = es.offsets(0)
-        tables = {}
         if gather_events is not None:
+            # the GPU spins briefly first, so the host has queued the launch and both events before the start
+            # event runs: the interval is the kernel's own time, not the host's launch latency after a sync
+            if hasattr(torch.cuda, '_sleep'):
+                torch.cuda._sleep(2_000_000)
             ev = (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
             ev[0].record()
-        for n in names:
-            p = es.params[n]
-            rows = es.buffer.gather(offsets[n], sum(p.shape), rows=directions)
-            tables[n] = tuple(rows.split(list(p.shape), dim=1))
+        tables = es.noise_tables({n: offsets[n] for n in names}, directions)
         if gather_events is not None:
             ev[1].record()
             gather_events.append(ev)
@@ -299,10 +299,11 @@ def main():
         kernels[key] = entry
     if gather_events:
         # the noise regeneration replacing the reference's buffer gather (eggroll.py:114, 126-127): one
-        # noise_gather_slices launch per perturbed matrix, writing its directions' a and b rows in fp32
+        # noise_gather_slice_groups launch for the 48 perturbed matrices, writing their directions' a and b rows
+        # in fp32
         ms = sum(s_.elapsed_time(e_) for s_, e_ in gather_events) / len(gather_events)
         written = 4 * len(directions) * sum(sum(shapes[n]) for n in names)
-        kernels['noise_gather_slices'] = dict(launches=len(names), ms_per_step=round(ms, 4), bytes_written=written,
+        kernels['noise_gather_slice_groups'] = dict(launches=1, ms_per_step=round(ms, 4), bytes_written=written,
                                               gbps=round(written / ms / 1e6, 1),
                                               hbm_frac=round(written / ms / 1e6 / (HBM_PEAK / 1e9), 4))
     timed = [k for k in kernels if 'tflops' in kernels[k]]

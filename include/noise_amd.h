@@ -65,6 +65,22 @@ int noise_randint(int64_t *out, int64_t n, uint64_t seed, uint64_t offset, int64
 int noise_gather_slices(float *out, int64_t nrows, int64_t width, const int64_t *offsets, const int64_t *rows,
                         int64_t numel, uint64_t seed, uint64_t offset, int64_t threads, noise_stream_t stream);
 
+/* Several parameters' slices in one launch (Eggroll.noise's gathers for every perturbed parameter of a step,
+ * eggroll.py:126-127, at the same directions): group k writes element (offsets[k][rows[r]] + j) of the draw to
+ * out[r * ld + col[k] + j] for j < width[k]. Groups are packed in order (col[0] = 0, col[k+1] = col[k] +
+ * width[k]), widths are multiples of 256, ld >= the total width; out-of-range elements are NaN as in
+ * noise_gather_slices. The descriptor is passed by value to the kernel (no device copy). */
+#define NOISE_SLICE_GROUPS_MAX 64
+typedef struct {
+    int32_t count;
+    const int64_t *offsets[NOISE_SLICE_GROUPS_MAX];
+    int64_t width[NOISE_SLICE_GROUPS_MAX];
+    int64_t col[NOISE_SLICE_GROUPS_MAX];
+} noise_slice_groups_t;
+int noise_gather_slice_groups(float *out, int64_t nrows, int64_t ld, const noise_slice_groups_t *groups,
+                              const int64_t *rows, int64_t numel, uint64_t seed, uint64_t offset, int64_t threads,
+                              noise_stream_t stream);
+
 /* Orthogonal draws of DUST.orthogonal_noise (run.py:223-238; hadamard run.py:143-152): out[i][f][j] for
  * draws i < n, frame positions f < bt (the reference's b*t tokens) and coordinates j < d (a power of two):
  *   index = index0 + i (the reference's rank*draws + chunk*n + i), row = (offset[f] + index) mod d,

@@ -13,6 +13,7 @@ SIGNATURES = {
     'noise_normal_fill': [_p, _i64, _i64, _u64, _u64, _i64, _f32, _f32, _p],
     'noise_randint': [_p, _i64, _u64, _u64, _i64, _u64, _i64, _p],
     'noise_gather_slices': [_p, _i64, _i64, _p, _p, _i64, _u64, _u64, _i64, _p],
+    'noise_gather_slice_groups': [_p, _i64, _i64, _p, _p, _i64, _u64, _u64, _i64, _p],
     'noise_orthogonal_draws': [_p, _i32, _i64, _i64, _i64, _i64, _p, _p, _i64, _p, _p],
     'noise_attention_fwd': [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
                             _i64, _i64, _i64, _i32, _i64, _i64, _i64, _i64, _f32, _p, _i64, _i64, _p, _p],
@@ -84,6 +85,15 @@ class Population(ctypes.Structure):
     """noise_population_t (rounding: ROUNDING_FUSED, the default, or ROUNDING_EAGER)."""
     _fields_ = [('members', ctypes.c_int64), ('tokens', ctypes.c_int64), ('sign', ctypes.c_void_p),
                 ('dir_div', ctypes.c_int64), ('rounding', ctypes.c_int64)]
+
+
+SLICE_GROUPS_MAX = 64  # NOISE_SLICE_GROUPS_MAX
+
+
+class SliceGroups(ctypes.Structure):
+    """noise_slice_groups_t: up to 64 parameters' [pairs] offsets, widths and output columns."""
+    _fields_ = [('count', ctypes.c_int32), ('offsets', ctypes.c_void_p * SLICE_GROUPS_MAX),
+                ('width', ctypes.c_int64 * SLICE_GROUPS_MAX), ('col', ctypes.c_int64 * SLICE_GROUPS_MAX)]
 
 
 class UpdateParam(ctypes.Structure):

@@ -76,6 +76,23 @@ __global__ __launch_bounds__(kBlock) void gather_slices_kernel(float *__restrict
     out[r * width + j] = v;
 }
 
+// The slices of several parameters in one launch: group k's elements (offsets_k[rows[r]] + j) for j < width_k
+// go to out[r * ld + col_k + j]. grid = (widest group / kBlock, rows, groups): blockIdx.z is the group, so its
+// descriptor entries are one uniform load each; the blocks past a narrower group's width exit at once.
+__global__ __launch_bounds__(kBlock) void gather_groups_kernel(float *__restrict__ out, int64_t ld,
+                                                               noise_slice_groups_t g,
+                                                               const int64_t *__restrict__ rows, int64_t numel,
+                                                               DrawLayout d) {
+    const int k = blockIdx.z;
+    const int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    if (j >= g.width[k]) return;
+    const int64_t r = blockIdx.y;
+    const int64_t src = rows ? rows[r] : r;
+    const int64_t L = g.offsets[k][src] + j;
+    const float v = (L >= 0 && L < numel) ? draw_normal(d, (uint64_t)L, 0.0f, 1.0f) : __builtin_nanf("");
+    out[r * ld + g.col[k] + j] = v;
+}
+
 // Orthogonal draws (run.py:223-238): out[(i * bt + f) * d + j] = H[row][j] * pattern * sign with
 // H[r][j] = (-1)^popcount(r & j), the Sylvester Hadamard matrix of run.py:143-152 (its recursion
 // [[H, H], [H, -H]] flips the sign exactly where both indices have the new top bit set).
@@ -188,6 +205,38 @@ extern "C" int noise_gather_slices(float *out, int64_t nrows, int64_t width, con
     hipLaunchKernelGGL(gather_slices_kernel, grid, dim3(kBlock), 0, (hipStream_t)stream, out, width, offsets, rows,
                        numel, d);
     return launch_status("noise_gather_slices");
+}
+
+extern "C" int noise_gather_slice_groups(float *out, int64_t nrows, int64_t ld, const noise_slice_groups_t *groups,
+                                         const int64_t *rows, int64_t numel, uint64_t seed, uint64_t offset,
+                                         int64_t threads, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_gather_slice_groups";
+    NOISE_CHECK_ARG(groups != nullptr, "%s: groups NULL", fn);
+    const noise_slice_groups_t g = *groups;
+    NOISE_CHECK_ARG(g.count >= 1 && g.count <= NOISE_SLICE_GROUPS_MAX, "%s: 1 .. %d groups, got %d", fn,
+                    NOISE_SLICE_GROUPS_MAX, g.count);
+    NOISE_CHECK_ARG(nrows >= 0 && nrows <= 65535, "%s: 0 .. 65535 rows per call, got %lld", fn, (long long)nrows);
+    NOISE_CHECK_ARG(threads > 0 && threads % 256 == 0, "%s: threads must be a positive multiple of 256", fn);
+    NOISE_CHECK_ARG(offset % 4 == 0, "%s: generator offset must be a multiple of 4", fn);
+    NOISE_CHECK_ARG(numel > 0, "%s: numel must be positive", fn);
+    int64_t end = 0, widest = 0;
+    for (int k = 0; k < g.count; ++k) {
+        NOISE_CHECK_ARG(g.offsets[k] != nullptr && g.width[k] > 0 && g.width[k] % kBlock == 0 && g.col[k] == end,
+                        "%s: group %d needs offsets, a width that is a positive multiple of %d, and to start at "
+                        "column %lld (groups are packed in order)", fn, k, kBlock, (long long)end);
+        end += g.width[k];
+        widest = g.width[k] > widest ? g.width[k] : widest;
+    }
+    NOISE_CHECK_ARG(ld >= end, "%s: row stride %lld below the groups' total width %lld", fn, (long long)ld,
+                    (long long)end);
+    if (nrows == 0) return NOISE_OK;
+    NOISE_CHECK_ARG(out != nullptr, "%s: out NULL", fn);
+    DrawLayout d{seed, offset, (uint64_t)threads};
+    NOISE_CHECK_ARG(widest / kBlock <= 65535, "%s: a group wider than %d columns", fn, 65535 * kBlock);
+    dim3 grid((unsigned)(widest / kBlock), (unsigned)nrows, (unsigned)g.count);
+    hipLaunchKernelGGL(gather_groups_kernel, grid, dim3(kBlock), 0, (hipStream_t)stream, out, ld, g, rows, numel, d);
+    return launch_status(fn);
 }
 
 extern "C" int noise_orthogonal_draws(void *out, int out_bf16, int64_t n, int64_t bt, int64_t d, int64_t index0,

@@ -49,12 +49,22 @@ struct DrawLayout {
 };
 
 __host__ __device__ inline Philox4 draw_block(const DrawLayout &d, uint64_t L, int *lane) {
-    uint64_t four_s = 4 * d.threads;
-    uint64_t k = L / four_s;
-    uint64_t r = L - k * four_s;
-    uint64_t q = r / d.threads;
-    uint64_t t = r - q * d.threads;
-    *lane = (int)q;
+    uint64_t k, t;
+    if ((d.threads & (d.threads - 1)) == 0) {
+        // S a power of two (torch's grid on MI355X is 2048 blocks: S = 2^19): shifts and masks instead of two
+        // 64-bit divisions, the larger part of a regenerated element's integer work besides Philox itself
+        const int s = __builtin_ctzll(d.threads);
+        k = L >> (s + 2);
+        *lane = (int)((L >> s) & 3);
+        t = L & (d.threads - 1);
+    } else {
+        const uint64_t four_s = 4 * d.threads;
+        k = L / four_s;
+        const uint64_t r = L - k * four_s;
+        const uint64_t q = r / d.threads;
+        t = r - q * d.threads;
+        *lane = (int)q;
+    }
     uint64_t c = d.offset / 4 + k;
     return philox4x32_10((uint32_t)c, (uint32_t)(c >> 32), (uint32_t)t, (uint32_t)(t >> 32),
                          (uint32_t)d.seed, (uint32_t)(d.seed >> 32));

@@ -661,6 +661,28 @@ class Eggroll:
             out[name] = tuple(rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
         return out
 
+    def noise_tables(self, offsets, directions):
+        """Eggroll.noise's values for the parameters in `offsets` at `directions`, regenerated in one launch for
+        the matrices whose rows are whole multiples of 256 (every block matrix and the head: a [dirs, sum of
+        out + in] table, each parameter's a and b column views of it) and per parameter for the rest."""
+        out = {}
+        grouped = [n for n in offsets if self.params[n].dim() == 2 and sum(self.params[n].shape) % 256 == 0]
+        if grouped:
+            widths = [sum(self.params[n].shape) for n in grouped]
+            table = self.buffer.gather_many([offsets[n] for n in grouped], widths, directions)
+            col = 0
+            for n, w in zip(grouped, widths):
+                o, i = self.params[n].shape
+                out[n] = (table[:, col:col + o], table[:, col + o:col + w])
+                col += w
+        for name, o in offsets.items():
+            if name in out:
+                continue
+            p = self.params[name]
+            rows = self.buffer.gather(o, sum(p.shape), rows=directions)
+            out[name] = tuple(rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
+        return out
+
     def population(self, step, x, y, weights=None, chunk=512, names=None, fp32_head=False):
         """This rank's population losses for one update (the hot loop of eggroll.py:133-146): members
         [rank * per_rank, (rank + 1) * per_rank), member g on direction (g mod 2P) // 2 with sign
@@ -676,11 +698,7 @@ class Eggroll:
         losses = torch.empty(per_rank, device=self.device)
         for start, n, _, seq in plan:
             directions = (torch.arange(start, start + n, 2, device=self.device) % (2 * pairs)) // 2
-            noise = {}
-            for name, o in offsets.items():
-                p = self.params[name]
-                rows = self.buffer.gather(o, sum(p.shape), rows=directions)
-                noise[name] = tuple(rows.split(list(p.shape), dim=1)) if p.dim() == 2 else rows
+            noise = self.noise_tables(offsets, directions)
             sign = _pair_signs(n // 2, SIGMA, self.device)
             losses[start - self.rank * per_rank:start - self.rank * per_rank + n] = population_forward(
                 W, noise, sign, x[seq], y[seq], dir_div=2)

@@ -76,7 +76,8 @@ def test_ctypes_signatures_match_the_header():
 
 
 def test_struct_layouts_match_the_header(tmp_path):
-    """The ctypes mirrors of noise_view_t, noise_rank1_t, noise_population_t and noise_update_param_t have the
+    """The ctypes mirrors of noise_view_t, noise_rank1_t, noise_population_t, noise_update_param_t and
+    noise_slice_groups_t have the
     sizes and field offsets a C compiler gives the header's structs (gcc on include/noise_amd.h)."""
     import ctypes
     import shutil
@@ -89,7 +90,7 @@ def test_struct_layouts_match_the_header(tmp_path):
     abi = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(abi)
     structs = {'noise_view_t': abi.View, 'noise_rank1_t': abi.Rank1, 'noise_population_t': abi.Population,
-               'noise_update_param_t': abi.UpdateParam}
+               'noise_update_param_t': abi.UpdateParam, 'noise_slice_groups_t': abi.SliceGroups}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "noise_amd.h"', 'int main(void) {']
     for c_name, py in structs.items():
         lines.append(f'    printf("{c_name} size %zu\\n", sizeof({c_name}));')

@@ -69,3 +69,24 @@ def test_gather_slices(dev):
     ref = buf[offsets[directions, None] + torch.arange(2560, device=dev)]
     out = draw.gather(offsets, 2560, directions)
     assert torch.equal(bits(out), bits(ref))
+
+
+def test_gather_many_equals_per_parameter_gathers(dev):
+    """One noise_gather_slice_groups launch for several parameters' slices (the step's 48 block matrices in the
+    population forward) gives each parameter's columns bit for bit what its own gather gives, over the 2^28
+    buffer's draw layout, with repeated and unordered rows; a width that is not a multiple of 256 is rejected."""
+    from noise_amd.noise import DeviceGenerator
+    from noise_amd import _lib
+    draw = DeviceGenerator(0, dev).take(2 ** 28)
+    g = torch.Generator(dev).manual_seed(7)
+    widths = [1024, 2560, 2560, 4608, 1024]
+    offsets = [torch.randint(0, 2 ** 28 - w, (300,), device=dev, generator=g) for w in widths]
+    rows = torch.tensor([5, 5, 299, 0, 17, 123, 123, 4], device=dev)
+    out = draw.gather_many(offsets, widths, rows)
+    assert out.shape == (8, sum(widths))
+    col = 0
+    for o, w in zip(offsets, widths):
+        assert torch.equal(bits(out[:, col:col + w]), bits(draw.gather(o, w, rows)))
+        col += w
+    with pytest.raises(RuntimeError, match='multiple of 256'):
+        draw.gather_many(offsets[:1], [1000], rows)
