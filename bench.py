@@ -91,11 +91,14 @@ def profiled_mfma_busy(kernel):
     name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel<true>' if kernel.startswith('noise_attention') else None)
     if not name or not os.path.exists(PROFILE):
         return None
+    col = None
     for line in open(PROFILE):
         cells = [c.strip() for c in line.strip().strip('|').split('|')]
-        if len(cells) == 11 and cells[0] == name:
+        if 'MFMA busy' in cells:
+            col = cells.index('MFMA busy')   # the counter table's header
+        elif col is not None and len(cells) > col and cells[0] == name:
             try:
-                return float(cells[2])
+                return float(cells[col])
             except ValueError:
                 return None
     return None
