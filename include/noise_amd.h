@@ -316,6 +316,30 @@ int noise_pop_block_qkv(const noise_population_t *pop, noise_view_t y, const voi
                         const int64_t *idx, int64_t idx_sm, const float *gate_w, const noise_rank1_t *gate_noise,
                         const noise_rank1_t *ve_noise, void *const out[3], noise_stream_t stream);
 
+/* DUST's jitter on a population block (block_forward, run.py:102-117, for the block a rerun enters at): bf16 rows
+ * [members * tokens][2048] added to mlp.c_fc's product before ReLU^2 (fc) and [members * tokens][512] added to
+ * mlp.c_proj's product (mlp), either may be NULL (not both); without mlp rows, zero_row is 512 zero bf16 values
+ * (16 B aligned) the kernel reads instead. The attention-output and attn.c_proj jitter go in before the call
+ * (noise_add_bf16 on y, noise_block_entry's residual). */
+typedef struct {
+    const void *fc;
+    const void *mlp;
+    const void *zero_row;
+} noise_block_jitter_t;
+
+/* noise_pop_block / noise_pop_block_qkv for an unperturbed block with jitter (no rank-1 or mixing-scalar noise,
+ * no next-matrix dots; no counterpart in the reference beyond block_forward's jitter arguments): the last block
+ * (mix 0, split3 1: the fp32 head input), or a block followed by the next block's q/k/v (mixing on). */
+int noise_pop_block_jit(const noise_population_t *pop, noise_view_t y, const void *w_o, noise_view_t xres,
+                        const void *w_fc, const void *w_proj, int mix, const float *lam_r, const float *lam_x,
+                        noise_view_t x0, void *hout, int split3, const noise_block_jitter_t *jit,
+                        noise_stream_t stream);
+int noise_pop_block_qkv_jit(const noise_population_t *pop, noise_view_t y, const void *w_o, noise_view_t xres,
+                            const void *w_fc, const void *w_proj, float *xout, const float *lam_r, const float *lam_x,
+                            noise_view_t x0, const void *const w_qkv[3], const void *rope_cos, const void *rope_sin,
+                            const float *ve, int64_t vocab, const int64_t *idx, int64_t idx_sm, const float *gate_w,
+                            void *const out[3], const noise_block_jitter_t *jit, noise_stream_t stream);
+
 /* w [rows][cols] bf16 -> the column order noise_pop_block reads: within every 32 columns, position 8g + j
  * (g < 4) holds column 4g + j for j < 4 and 16 + 4g + (j - 4) for j >= 4. cols a multiple of 32. */
 int noise_block_weight_layout(const void *w, void *out, int64_t rows, int64_t cols, noise_stream_t stream);
@@ -383,6 +407,17 @@ int noise_draw_errors(const float *reward, const void *a, int64_t n, int64_t row
  *               device: the mixing of the blocks after the entry (run.py:267-268), x0 repeated by indexing. */
 int noise_rerun_rows(const float *x, int64_t x_rows, const void *add, const float *x0, int64_t x0_rows,
                      const float *lam_r, const float *lam_x, int64_t rows, float *out, noise_stream_t stream);
+
+/* A jittered block's entry on the population kernels (DUST.rerun, run.py:265 with block_forward's attn jitter,
+ * run.py:114): out[r] = x[r mod x_rows] + add[r] (fp32; add bf16 [rows][512] or NULL: the attn.c_proj jitter
+ * folded into the residual the block adds its product to) and h[r] = bf16(norm(x[r mod x_rows])), the block's
+ * normalised input. */
+int noise_block_entry(const float *x, int64_t x_rows, const void *add, int64_t rows, float *out, void *h,
+                      noise_stream_t stream);
+
+/* y = bf16(y + add) over n bf16 elements (n a multiple of 8, 16 B aligned): block_forward's attention-output
+ * jitter (run.py:114). */
+int noise_add_bf16(void *y, const void *add, int64_t n, noise_stream_t stream);
 
 /* DUST.rerun's mixing into a block that runs on the population kernels (run.py:266-268, then the block's
  * norm(x), utils/model.py:117): out[r] = rl * x[r mod x_rows] + ml * x0[r mod x0_rows] (fp32, rl = *lam_r,

@@ -8,7 +8,7 @@ from pathlib import Path
 import torch
 
 from .abi import (SIGNATURES, LINEAR_AUTOCAST, ROUNDING_FUSED, ROUNDING_EAGER, ATTN_V_TRANSPOSED,  # noqa: F401
-                  ATTN_QK_NORMED, View, Rank1, Population, UpdateParam, SliceGroups, SLICE_GROUPS_MAX, bind)
+                  ATTN_QK_NORMED, View, Rank1, Population, UpdateParam, SliceGroups, SLICE_GROUPS_MAX, BlockJitter, bind)
 
 # the in-tree build (noise_amd/build.py); no other library is ever loaded
 LIB_PATH = Path(__file__).resolve().with_name('libnoise_amd.so')

@@ -47,6 +47,11 @@ SIGNATURES = {
     'noise_draw_errors': [_p, _p, _i64, _i64, _i64, _f32, _p, _p],
     'noise_rerun_rows': [_p, _i64, _p, _p, _i64, _p, _p, _i64, _p, _p],
     'noise_rerun_mix_norm': [_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _p],
+    'noise_block_entry': [_p, _i64, _p, _i64, _p, _p, _p],
+    'noise_add_bf16': [_p, _p, _i64, _p],
+    'noise_pop_block_jit': [_p, 'View', _p, 'View', _p, _p, _i32, _p, _p, 'View', _p, _i32, _p, _p],
+    'noise_pop_block_qkv_jit': [_p, 'View', _p, 'View', _p, _p, _p, _p, _p, 'View', _p, _p, _p, _p, _i64, _p, _i64, _p,
+                                _p, _p, _p],
     'noise_dust_block_workspace_bytes': [_i64, _i64, _i32],
     'noise_dust_block': [_p, _p, _i64, _i64, _p, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _p],
     'noise_dust_block_static_max_bytes': [],
@@ -94,6 +99,11 @@ class SliceGroups(ctypes.Structure):
     """noise_slice_groups_t: up to 64 parameters' [pairs] offsets, widths and output columns."""
     _fields_ = [('count', ctypes.c_int32), ('offsets', ctypes.c_void_p * SLICE_GROUPS_MAX),
                 ('width', ctypes.c_int64 * SLICE_GROUPS_MAX), ('col', ctypes.c_int64 * SLICE_GROUPS_MAX)]
+
+
+class BlockJitter(ctypes.Structure):
+    """noise_block_jitter_t: bf16 jitter rows added to mlp.c_fc's and mlp.c_proj's products (NULL: none)."""
+    _fields_ = [('fc', ctypes.c_void_p), ('mlp', ctypes.c_void_p), ('zero_row', ctypes.c_void_p)]
 
 
 class UpdateParam(ctypes.Structure):

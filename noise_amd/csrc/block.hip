@@ -67,6 +67,11 @@ constexpr int kVAo = kVNb + 3 * kModel * 4;      // attn.c_proj's a [512]
 constexpr int kVBfc = kVAo + kModel * 4;         // c_fc's b       [512]
 constexpr int kBlkLds = kVBfc + kModel * 4;      // 156 KiB
 static_assert(kBlkLds <= 160 * 1024, "LDS of one CU");
+// JIT (an unperturbed block with DUST's per-token jitter): the rank-1 vectors are not used, and the c_fc jitter of
+// three steps ([128 tokens][32 units] bf16, 8 KiB each) rides in their place, copied with the c_fc stages
+constexpr int kJitRing = kVAfc;
+constexpr int kJitSlot = kBlkTok * kUnits * 2;
+static_assert(kJitRing + 3 * kJitSlot <= kVAo, "the jitter ring overlaps the vectors the x_mid epilogue reads");
 constexpr int kBlkQkvLds = kBlkLds > kQLds ? kBlkLds : kQLds;  // with the next block's q/k/v phase
 
 struct BlockArgs {
@@ -98,6 +103,9 @@ struct BlockArgs {
     int64_t nb_stride[3];
     float *ndots;                          // [rows][NNEXT]
     QkvRowsArgs q;                         // the next block's q/k/v (QKV): its x is h, its dots come from the epilogue
+    const __bf16 *jfc;                     // JIT: mlp.c_fc jitter bf16 [m * T][2048] (added before ReLU^2) or NULL
+    const __bf16 *jmlp;                    // JIT: mlp.c_proj jitter bf16, row r at r * jmlp_st (added to its product)
+    int64_t jmlp_st;                       //   512, or 0 with one zero row when the block has no mlp.c_proj jitter
 };
 
 // sum over the four lanes holding one token's features (l % 16 + 16 g)
@@ -108,8 +116,12 @@ __device__ __forceinline__ float token_sum(float v) {
 
 // QKV: 0, or the next block's q/k/v after the tail (1; 2 with its value embeddings) in place of the hout and
 // next_dots stores
-template <bool MIX, int NNEXT, bool SPLIT3, int QKV>
+// JIT: the block unperturbed (no rank-1 terms) with DUST's jitter: 1 at mlp.c_fc (p.jfc, staged with the c_fc
+// stages) and optionally mlp.c_proj (p.jmlp); 2 at mlp.c_proj only
+template <bool MIX, int NNEXT, bool SPLIT3, int QKV, int JIT = 0>
 __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
+    static_assert(JIT == 0 || NNEXT == 0, "a jittered block is unperturbed: no next-matrix dots");
+    constexpr bool kJit = JIT != 0, kJitFc = JIT == 1;
     __shared__ __attribute__((aligned(16))) char lds[QKV ? kBlkQkvLds : kBlkLds];
     const int T = p.tokens, tiles_t = T / kBlkTok;
     const int m = blockIdx.x / tiles_t, t0 = (blockIdx.x % tiles_t) * kBlkTok;
@@ -122,7 +134,7 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
     const unsigned lbase = lds_addr(lds);
 
     // per-member vectors into LDS (zeros when a matrix is unperturbed, so no branches later)
-    {
+    if constexpr (!kJit) {
         auto vcopy = [&](const float *src, int off, int n) {
             float *dst = reinterpret_cast<float *>(lds + off);
             for (int i = tid; i < n / 4; i += kBlkThreads)
@@ -167,6 +179,13 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
                 copy128(p.wfc + (int64_t)(kUnits * js) * kModel + 64 * wave, kModel, 8 * i, dst + wave * 4096);
+            if constexpr (kJitFc) {
+                // the step's c_fc jitter of this wave's 16 tokens: token row (lane / 4), 16 B chunk (lane % 4) of
+                // its 32 units, into slot js % 3 of the ring as [16 tokens][64 B] (a fifth copy of this stage)
+                const __bf16 *src = p.jfc + ((int64_t)m * T + t0 + 16 * wave) * kHidden + kUnits * js;
+                lds_dma16_at(src, (unsigned)((lane >> 2) * kHidden * 2 + (lane & 3) * 16),
+                             lbase + kJitRing + (js % 3) * kJitSlot + wave * 1024);
+            }
         } else {
 #pragma unroll
             for (int i = 0; i < 4; ++i) copy64(p.wpj + kUnits * js, kHidden, 64 * wave + 16 * i, dst);
@@ -246,6 +265,11 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         float ssq = 0.f;
 #pragma unroll
         for (int ob = 0; ob < 32; ++ob) {
+            if constexpr (kJit) {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) ssq += out[ob][r] * out[ob][r];
+                continue;
+            }
             const float4 a4 = ld4(ao + 16 * ob);
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
@@ -281,12 +305,25 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
     float pd = 0.f;  // this lane's share of hid . b_proj
     const float *afc_l = reinterpret_cast<const float *>(lds + kVAfc) + 4 * g;
     const float *bpj_l = reinterpret_cast<const float *>(lds + kVBpj) + 4 * g;
-    vm_wait<8>();     // stage 0 landed (stages 1 and 2 may still be in flight)
+    // stage 0 landed (stages 1 and 2 may still be in flight: 4 copies per wave each, 5 for a c_fc stage with JIT)
+    vm_wait<kJitFc ? 9 : 8>();
     __syncthreads();
     constexpr int kStages = 2 * kSteps;
     // after stage k: stage k + 1 must have landed; the stages issued after it (up to k + 3) may still fly
     auto stage_end = [&](int k) {
-        vm_wait_groups<4, 2>(kStages - 2 - k < 2 ? kStages - 2 - k : 2);
+        if constexpr (kJitFc) {
+            // two stages in flight are one c_fc stage (5 copies) and one mlp.c_proj stage (4); one is the last,
+            // an mlp.c_proj stage
+            const int r = kStages - 2 - k;
+            if (r >= 2)
+                vm_wait<9>();
+            else if (r == 1)
+                vm_wait<4>();
+            else
+                vm_wait<0>();
+        } else {
+            vm_wait_groups<4, 2>(kStages - 2 - k < 2 ? kStages - 2 - k : 2);
+        }
         __syncthreads();  // every wave's copies of stage k + 1 landed; every wave is done with buffer k & 3
     };
 #pragma unroll 1
@@ -316,7 +353,25 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         // ReLU^2 with the rank-1 term, bf16, packed as the second product's B operand (k = 8 g + j holds hidden unit
         // 4 g + j of block 0 for j < 4, of block 1 for j >= 4); this lane's share of hid . b_proj
         bf16x8 hb;
-        {
+        if constexpr (kJit) {
+            // the c_fc jitter of this lane's token (units 4 g .. + 3 of each 16-unit block), then ReLU^2
+            bf16x4 j0, j1;
+            if constexpr (kJitFc) {
+                const char *jr = lds + kJitRing + (js % 3) * kJitSlot + (16 * wave + tl) * 64 + 8 * g;
+                j0 = *reinterpret_cast<const bf16x4 *>(jr);
+                j1 = *reinterpret_cast<const bf16x4 *>(jr + 32);
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) j0[r] = j1[r] = (__bf16)0.0f;
+            }
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v0 = fmaxf(hacc[0][r] + (float)j0[r], 0.f);
+                float v1 = fmaxf(hacc[1][r] + (float)j1[r], 0.f);
+                hb[r] = (__bf16)(v0 * v0);
+                hb[4 + r] = (__bf16)(v1 * v1);
+            }
+        } else {
             const float4 a0 = ld4(afc_l + kUnits * js), a1 = ld4(afc_l + kUnits * js + 16);
             const float4 b0 = ld4(bpj_l + kUnits * js), b1 = ld4(bpj_l + kUnits * js + 16);
 #pragma unroll
@@ -363,6 +418,7 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
     {
         const float *apj = reinterpret_cast<const float *>(lds + kVApj) + 4 * g;
         const float *zr = MIX ? p.x0 + m * p.x0_m + (int64_t)tok * p.x0_t + 4 * g : nullptr;
+        const __bf16 *jr = kJit ? p.jmlp + row * p.jmlp_st + 4 * g : nullptr;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             float4 zv[8];
@@ -370,18 +426,26 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
 #pragma unroll
                 for (int i = 0; i < 8; ++i) zv[i] = ld4(zr + 16 * (8 * q + i));
             }
+            bf16x4 jv[8];
+            if constexpr (kJit) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) jv[i] = load_bf16x4(jr + 16 * (8 * q + i));
+            }
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
                 const int ob = 8 * q + i;
-                const float4 a4 = ld4(apj + 16 * ob);
+                const float4 a4 = kJit ? float4{0.f, 0.f, 0.f, 0.f} : ld4(apj + 16 * ob);
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    float v = out[ob][r] + corr * f4get(a4, r);
+                    // with JIT: the block's mlp.c_proj product plus its jitter (the rank-1 terms are off)
+                    float v = kJit ? out[ob][r] + (float)jv[i][r] : out[ob][r] + corr * f4get(a4, r);
                     if constexpr (MIX) v = rl * v + ml * f4get(zv[i], r);
                     out[ob][r] = v;
                     ssq += v * v;
                 }
             }
+            // with JIT, one chunk's x0 and jitter rows at a time: hoisting all four chunks' loads spills
+            if constexpr (kJit) __builtin_amdgcn_sched_barrier(0);
         }
     }
     const float rstd = rsqrtf(token_sum(ssq) * (1.0f / kModel) + kBlkEps);
@@ -524,6 +588,30 @@ void launch_block_qkv(const BlockArgs &a, int nnext, bool ve, dim3 grid, hipStre
         launch_block_qkv_n<MIX, 0>(a, ve, grid, s);
 }
 
+// the jittered (unperturbed) block: the last block before the fp32 head (no mixing, split3 head input), or a
+// block followed by the next block's q/k/v with or without its value embeddings (with the next mixing)
+template <int JIT>
+bool launch_block_jit_n(const BlockArgs &a, bool mix, bool split3, int qkv, dim3 grid, hipStream_t s) {
+    if (qkv == 0 && !mix && split3)
+        hipLaunchKernelGGL((block_kernel<false, 0, true, 0, JIT>), grid, dim3(kBlkThreads), 0, s, a);
+    else if (qkv == 1 && mix)
+        hipLaunchKernelGGL((block_kernel<true, 0, false, 1, JIT>), grid, dim3(kBlkThreads), 0, s, a);
+    else if (qkv == 2 && mix)
+        hipLaunchKernelGGL((block_kernel<true, 0, false, 2, JIT>), grid, dim3(kBlkThreads), 0, s, a);
+    else
+        return false;
+    return true;
+}
+
+int launch_block_jit(const char *fn, const BlockArgs &a, bool mix, bool split3, int qkv, dim3 grid, hipStream_t s) {
+    const bool ok = a.jfc ? launch_block_jit_n<1>(a, mix, split3, qkv, grid, s)
+                          : launch_block_jit_n<2>(a, mix, split3, qkv, grid, s);
+    if (!ok)
+        NOISE_CHECK_ARG(false, "%s: jitter is served for the last block with the split3 head input and no mixing, "
+                               "or for a block followed by the next block's q/k/v with its mixing", fn);
+    return launch_status(fn);
+}
+
 }  // namespace
 }  // namespace noise
 
@@ -600,14 +688,37 @@ int block_args(const char *fn, BlockArgs &a, const noise_population_t *pop, nois
 }  // namespace
 }  // namespace noise
 
-extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
-                               const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
-                               const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout,
-                               int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
-                               int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
-                               int64_t nnext, float *next_dots, noise_stream_t stream) {
-    clear_error();
-    const char *fn = "noise_pop_block";
+namespace noise {
+namespace {
+
+// the jitter of a jittered block: the block must be unperturbed (DUST's block_forward, run.py:102-117); the
+// rows are [members * tokens][2048] (mlp.c_fc) and [members * tokens][512] (mlp.c_proj), bf16, 16 B aligned
+int block_jitter(const char *fn, BlockArgs &a, const noise_block_jitter_t *jit) {
+    NOISE_CHECK_ARG(jit && (jit->fc || jit->mlp), "%s: jitter NULL or empty", fn);
+    NOISE_CHECK_ARG(!a.ao && !a.afc && !a.apj && !a.eps_r && !a.eps_x && !a.nb[0] && !a.nb[1] && !a.nb[2],
+                    "%s: a jittered block takes no rank-1 or mixing-scalar noise", fn);
+    NOISE_CHECK_ARG((!jit->fc || aligned(jit->fc, 16)) && (!jit->mlp || aligned(jit->mlp, 16)),
+                    "%s: jitter rows must be 16 B aligned", fn);
+    // no mlp.c_proj jitter: every row reads one zero row (the kernel's epilogue loads unconditionally)
+    a.jmlp = (const __bf16 *)jit->mlp;
+    a.jmlp_st = kModel;
+    if (!a.jmlp) {
+        NOISE_CHECK_ARG(jit->zero_row && aligned(jit->zero_row, 16), "%s: without mlp jitter a 512-element zero row "
+                        "(bf16, 16 B aligned) must be given", fn);
+        a.jmlp = (const __bf16 *)jit->zero_row;
+        a.jmlp_st = 0;
+    }
+    a.jfc = (const __bf16 *)jit->fc;   // each workgroup copies only its own token rows of it
+    return NOISE_OK;
+}
+
+int pop_block_impl(const char *fn, const noise_population_t *pop, noise_view_t y, const void *w_o,
+                   const noise_rank1_t *r_o, const float *o_dots, int64_t o_dots_n, noise_view_t xres,
+                   const void *w_fc, const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj,
+                   float *xout, int mix, const float *lam_r, const float *lam_x, const float *eps_r,
+                   const float *eps_x, int64_t eps_stride, noise_view_t x0, void *hout, int split3,
+                   const noise_rank1_t *next, int64_t nnext, float *next_dots, const noise_block_jitter_t *jit,
+                   noise_stream_t stream) {
     BlockArgs a;
     const int st = block_args(fn, a, pop, y, w_o, r_o, o_dots, o_dots_n, xres, w_fc, r_fc, w_proj, r_proj, xout, mix,
                               lam_r, lam_x, eps_r, eps_x, eps_stride, x0, next, nnext);
@@ -617,6 +728,11 @@ extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, co
     a.hout = (__bf16 *)hout;
     a.ndots = next_dots;
     const dim3 grid((unsigned)(pop->members * (pop->tokens / kBlkTok)));
+    if (jit) {
+        const int js = block_jitter(fn, a, jit);
+        if (js != NOISE_OK) return js;
+        return launch_block_jit(fn, a, mix != 0, split3 != 0, 0, grid, (hipStream_t)stream);
+    }
     if (mix)
         launch_block<true>(a, (int)nnext, split3 != 0, grid, (hipStream_t)stream);
     else
@@ -624,18 +740,15 @@ extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, co
     return launch_status(fn);
 }
 
-extern "C" int noise_pop_block_qkv(const noise_population_t *pop, noise_view_t y, const void *w_o,
-                                   const noise_rank1_t *r_o, const float *o_dots, int64_t o_dots_n, noise_view_t xres,
-                                   const void *w_fc, const noise_rank1_t *r_fc, const void *w_proj,
-                                   const noise_rank1_t *r_proj, float *xout, int mix, const float *lam_r,
-                                   const float *lam_x, const float *eps_r, const float *eps_x, int64_t eps_stride,
-                                   noise_view_t x0, const void *const w_qkv[3], const noise_rank1_t r_qkv[3],
-                                   const void *rope_cos, const void *rope_sin, const float *ve, int64_t vocab,
-                                   const int64_t *idx, int64_t idx_sm, const float *gate_w,
-                                   const noise_rank1_t *gate_noise, const noise_rank1_t *ve_noise, void *const out[3],
-                                   noise_stream_t stream) {
-    clear_error();
-    const char *fn = "noise_pop_block_qkv";
+int pop_block_qkv_impl(const char *fn, const noise_population_t *pop, noise_view_t y, const void *w_o,
+                       const noise_rank1_t *r_o, const float *o_dots, int64_t o_dots_n, noise_view_t xres,
+                       const void *w_fc, const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj,
+                       float *xout, int mix, const float *lam_r, const float *lam_x, const float *eps_r,
+                       const float *eps_x, int64_t eps_stride, noise_view_t x0, const void *const w_qkv[3],
+                       const noise_rank1_t r_qkv[3], const void *rope_cos, const void *rope_sin, const float *ve,
+                       int64_t vocab, const int64_t *idx, int64_t idx_sm, const float *gate_w,
+                       const noise_rank1_t *gate_noise, const noise_rank1_t *ve_noise, void *const out[3],
+                       const noise_block_jitter_t *jit, noise_stream_t stream) {
     const bool pq = r_qkv && (r_qkv[0].a || r_qkv[1].a || r_qkv[2].a);
     BlockArgs a;
     const int st = block_args(fn, a, pop, y, w_o, r_o, o_dots, o_dots_n, xres, w_fc, r_fc, w_proj, r_proj, xout, mix,
@@ -671,9 +784,69 @@ extern "C" int noise_pop_block_qkv(const noise_population_t *pop, noise_view_t y
     a.q.gate_a = gn ? gate_noise->a : nullptr; a.q.gate_b = gn ? gate_noise->b : nullptr;
     a.q.gate_a_stride = gn ? gate_noise->a_stride : 0; a.q.gate_b_stride = gn ? gate_noise->b_stride : 0;
     const dim3 grid((unsigned)(pop->members * (pop->tokens / kBlkTok)));
+    if (jit) {
+        NOISE_CHECK_ARG(!pq && !gn && !vn, "%s: a jittered block's next q/k/v take no noise", fn);
+        const int js = block_jitter(fn, a, jit);
+        if (js != NOISE_OK) return js;
+        return launch_block_jit(fn, a, mix != 0, false, ve ? 2 : 1, grid, (hipStream_t)stream);
+    }
     if (mix)
         launch_block_qkv<true>(a, pq ? 3 : 0, ve != nullptr, grid, (hipStream_t)stream);
     else
         launch_block_qkv<false>(a, pq ? 3 : 0, ve != nullptr, grid, (hipStream_t)stream);
     return launch_status(fn);
+}
+
+}  // namespace
+}  // namespace noise
+
+extern "C" int noise_pop_block(const noise_population_t *pop, noise_view_t y, const void *w_o, const noise_rank1_t *r_o,
+                               const float *o_dots, int64_t o_dots_n, noise_view_t xres, const void *w_fc,
+                               const noise_rank1_t *r_fc, const void *w_proj, const noise_rank1_t *r_proj, float *xout,
+                               int mix, const float *lam_r, const float *lam_x, const float *eps_r, const float *eps_x,
+                               int64_t eps_stride, noise_view_t x0, void *hout, int split3, const noise_rank1_t *next,
+                               int64_t nnext, float *next_dots, noise_stream_t stream) {
+    clear_error();
+    return pop_block_impl("noise_pop_block", pop, y, w_o, r_o, o_dots, o_dots_n, xres, w_fc, r_fc, w_proj, r_proj,
+                          xout, mix, lam_r, lam_x, eps_r, eps_x, eps_stride, x0, hout, split3, next, nnext, next_dots,
+                          nullptr, stream);
+}
+
+extern "C" int noise_pop_block_jit(const noise_population_t *pop, noise_view_t y, const void *w_o, noise_view_t xres,
+                                   const void *w_fc, const void *w_proj, int mix, const float *lam_r,
+                                   const float *lam_x, noise_view_t x0, void *hout, int split3,
+                                   const noise_block_jitter_t *jit, noise_stream_t stream) {
+    clear_error();
+    return pop_block_impl("noise_pop_block_jit", pop, y, w_o, nullptr, nullptr, 0, xres, w_fc, nullptr, w_proj,
+                          nullptr, nullptr, mix, lam_r, lam_x, nullptr, nullptr, 0, x0, hout, split3, nullptr, 0,
+                          nullptr, jit, stream);
+}
+
+extern "C" int noise_pop_block_qkv(const noise_population_t *pop, noise_view_t y, const void *w_o,
+                                   const noise_rank1_t *r_o, const float *o_dots, int64_t o_dots_n, noise_view_t xres,
+                                   const void *w_fc, const noise_rank1_t *r_fc, const void *w_proj,
+                                   const noise_rank1_t *r_proj, float *xout, int mix, const float *lam_r,
+                                   const float *lam_x, const float *eps_r, const float *eps_x, int64_t eps_stride,
+                                   noise_view_t x0, const void *const w_qkv[3], const noise_rank1_t r_qkv[3],
+                                   const void *rope_cos, const void *rope_sin, const float *ve, int64_t vocab,
+                                   const int64_t *idx, int64_t idx_sm, const float *gate_w,
+                                   const noise_rank1_t *gate_noise, const noise_rank1_t *ve_noise, void *const out[3],
+                                   noise_stream_t stream) {
+    clear_error();
+    return pop_block_qkv_impl("noise_pop_block_qkv", pop, y, w_o, r_o, o_dots, o_dots_n, xres, w_fc, r_fc, w_proj,
+                              r_proj, xout, mix, lam_r, lam_x, eps_r, eps_x, eps_stride, x0, w_qkv, r_qkv, rope_cos,
+                              rope_sin, ve, vocab, idx, idx_sm, gate_w, gate_noise, ve_noise, out, nullptr, stream);
+}
+
+extern "C" int noise_pop_block_qkv_jit(const noise_population_t *pop, noise_view_t y, const void *w_o,
+                                       noise_view_t xres, const void *w_fc, const void *w_proj, float *xout,
+                                       const float *lam_r, const float *lam_x, noise_view_t x0,
+                                       const void *const w_qkv[3], const void *rope_cos, const void *rope_sin,
+                                       const float *ve, int64_t vocab, const int64_t *idx, int64_t idx_sm,
+                                       const float *gate_w, void *const out[3], const noise_block_jitter_t *jit,
+                                       noise_stream_t stream) {
+    clear_error();
+    return pop_block_qkv_impl("noise_pop_block_qkv_jit", pop, y, w_o, nullptr, nullptr, 0, xres, w_fc, nullptr,
+                              w_proj, nullptr, xout, 1, lam_r, lam_x, nullptr, nullptr, 0, x0, w_qkv, nullptr,
+                              rope_cos, rope_sin, ve, vocab, idx, idx_sm, gate_w, nullptr, nullptr, out, jit, stream);
 }

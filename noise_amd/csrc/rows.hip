@@ -684,6 +684,73 @@ extern "C" int noise_rerun_rows(const float *x, int64_t x_rows, const void *add,
     return launch_status(fn);
 }
 
+namespace noise {
+namespace {
+
+// A jittered block's entry (run.py:265, 102-110): out[r] = x[r % x_rows] + add[r] (the attn.c_proj jitter folded
+// into the residual the block adds its product to), h[r] = bf16(norm(x[r % x_rows])) (the block's own input).
+__global__ __launch_bounds__(256) void block_entry_kernel(const float *x, int64_t x_rows, const __bf16 *add,
+                                                          int64_t rows, float *out, __bf16 *h) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    float v[8];
+    ld8(x + (row % x_rows) * 512 + lane * 8, v);
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ss += v[i] * v[i];
+    const float r = rsqrtf(wave_sum(ss) * (1.0f / 512.0f) + kEps);
+    bf16x8 hb;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) hb[i] = (__bf16)(v[i] * r);
+    store_bf16x8(h + row * 512 + lane * 8, hb);
+    if (add) {
+        const bf16x8 a = load_bf16x8(add + row * 512 + lane * 8);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] += (float)a[i];
+    }
+    st8(out + row * 512 + lane * 8, v);
+}
+
+// y = bf16(y + add), 8 elements per thread
+__global__ __launch_bounds__(256) void add_bf16_rows_kernel(__bf16 *__restrict__ y, const __bf16 *__restrict__ add,
+                                                            int64_t n8) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    bf16x8 a = load_bf16x8(y + 8 * i);
+    const bf16x8 b = load_bf16x8(add + 8 * i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a[e] = (__bf16)((float)a[e] + (float)b[e]);
+    store_bf16x8(y + 8 * i, a);
+}
+
+}  // namespace
+}  // namespace noise
+
+extern "C" int noise_block_entry(const float *x, int64_t x_rows, const void *add, int64_t rows, float *out, void *h,
+                                 noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_block_entry";
+    NOISE_CHECK_ARG(x && out && h && rows > 0 && x_rows > 0 && aligned(x, 16) && aligned(out, 16) && aligned(h, 16),
+                    "%s: bad x / out / h", fn);
+    NOISE_CHECK_ARG(!add || aligned(add, 16), "%s: add must be 16 B aligned", fn);
+    hipLaunchKernelGGL(block_entry_kernel, dim3(rows_grid(rows)), dim3(256), 0, (hipStream_t)stream, x, x_rows,
+                       (const __bf16 *)add, rows, out, (__bf16 *)h);
+    return launch_status(fn);
+}
+
+extern "C" int noise_add_bf16(void *y, const void *add, int64_t n, noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_add_bf16";
+    NOISE_CHECK_ARG(y && add && n > 0 && n % 8 == 0 && aligned(y, 16) && aligned(add, 16),
+                    "%s: 16 B aligned y and add and n a positive multiple of 8 required", fn);
+    const int64_t n8 = n / 8;
+    NOISE_CHECK_ARG((n8 + 255) / 256 < (1ll << 31), "%s: n too large", fn);
+    hipLaunchKernelGGL(add_bf16_rows_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (__bf16 *)y, (const __bf16 *)add, n8);
+    return launch_status(fn);
+}
+
 extern "C" int noise_rerun_mix_norm(const float *x, int64_t x_rows, const float *x0, int64_t x0_rows,
                                     const float *lam_r, const float *lam_x, int64_t rows, float *out, void *h,
                                     noise_stream_t stream) {

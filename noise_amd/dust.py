@@ -192,11 +192,12 @@ def rerun(dust, n, entry, jitter):
     targets, [batch, length]) and weights (the per-block dicts of run.py:172-175). jitter: site name ->
     [n * batch, length, width] (sigma * draws).
 
-    The chain: the cached input of block `entry` repeated n times through that block with its jitter sites
-    (noise_dust_block, the block with per-token jitter epilogues), or the jittered embedding entry normed; then
-    every later block's mixing and the blocks on the population kernels (blocks_forward: n * batch members, one
-    token row each, no rank-1 terms), the final norm and the fp32 head (split-bf16x3) with the soft cap and CE.
-    A jittered last block goes straight to the head (head_loss)."""
+    The chain, on the population kernels with n * batch members of one token row each and no rank-1 terms
+    (blocks_forward): the cached input of block `entry` read for every draw with its attn.c_proj jitter folded
+    into the residual (noise_block_entry), or the jittered embedding entry normed and mixed; block `entry` with
+    its attention-output jitter (noise_add_bf16) and its mlp.c_fc / mlp.c_proj jitter in the block kernel's
+    MLP (noise_pop_block_qkv_jit, noise_pop_block_jit); every later block with its mixing; the final norm and
+    the fp32 head (split-bf16x3) with the soft cap and per-token CE."""
     from .eggroll import blocks_forward
     model = dust.model
     T, b = dust.length, dust.batch
@@ -206,36 +207,39 @@ def rerun(dust, n, entry, jitter):
     L = model.config.n_layer
     W = _weights(dust)
     cos, sin = _rotary(model, T, dev)
+    idx = dust.x.to(device=dev, dtype=torch.int64).repeat(n, 1).contiguous()
+    targets = dust.y.to(device=dev, dtype=torch.int64).repeat(n, 1).contiguous()
+    rope = (cos.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous(),
+            sin.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous())
+    x_in = torch.empty(n * b, T, 512, dtype=F32, device=dev)
+    h_in = torch.empty(n * b, T, 512, dtype=BF16, device=dev)
+    sites = {}
     if entry is None:
+        # the jittered embedding entry x = x0 = norm(embedding + jitter), then block 0's mixing and norm
         emb = dust.outputs['transformer.wte'].detach().to(F32).contiguous()
         add = jitter.get('transformer.wte')
         add = None if add is None else add.reshape(n * b, T, -1).to(BF16).contiguous()
         x0 = torch.empty(n * b, T, 512, dtype=F32, device=dev)
         _lib.call('noise_rerun_rows', emb.data_ptr(), b * T, _lib.ptr(add), None, 0, None, None, rows, x0.data_ptr(),
                   stream)
-        x_prev, first = x0, 0
+        _lib.call('noise_rerun_mix_norm', x0.data_ptr(), rows, x0.data_ptr(), rows, W.lam_r(0), W.lam_x(0), rows,
+                  x_in.data_ptr(), h_in.data_ptr(), stream)
+        first = 0
     else:
-        x = dust.blocks[entry].detach().to(F32).repeat(n, 1, 1).contiguous()
-        ve = dust.outputs.get(f'value_embeds.{entry}')
-        ve = None if ve is None else ve.detach().repeat(n, 1, 1)
-        sites = {key: jitter.get(site.format(entry)) for key, site in SITES.items()}
-        x_prev = block_forward_eager(x, dust.weights[entry], ve, cos, sin, model.window_sizes[entry][0], **sites)
-        if entry == L - 1:
-            loss = head_loss_eager(x_prev, model.lm_head.weight.detach().float(), dust.y.repeat(n, 1),
-                                   model.config.vocab_size)
-            return loss.view(n, b, T)
+        # the cached input of block `entry` for every draw (row r reads row r mod batch * length), its norm, and the
+        # residual with the attn.c_proj jitter folded in; the block's other jitter sites go to blocks_forward
+        x = dust.blocks[entry].detach().to(F32).contiguous()
+        width = {'o': 512, 'attn': 512, 'fc': 2048, 'mlp': 512}
+        for key, site in SITES.items():
+            t = jitter.get(site.format(entry))
+            if t is not None:
+                sites[key] = t.reshape(n * b, T, width[key]).to(BF16).contiguous()
+        attn = sites.pop('attn', None)
+        _lib.call('noise_block_entry', x.data_ptr(), b * T, _lib.ptr(attn), rows, x_in.data_ptr(), h_in.data_ptr(),
+                  stream)
         x0 = dust.x0.detach().to(F32).repeat(n, 1, 1).contiguous()
-        first = entry + 1
-    # the first block after the entry: its mixing (run.py:267-268) and norm, then the population chain
-    x_in = torch.empty(n * b, T, 512, dtype=F32, device=dev)
-    h_in = torch.empty(n * b, T, 512, dtype=BF16, device=dev)
-    _lib.call('noise_rerun_mix_norm', x_prev.data_ptr(), rows, x0.data_ptr(), rows, W.lam_r(first), W.lam_x(first),
-              rows, x_in.data_ptr(), h_in.data_ptr(), stream)
-    idx = dust.x.to(device=dev, dtype=torch.int64).repeat(n, 1).contiguous()
-    targets = dust.y.to(device=dev, dtype=torch.int64).repeat(n, 1).contiguous()
-    rope = (cos.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous(),
-            sin.reshape(-1)[:T * 32].view(T, 32).to(BF16).contiguous())
-    loss = blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=rope)
+        first = entry
+    loss = blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=rope, jitter=sites)
     return loss.view(n, b, T)
 
 

@@ -407,15 +407,27 @@ def population_forward(W, noise, sign, idx, targets, dir_div=1, rope=None, buffe
     return out
 
 
-def blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=None, buffers=None):
+_ZERO_BF16 = {}
+
+
+def _zero_row_bf16(dev):
+    """512 zero bf16 values on dev (the mlp.c_proj jitter row a jittered block reads when it has none)."""
+    if dev not in _ZERO_BF16:
+        _ZERO_BF16[dev] = torch.zeros(N_EMBD, dtype=BF16, device=dev)
+    return _ZERO_BF16[dev]
+
+
+def blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=None, buffers=None, jitter=None):
     """Per-token losses [m, T] of the fixed (unperturbed) model run from block `first` on m token rows: the
     blocks first .. L-1 on the population kernels (the same launches as population_forward's fused path), the
     final norm and the head (fp32 as split-bf16x3 when W.fp32_head), the soft cap and CE (ignore_index -1).
 
     x_in: fp32 [m, T, 512], block `first`'s input after its mixing; h_in: bf16 [m, T, 512] = norm(x_in); x0:
     fp32 [m, T, 512], the normed embedding every block mixes in; idx, targets: [m, T] int64 (one token row per
-    member: the value embeddings of blocks with them, and the head's targets). DUST's rerun runs the blocks
-    after its jittered one this way (run.py:265-278)."""
+    member: the value embeddings of blocks with them, and the head's targets). jitter: block `first`'s
+    block_forward jitter (run.py:102-117) by keyword, bf16 [m, T, width] each: 'o' (the attention output),
+    'fc' (mlp.c_fc's product, before ReLU^2), 'mlp' (mlp.c_proj's product); its attn.c_proj jitter is the
+    caller's to fold into x_in (noise_block_entry). DUST's rerun runs its blocks this way (run.py:256-279)."""
     dev = W.device
     m, T = idx.shape
     E = N_EMBD
@@ -425,6 +437,18 @@ def blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=None, buffers=No
                          f'{tuple(targets.shape)}')
     if not 0 <= first < L:
         raise ValueError(f'blocks_forward: first block {first} outside 0 .. {L - 1}')
+    jitter = {k: v for k, v in (jitter or {}).items() if v is not None}
+    if set(jitter) - {'o', 'fc', 'mlp'}:
+        raise ValueError(f'blocks_forward: jitter at o, fc or mlp only, got {sorted(jitter)}')
+    if jitter and not W.fp32_head and first == L - 1:
+        raise ValueError('blocks_forward: a jittered last block feeds the fp32 head (Weights(fp32_head=True))')
+    jit = {}
+    for k, width in (('o', E), ('fc', 4 * E), ('mlp', E)):
+        if k in jitter:
+            t = jitter[k]
+            if t.shape != (m, T, width) or t.dtype != BF16 or not t.is_contiguous():
+                raise ValueError(f'blocks_forward: jitter {k!r} must be contiguous bf16 [{m}, {T}, {width}]')
+            jit[k] = t
     for t, dt in ((x_in, F32), (h_in, BF16), (x0, F32)):
         if t.shape != (m, T, E) or t.dtype != dt or not t.is_contiguous():
             raise ValueError(f'blocks_forward: x_in, x0 fp32 and h_in bf16, contiguous [{m}, {T}, {E}]')
@@ -460,6 +484,27 @@ def blocks_forward(W, first, x_in, h_in, x0, idx, targets, rope=None, buffers=No
               yv.stride(0), yv.stride(2), yv.stride(1), W.windows[i], 1.0 / math.sqrt(HEAD_DIM), None, 0, 1, None,
               stream, label=f'window {W.windows[i]}')
         xres = _view(x_in, T * E, E) if i == first else _view(B.resid, T * E, E)
+        if i == first and jit:
+            if 'o' in jit:
+                _call('noise_add_bf16', B.y.data_ptr(), jit['o'].data_ptr(), B.y.numel(), stream)
+            if 'fc' in jit or 'mlp' in jit:
+                js = _lib.BlockJitter(_lib.ptr(jit.get('fc')), _lib.ptr(jit.get('mlp')),
+                                      _zero_row_bf16(dev).data_ptr())
+                if i < L - 1:
+                    nblk = W.blocks[i + 1]
+                    nws = (ctypes.c_void_p * 3)(nblk['q_blk'].data_ptr(), nblk['k_blk'].data_ptr(),
+                                                nblk['v_blk'].data_ptr())
+                    _call('noise_pop_block_qkv_jit', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), xres,
+                          blk['fc_blk'].data_ptr(), blk['mp_blk'].data_ptr(), B.resid.data_ptr(), W.lam_r(i + 1),
+                          W.lam_x(i + 1), x0v, nws, cos_t.data_ptr(), sin_t.data_ptr(),
+                          nblk['ve'].data_ptr() if 've' in nblk else None, nblk['ve'].shape[0] if 've' in nblk else 0,
+                          idx.data_ptr(), T, nblk['gate'].data_ptr() if 've' in nblk else None, qkv_out,
+                          ctypes.byref(js), stream, label='block (jitter)')
+                else:
+                    _call('noise_pop_block_jit', popp, _view(B.y, T * E, E), blk['o'].data_ptr(), xres,
+                          blk['fc_blk'].data_ptr(), blk['mp_blk'].data_ptr(), 0, None, None, x0v, B.h3.data_ptr(), 1,
+                          ctypes.byref(js), stream, label='block (jitter)')
+                continue
         if i < L - 1:
             # the block, then the next block's mixing, norm, gates and q/k/v (norm and dots stay in registers)
             nblk = W.blocks[i + 1]

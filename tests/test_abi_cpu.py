@@ -90,7 +90,8 @@ def test_struct_layouts_match_the_header(tmp_path):
     abi = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(abi)
     structs = {'noise_view_t': abi.View, 'noise_rank1_t': abi.Rank1, 'noise_population_t': abi.Population,
-               'noise_update_param_t': abi.UpdateParam, 'noise_slice_groups_t': abi.SliceGroups}
+               'noise_update_param_t': abi.UpdateParam, 'noise_slice_groups_t': abi.SliceGroups,
+               'noise_block_jitter_t': abi.BlockJitter}
     lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "noise_amd.h"', 'int main(void) {']
     for c_name, py in structs.items():
         lines.append(f'    printf("{c_name} size %zu\\n", sizeof({c_name}));')

@@ -136,11 +136,15 @@ def test_draw_errors_matches_oracle(d):
     assert np.all(np.abs(got - ref) <= step)
 
 
+FC, MLP, ATTN, O = 'transformer.h.{}.mlp.c_fc', 'transformer.h.{}.mlp.c_proj', 'transformer.h.{}.attn.c_proj', 'o@{}'
+WIDTH = {FC: 2048, MLP: 512, ATTN: 512, O: 512, 'transformer.wte': 512}
+
+
 @pytest.mark.parametrize('impl', ['rerun', 'rerun_tiled'])
-@pytest.mark.parametrize('entry,site,width', [(None, 'transformer.wte', 512), (3, 'transformer.h.{}.mlp.c_fc', 2048),
-                                              (6, 'o@{}', 512), (7, 'transformer.h.{}.mlp.c_proj', 512)],
-                         ids=['embedding', 'fc-3', 'o-6', 'mlp-7'])
-def test_rerun_matches_oracle(entry, site, width, impl):
+@pytest.mark.parametrize('entry,sites', [(None, ['transformer.wte']), (3, [FC]), (6, [O]), (7, [MLP]), (0, [ATTN]),
+                                         (2, [FC]), (7, [FC]), (4, [MLP]), (2, [O, ATTN, FC, MLP])],
+                         ids=['embedding', 'fc-3', 'o-6', 'mlp-7', 'attn-0', 'fc-2', 'fc-7', 'mlp-4', 'all-2'])
+def test_rerun_matches_oracle(entry, sites, impl):
     """DUST.rerun (run.py:256-279) end to end -- the cached input repeated n times (or the jittered embedding
     entry), the later blocks' mixing, block_forward with the entry's jitter, the final norm and fp32 head --
     against the oracle rerun composed from the pinned pieces (oracle/dust.py), per draw and per token. The
@@ -149,8 +153,10 @@ def test_rerun_matches_oracle(entry, site, width, impl):
     within 1e-3 of the fp32 oracle, and so does the jitter's effect (rerun minus the unjittered rerun, the
     reward DUST forms) per draw. Per token, bf16 products and attention through up to 8 blocks (the
     reference's autocast numerics) put single tokens up to 2e-2 from fp32 (measured 1.95e-2 from the
-    embedding): the per-token bound is 3e-2. Both forms: rerun (the blocks after the entry on the population
-    kernels) and rerun_tiled (every block on noise_dust_block)."""
+    embedding): the per-token bound is 3e-2. Both forms: rerun (every block on the population kernels, the
+    entry block's jitter in noise_block_entry, noise_add_bf16 and the jittered block kernels: mlp.c_fc jitter
+    before a block with and without value embeddings and before the head, mlp.c_proj jitter alone, all four
+    sites at once) and rerun_tiled (every block on noise_dust_block)."""
     from types import SimpleNamespace
     import noise_amd.dust as ndust
     rerun = getattr(ndust, impl)
@@ -164,13 +170,15 @@ def test_rerun_matches_oracle(entry, site, width, impl):
     rows = torch.randint(0, 4096, (b, T + 1), generator=g)
     x, y = rows[:, :-1], rows[:, 1:]
     cache = odust.capture(P, x)
-    name = site.format(entry) if entry is not None else site
-    draws = (torch.randint(0, 2, (n * b, T, width), generator=g) * 2 - 1).bfloat16()
-    jitter = {name: (0.1 * draws.float()).bfloat16()}
-    print(f'rerun: entry {entry}, jitter at {name}, {n} draws x {b} sequences x {T} tokens', flush=True)
+    names = [site.format(entry) if entry is not None else site for site in sites]
+    jitter = {}
+    for site, name in zip(sites, names):
+        draws = (torch.randint(0, 2, (n * b, T, WIDTH[site]), generator=g) * 2 - 1).bfloat16()
+        jitter[name] = (0.1 * draws.float()).bfloat16()
+    print(f'rerun: entry {entry}, jitter at {names}, {n} draws x {b} sequences x {T} tokens', flush=True)
     ref = odust.rerun(P, cache, y, n, entry, jitter)
-    ref0 = odust.rerun(P, cache, y, n, entry, {})  if entry is not None else \
-        odust.rerun(P, cache, y, n, entry, {name: torch.zeros(n * b, T, width)})
+    zero = {name: torch.zeros_like(t) for name, t in jitter.items()}
+    ref0 = odust.rerun(P, cache, y, n, entry, {} if entry is not None else zero)
     dev = torch.device('cuda', 0)
     m = model.to(dev)
     to = lambda d: {k: v.to(dev) for k, v in d.items()}
@@ -179,7 +187,7 @@ def test_rerun_matches_oracle(entry, site, width, impl):
                            weights=[{k: (None if v is None else v.to(dev)) for k, v in odust.block_weights(P, i).items()}
                                     for i in range(8)])
     got = rerun(dust, n, entry, to(jitter)).cpu()
-    got0 = rerun(dust, n, entry, {} if entry is not None else {name: torch.zeros(n * b, T, width, device=dev)}).cpu()
+    got0 = rerun(dust, n, entry, {} if entry is not None else to(zero)).cpu()
     assert got.shape == (n, b, T) and torch.isfinite(got).all()
     tok = (got - ref).abs().max().item()
     mean = (got.mean(-1) - ref.mean(-1)).abs().max().item()
