@@ -366,3 +366,47 @@ def test_rerun_fp32_stream_against_the_bf16_flow(entry, site, width):
     print(f'fp32 stream vs the bf16 flow: per-draw mean {mean:.2e}, jitter effect {eff:.2e} (effect size '
           f'{size:.2e}), per token {tok:.2e}', flush=True)
     assert mean <= 2e-3 and eff <= 1e-3
+
+
+@pytest.mark.parametrize('entry,sites', [(2, [FC, O]), (5, [MLP, ATTN]), (7, [FC, MLP])], ids=['fc-o-2', 'mlp-attn-5', 'fc-mlp-7'])
+def test_rerun_full_length(entry, sites):
+    """rerun at T = 2048 (the model's windows active: 1024 in blocks 0-2 and 4-6, 2048 in 3 and 7; 16 block-kernel
+    tiles per sequence, every jitter row of a 2048-token row-set) against the fp32 oracle: per-draw mean loss and
+    the jitter's effect within 1e-3, per token within 3e-2; and against rerun_tiled (the tiled kernels, another
+    summation order of the same bf16 products) per-draw mean within 1e-3."""
+    from types import SimpleNamespace
+    from noise_amd.dust import rerun, rerun_tiled
+    from noise_amd.model import make_model
+    model = make_model('cpu', 0)
+    with torch.no_grad():
+        model.lm_head.weight.mul_(30)
+    P = {k: v.detach().float().clone() for k, v in model.named_parameters()}
+    g = torch.Generator().manual_seed(61 + entry)
+    b, T, n = 1, 2048, 2
+    rows = torch.randint(0, 4096, (b, T + 1), generator=g)
+    x, y = rows[:, :-1], rows[:, 1:]
+    cache = odust.capture(P, x)
+    jitter = {}
+    for site in sites:
+        draws = (torch.randint(0, 2, (n * b, T, WIDTH[site]), generator=g) * 2 - 1).bfloat16()
+        jitter[site.format(entry)] = (0.1 * draws.float()).bfloat16()
+    print(f'rerun at T = {T}: entry {entry}, jitter at {list(jitter)}', flush=True)
+    ref = odust.rerun(P, cache, y, n, entry, jitter)
+    ref0 = odust.rerun(P, cache, y, n, entry, {})
+    dev = torch.device('cuda', 0)
+    to = lambda d: {k: v.to(dev) for k, v in d.items()}
+    dust = SimpleNamespace(model=model.to(dev), length=T, batch=b, outputs=to(cache['outputs']),
+                           blocks=to(cache['blocks']), x0=cache['x0'].to(dev), x=x.to(dev), y=y.to(dev),
+                           weights=[{k: (None if v is None else v.to(dev)) for k, v in odust.block_weights(P, i).items()}
+                                    for i in range(8)])
+    got = rerun(dust, n, entry, to(jitter)).cpu()
+    got0 = rerun(dust, n, entry, {}).cpu()
+    tiled = rerun_tiled(dust, n, entry, to(jitter)).cpu()
+    tok = (got - ref).abs().max().item()
+    mean = (got.mean(-1) - ref.mean(-1)).abs().max().item()
+    eff = ((got - got0).mean(-1) - (ref - ref0).mean(-1)).abs().max().item()
+    vs_tiled = (got.mean(-1) - tiled.mean(-1)).abs().max().item()
+    print(f'  per-token {tok:.2e}, per-draw mean {mean:.2e}, jitter effect {eff:.2e} (size '
+          f'{(ref - ref0).mean(-1).abs().max().item():.2e}), vs rerun_tiled {vs_tiled:.2e}', flush=True)
+    assert torch.isfinite(got).all()
+    assert tok <= 3e-2 and mean <= 1e-3 and eff <= 1e-3 and vs_tiled <= 1e-3
