@@ -188,7 +188,7 @@ def main():
     ap.add_argument('--steps', type=int, default=5)
     ap.add_argument('--warmup', type=int, default=2)
     ap.add_argument('--workload', choices=('population', 'orthogonal-fp32-head', 'update', 'head-error', 'dust-block',
-                                           'dust-rerun', 'attention', 'lowrank', 'cpu-forward'),
+                                           'dust-rerun', 'dust-direct', 'attention', 'lowrank', 'cpu-forward'),
                     default='population')
     ap.add_argument('--pairs', type=int, default=None,
                     help='update workload: antithetic pairs (default 512; the reference trains with 131072)')
@@ -223,6 +223,8 @@ def main():
         return bench_dust_block(args)
     if args.workload == 'dust-rerun':
         return bench_dust_rerun(args)
+    if args.workload == 'dust-direct':
+        return bench_dust_direct(args)
     if args.workload == 'attention':
         return bench_attention(args)
     if args.workload == 'lowrank':
@@ -551,6 +553,61 @@ def bench_dust_rerun(args):
         mean_loss=round(loss.mean().item(), 6), max_abs_vs_tiled=float((loss - tiled_loss).abs().max()),
         mean_abs_vs_tiled=float((loss.mean(-1) - tiled_loss.mean(-1)).abs().max()),
         finite=bool(torch.isfinite(loss).all().item()))), flush=True)
+
+
+def bench_dust_direct(args):
+    """DUST.direct_errors (run.py:332-378) as a step calls it for one block's sites: entry block 3, sites mlp.c_fc
+    (live units only) and attn.c_proj, 32 orthogonal draws in 2 reruns of 16 (nrep 16), 8 sequences x 2048 tokens,
+    sigma 0.1. The capture state is synthetic (normed random block input, random c_fc outputs for the live mask):
+    the work per call does not depend on its values."""
+    import torch
+    import torch.nn.functional as F
+    from types import SimpleNamespace
+    from noise_amd import dust as ndust
+    from noise_amd.model import make_model
+    from noise_amd.noise import OrthogonalDraws
+    dev = torch.device('cuda', 0)
+    b, T, draws, nrep, entry = 8, TOKENS, 32, 16, 3
+    model = make_model('cpu', 0).to(dev)
+    g = torch.Generator(device=dev).manual_seed(0)
+    x = torch.randint(0, 4096, (b, T), device=dev, generator=g)
+    y = torch.randint(0, 4096, (b, T), device=dev, generator=g)
+    with torch.no_grad():
+        emb = model.transformer.wte.weight[x].float()
+        x0 = F.rms_norm(emb, (512,))
+        block = F.rms_norm(torch.randn(b, T, 512, device=dev, generator=g), (512,))
+    outputs = {'transformer.wte': emb, f'transformer.h.{entry}.mlp.c_fc': torch.randn(b, T, 2048, device=dev, generator=g),
+               f'transformer.h.{entry}.attn.c_proj': torch.randn(b, T, 512, device=dev, generator=g)}
+    weights = [dict(q=blk.attn.c_q.weight, k=blk.attn.c_k.weight, v=blk.attn.c_v.weight,
+                    gate=blk.attn.ve_gate.weight if blk.attn.ve_gate is not None else None,
+                    proj=blk.attn.c_proj.weight, fc=blk.mlp.c_fc.weight, out=blk.mlp.c_proj.weight)
+               for blk in model.transformer.h]
+    draw = OrthogonalDraws(seed=0, device=dev)
+    state = SimpleNamespace(model=model, length=T, batch=b, outputs=outputs, blocks={entry: block}, x0=x0, x=x, y=y,
+                            weights=weights, clean_loss=8.3 + 0.1 * torch.randn(b, T, device=dev, generator=g),
+                            dtype=torch.bfloat16, recipe=SimpleNamespace(nrep=nrep), alpha={}, estimates={}, fits={},
+                            prior_sites=[],
+                            orthogonal_noise=lambda *a: draw(*a, dtype=torch.bfloat16))
+    sites = [f'transformer.h.{entry}.mlp.c_fc', f'transformer.h.{entry}.attn.c_proj']
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            ndust.direct_errors(state, sites, draws, 0.1, entry=entry)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(args.steps):
+            out = ndust.direct_errors(state, sites, draws, 0.1, entry=entry)
+        e.record()
+        torch.cuda.synchronize()
+    ms = s.elapsed_time(e) / args.steps
+    print(json.dumps(dict(
+        metric='DUST direct_errors throughput (2 sites of block 3, 32 draws in reruns of 16), sequence-token-draws/s',
+        value=round(draws * b * T / ms * 1e3), unit='token-draws/s', n_gpus=1, steps=args.steps, warmup=args.warmup,
+        ms_per_step=round(ms, 3), higher_is_better=True, scaling='weak', vs_baseline=None, dtype='bf16',
+        data='synthetic', config=dict(workload=f'{draws} draws x {b} sequences x {T} tokens from block {entry} of the '
+                                               'fixed 37.7M GPT, sites mlp.c_fc (live units) and attn.c_proj'),
+        ms_per_rerun=round(ms / (draws // nrep), 3),
+        finite=bool(all(torch.isfinite(v).all().item() for v in out.values())))), flush=True)
 
 
 def bench_attention(args):

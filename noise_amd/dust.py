@@ -158,12 +158,12 @@ SITES = {'o': 'o@{}', 'attn': 'transformer.h.{}.attn.c_proj', 'fc': 'transformer
 
 
 def _rotary(model, T, dev):
-    """The model's bf16 rotary tables for T tokens (utils/model.py:144-147 buffers when the model has them)."""
+    """The model's bf16 rotary tables for T tokens (utils/model.py:144-147 buffers when the model has them, else the
+    device tables built once per length: a copy from host memory per call would wait for the stream)."""
     if hasattr(model, 'cos'):
         return model.cos[:, :T], model.sin[:, :T]
-    from .model import rotary_tables
-    cos, sin = rotary_tables(T)
-    return cos.bfloat16().to(dev), sin.bfloat16().to(dev)
+    from .eggroll import _rope_tables
+    return _rope_tables(T, dev)
 
 
 def _weights(dust):
