@@ -393,6 +393,13 @@ int noise_coordinate_differences(const void *raw, int raw_bf16, int64_t rows, in
                                  const int64_t *targets, float sigma, float *out, int64_t out_width,
                                  int64_t out_stride, noise_stream_t stream);
 
+/* direct_errors' draws of one site for a chunk (run.py:344-349), in place and in one pass: a[i][r] *= mask[r] for
+ * i < n draws and r < per_draw (mask bf16 0/1 [per_draw], the live units of an mlp.c_fc site, or NULL), and
+ * scaled[i][r] = bf16(scale * a[i][r]) (the rerun's jitter sigma * a). bf16, 16 B aligned, per_draw a multiple
+ * of 8. */
+int noise_mask_scale(void *a, const void *mask, int64_t n, int64_t per_draw, float scale, void *scaled,
+                     noise_stream_t stream);
+
 /* DUST.direct_errors' estimate update (run.py:351-355) for one site and chunk of n draws:
  * errors[r][j] += scale * e[r][j], e = einsum('nbt,nbtd->btd', reward.to(bf16), a) with rows r = (b, t):
  * reward fp32 [n][rows], a bf16 [n][rows][d] (the site's draws), fp32 sums rounded to bf16 as the

@@ -49,6 +49,7 @@ SIGNATURES = {
     'noise_rerun_mix_norm': [_p, _i64, _p, _i64, _p, _p, _i64, _p, _p, _p],
     'noise_block_entry': [_p, _i64, _p, _i64, _p, _p, _p],
     'noise_add_bf16': [_p, _p, _i64, _p],
+    'noise_mask_scale': [_p, _p, _i64, _i64, _f32, _p, _p],
     'noise_pop_block_jit': [_p, 'View', _p, 'View', _p, _p, _i32, _p, _p, 'View', _p, _i32, _p, _p],
     'noise_pop_block_qkv_jit': [_p, 'View', _p, 'View', _p, _p, _p, _p, _p, 'View', _p, _p, _p, _p, _i64, _p, _i64, _p,
                                 _p, _p, _p],

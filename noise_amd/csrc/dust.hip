@@ -93,10 +93,45 @@ __global__ __launch_bounds__(256) void draw_errors_kernel(const float *__restric
     *reinterpret_cast<float4 *>(out + 4) = o1;
 }
 
+// direct_errors' per-chunk draw preparation (run.py:344-349): a[i][r] *= mask[r] for the n draws (mask bf16 0/1
+// over one draw's rows * d coordinates, or none) and scaled[i][r] = bf16(scale * a[i][r]), the jitter the rerun
+// adds. One thread per 8 coordinates.
+__global__ __launch_bounds__(256) void mask_scale_kernel(__bf16 *__restrict__ a, const __bf16 *__restrict__ mask,
+                                                         int64_t n8, int64_t per_draw8, float scale,
+                                                         __bf16 *__restrict__ scaled) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n8) return;
+    bf16x8 v = *reinterpret_cast<const bf16x8 *>(a + 8 * i);
+    if (mask) {
+        const bf16x8 m = *reinterpret_cast<const bf16x8 *>(mask + 8 * (i % per_draw8));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (__bf16)((float)v[e] * (float)m[e]);
+        *reinterpret_cast<bf16x8 *>(a + 8 * i) = v;
+    }
+    bf16x8 o;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = (__bf16)(scale * (float)v[e]);
+    *reinterpret_cast<bf16x8 *>(scaled + 8 * i) = o;
+}
+
 }  // namespace
 }  // namespace noise
 
 using namespace noise;
+
+extern "C" int noise_mask_scale(void *a, const void *mask, int64_t n, int64_t per_draw, float scale, void *scaled,
+                                noise_stream_t stream) {
+    clear_error();
+    const char *fn = "noise_mask_scale";
+    NOISE_CHECK_ARG(n >= 1 && per_draw >= 8 && per_draw % 8 == 0, "%s: n >= 1 and per_draw a positive multiple of 8", fn);
+    NOISE_CHECK_ARG(a && scaled && aligned(a, 16) && aligned(scaled, 16) && (!mask || aligned(mask, 16)),
+                    "%s: a, scaled (and mask) must be non-NULL and 16 B aligned", fn);
+    const int64_t n8 = n * per_draw / 8;
+    NOISE_CHECK_ARG((n8 + 255) / 256 < (1ll << 31), "%s: too many elements", fn);
+    hipLaunchKernelGGL(mask_scale_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       (__bf16 *)a, (const __bf16 *)mask, n8, per_draw / 8, scale, (__bf16 *)scaled);
+    return launch_status(fn);
+}
 
 extern "C" int noise_draw_errors(const float *reward, const void *a, int64_t n, int64_t rows, int64_t d, float scale,
                                  float *errors, noise_stream_t stream) {

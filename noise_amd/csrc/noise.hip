@@ -117,6 +117,53 @@ __global__ __launch_bounds__(kBlock) void orthogonal_kernel(void *__restrict__ o
     }
 }
 
+// The same draws, 8 coordinates per thread for 8 <= d <= 2048: a workgroup takes one draw i and a run of frame
+// positions f, threads tile each row in 8-wide chunks (d / 8 threads per row, 2048 / d rows side by side). For
+// a chunk at j0 (a multiple of 8), popcount(row & (j0 + e)) has the parity of popcount(row & j0) xor that of
+// popcount(row & e), the latter a byte of kLowParity indexed by row mod 8; the pattern bits of the chunk are
+// read once per workgroup; a row costs two index loads, a byte of logic and one 16 B (bf16) or 32 B store.
+constexpr uint64_t kLowParity = 0x963C5AF066CCAA00ull;  // byte r: bit e = popcount(r & e) mod 2, r, e < 8
+
+template <bool BF16>
+__global__ __launch_bounds__(kBlock) void orthogonal8_kernel(void *__restrict__ out, int64_t bt, int64_t d,
+                                                             int64_t index0, const int64_t *__restrict__ offset,
+                                                             const int64_t *__restrict__ pattern,
+                                                             const int64_t *__restrict__ sign, int64_t rows_per_block) {
+    const int tpr = (int)(d >> 3);                  // threads per row (d <= 2048: at most kBlock)
+    const int rpi = kBlock / tpr;                   // rows side by side
+    const int tr = threadIdx.x / tpr, tc = threadIdx.x - tr * tpr;
+    const int64_t i = blockIdx.y, index = index0 + i;
+    const int64_t j0 = 8 * (int64_t)tc;
+    const int64_t *pat = pattern + (index / d) * d + j0;
+    unsigned pbits = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pbits |= (unsigned)(pat[e] & 1) << e;
+    const int64_t f0 = (int64_t)blockIdx.x * rows_per_block;
+    const int64_t f1 = f0 + rows_per_block < bt ? f0 + rows_per_block : bt;
+    for (int64_t f = f0 + tr; f < f1; f += rpi) {
+        const int64_t row = (offset[f] + index) & (d - 1);
+        unsigned neg = (unsigned)(kLowParity >> (8 * (row & 7))) & 0xFFu;
+        neg ^= (__builtin_popcountll((uint64_t)(row & j0)) & 1) ? 0xFFu : 0u;
+        neg ^= pbits ^ ((sign[i * bt + f] & 1) ? 0xFFu : 0u);
+        const int64_t at = (i * bt + f) * d + j0;
+        if constexpr (BF16) {
+            uint32_t w[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w[k] = (0x3F80u | (((neg >> (2 * k)) & 1u) << 15)) |
+                       ((0x3F80u | (((neg >> (2 * k + 1)) & 1u) << 15)) << 16);
+            *reinterpret_cast<uint4 *>(static_cast<__bf16 *>(out) + at) = uint4{w[0], w[1], w[2], w[3]};
+        } else {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] = ((neg >> e) & 1u) ? -1.0f : 1.0f;
+            float *o = static_cast<float *>(out) + at;
+            *reinterpret_cast<float4 *>(o) = float4{v[0], v[1], v[2], v[3]};
+            *reinterpret_cast<float4 *>(o + 4) = float4{v[4], v[5], v[6], v[7]};
+        }
+    }
+}
+
 int grid_for(int64_t work) {
     int64_t g = (work + kBlock - 1) / kBlock;
     if (g > 65536) g = 65536;
@@ -255,6 +302,20 @@ extern "C" int noise_orthogonal_draws(void *out, int out_bf16, int64_t n, int64_
     NOISE_CHECK_ARG(out && offset && pattern && sign, "noise_orthogonal_draws: NULL pointer");
     NOISE_CHECK_ARG(aligned(out, out_bf16 ? 2 : 4) && aligned(offset, 8) && aligned(pattern, 8) && aligned(sign, 8),
                     "noise_orthogonal_draws: misaligned pointer");
+    if (d >= 8 && d <= 8 * kBlock && n <= 65535 && aligned(out, 16)) {
+        // rows per workgroup: about 16 row-iterations, at most 65535 workgroups along the frame
+        const int64_t rpi = kBlock / (d / 8);
+        int64_t rows = rpi * 16;
+        if ((bt + rows - 1) / rows > 65535) rows = (bt + 65534) / 65535;
+        const dim3 grid((unsigned)((bt + rows - 1) / rows), (unsigned)n);
+        if (out_bf16)
+            hipLaunchKernelGGL(orthogonal8_kernel<true>, grid, dim3(kBlock), 0, (hipStream_t)stream, out, bt, d, index0,
+                               offset, pattern, sign, rows);
+        else
+            hipLaunchKernelGGL(orthogonal8_kernel<false>, grid, dim3(kBlock), 0, (hipStream_t)stream, out, bt, d,
+                               index0, offset, pattern, sign, rows);
+        return launch_status("noise_orthogonal_draws");
+    }
     hipLaunchKernelGGL(orthogonal_kernel, dim3(grid_for(n * bt * d)), dim3(kBlock), 0, (hipStream_t)stream, out,
                        out_bf16, n, bt, d, index0, offset, pattern, sign);
     return launch_status("noise_orthogonal_draws");

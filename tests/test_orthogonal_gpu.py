@@ -44,8 +44,12 @@ def torch_orthogonal(seed, rank, world, calls):
 
 # (site, draws, chunk, n, b, t, d); every call stays within its site's draws (chunk * n + n <= draws), as
 # the reference's callers split a step's draws into chunks
+# the calls cover both kernels (8 <= d <= 2048: eight coordinates per thread; d = 4: one per thread), frames longer
+# than one workgroup's rows (300 x 8 positions at d = 512), draws across pattern cycles and d = 8, 16
 CALLS = [('q', 2048, 0, 1024, 1, 1, 512), ('k', 4096, 0, 1024, 1, 1, 2048), ('q', 2048, 1, 1024, 1, 1, 512),
-         ('tok', 48, 0, 16, 2, 64, 512), ('tok', 48, 1, 16, 2, 64, 512), ('small', 3, 0, 3, 1, 5, 4)]
+         ('tok', 48, 0, 16, 2, 64, 512), ('tok', 48, 1, 16, 2, 64, 512), ('small', 3, 0, 3, 1, 5, 4),
+         ('wide', 4096, 1, 2048, 2, 3, 2048), ('frame', 64, 1, 32, 8, 300, 512), ('d8', 32, 0, 32, 3, 7, 8),
+         ('d16', 48, 1, 24, 4, 40, 16)]
 
 
 def test_calls_are_valid():
