@@ -339,7 +339,7 @@ def direct_errors(dust, sites, draws, sigma, entry=None, gamma=0.0, retrieved=No
     width = {s: _site_width(dust, s) for s in sites}
     errors = {s: torch.zeros(b, t, width[s], dtype=F32, device=dev) for s in sites}
     # an mlp.c_fc site is jittered at its live units only (ReLU is flat below 0); its prior is masked alike
-    live = {s: (dust.outputs[s] > 0).to(dtype).contiguous() for s in sites if s.endswith('mlp.c_fc')}
+    live = {s: (dust.outputs[s] > 0).to(BF16).contiguous() for s in sites if s.endswith('mlp.c_fc')}
     for s, mask in live.items():
         if s in priors:
             priors[s] = priors[s] * mask.float()
@@ -349,15 +349,14 @@ def direct_errors(dust, sites, draws, sigma, entry=None, gamma=0.0, retrieved=No
         a, jitter = {}, {}
         for s in sites:
             draw = dust.orthogonal_noise(s, draws, chunk, n, b, t, width[s])
-            if draw.dtype == BF16 and draw.is_contiguous() and width[s] % 8 == 0:
-                # the live-unit mask in place and the jitter sigma * a in one pass (noise_mask_scale)
-                scaled = torch.empty_like(draw)
-                _lib.call('noise_mask_scale', draw.data_ptr(), _lib.ptr(live.get(s)), n, b * t * width[s],
-                          float(sigma), scaled.data_ptr(), _lib.stream_ptr(dev))
-            else:
-                if s in live:
-                    draw = draw * live[s]
-                scaled = sigma * draw
+            if draw.dtype != BF16 or draw.device != dev or draw.shape != (n, b, t, width[s]):
+                raise ValueError(f'direct_errors: the draws of {s!r} must be bf16 [{n}, {b}, {t}, {width[s]}] on '
+                                 f'{dev} (the reference draws in bf16 on a GPU), got {draw.dtype} {tuple(draw.shape)}')
+            # the live-unit mask in place and the jitter sigma * a in one pass (noise_mask_scale)
+            draw = draw.contiguous()
+            scaled = torch.empty_like(draw)
+            _lib.call('noise_mask_scale', draw.data_ptr(), _lib.ptr(live.get(s)), n, b * t * width[s], float(sigma),
+                      scaled.data_ptr(), _lib.stream_ptr(dev))
             a[s] = draw.reshape(n * b, t, width[s])
             jitter[s] = scaled.reshape(n * b, t, width[s])
         loss = rerun(dust, n, entry, jitter)
