@@ -410,3 +410,35 @@ def test_rerun_full_length(entry, sites):
           f'{(ref - ref0).mean(-1).abs().max().item():.2e}), vs rerun_tiled {vs_tiled:.2e}', flush=True)
     assert torch.isfinite(got).all()
     assert tok <= 3e-2 and mean <= 1e-3 and eff <= 1e-3 and vs_tiled <= 1e-3
+
+
+def test_rerun_row_kernels():
+    """The rerun's row kernels against torch on the same inputs: noise_mask_scale (a * mask in place and
+    bf16(sigma * a), run.py:344-349) and noise_add_bf16 (y + o in bf16, run.py:114) bit for bit; noise_block_entry
+    (x + attn jitter in fp32, bit for bit, and bf16(norm(x)) to one bf16 step; rows read modulo the cached rows)."""
+    from noise_amd import _lib
+    dev = torch.device('cuda', 0)
+    g = torch.Generator(device=dev).manual_seed(71)
+    n, b, t, d = 3, 2, 256, 2048
+    a = (torch.randint(0, 2, (n, b, t, d), device=dev, generator=g) * 2 - 1).bfloat16()
+    mask = (torch.rand(b, t, d, device=dev, generator=g) > 0.4).bfloat16()
+    want_a, want_j = a * mask, 0.1 * (a * mask)
+    scaled = torch.empty_like(a)
+    _lib.call('noise_mask_scale', a.data_ptr(), mask.data_ptr(), n, b * t * d, 0.1, scaled.data_ptr(),
+              _lib.stream_ptr(dev))
+    assert torch.equal(a, want_a) and torch.equal(scaled, want_j)
+    y = torch.randn(4, 256, 512, device=dev, generator=g).bfloat16()
+    o = (0.1 * torch.randn(4, 256, 512, device=dev, generator=g)).bfloat16()
+    want = y + o
+    _lib.call('noise_add_bf16', y.data_ptr(), o.data_ptr(), y.numel(), _lib.stream_ptr(dev))
+    assert torch.equal(y, want)
+    x = torch.randn(2, 256, 512, device=dev, generator=g) * 3
+    add = (0.1 * torch.randn(6, 256, 512, device=dev, generator=g)).bfloat16()
+    out = torch.empty(6, 256, 512, device=dev)
+    h = torch.empty(6, 256, 512, dtype=torch.bfloat16, device=dev)
+    _lib.call('noise_block_entry', x.data_ptr(), 2 * 256, add.data_ptr(), 6 * 256, out.data_ptr(), h.data_ptr(),
+              _lib.stream_ptr(dev))
+    xr = x.repeat(3, 1, 1)
+    assert torch.equal(out, xr + add.float())
+    href = torch.nn.functional.rms_norm(xr, (512,))
+    assert ((h.float() - href).abs() <= href.abs() * 2 ** -7 + 1e-6).all()
