@@ -132,13 +132,29 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
     const int tok = t0 + 16 * wave + tl;
     const int64_t row = (int64_t)m * T + tok;
     const unsigned lbase = lds_addr(lds);
+    // the next block's mixing scalars, read at entry so that the epilogue does not wait for them (wave-uniform)
+    float rl = 0.f, ml = 0.f;
+    if constexpr (MIX) {
+        rl = *p.lam_r;
+        ml = *p.lam_x;
+        if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
+        if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
+        rl = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, rl)));
+        ml = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, ml)));
+    }
 
-    // per-member vectors into LDS (zeros when a matrix is unperturbed, so no branches later)
+    // per-member vectors into LDS (zeros when a matrix is unperturbed, so no branches later), by direct copies of
+    // 1 KiB per wave-wide copy that land with the rows below (a load, a wait and an LDS store per vector would be
+    // one global round trip each)
     if constexpr (!kJit) {
-        auto vcopy = [&](const float *src, int off, int n) {
-            float *dst = reinterpret_cast<float *>(lds + off);
-            for (int i = tid; i < n / 4; i += kBlkThreads)
-                st4(dst + 4 * i, src ? ld4(src + 4 * i) : float4{0.f, 0.f, 0.f, 0.f});
+        auto vcopy = [&](const float *src, int off, int n) {  // n a multiple of 256
+            if (src) {
+                for (int c = wave; c < n / 256; c += kBlkThreads / 64)
+                    lds_dma16_at(src + 256 * c, (unsigned)(16 * lane), lbase + off + 1024 * c);
+            } else {
+                float *dst = reinterpret_cast<float *>(lds + off);
+                for (int i = tid; i < n / 4; i += kBlkThreads) st4(dst + 4 * i, float4{0.f, 0.f, 0.f, 0.f});
+            }
         };
         vcopy(p.afc ? p.afc + dir * p.afc_stride : nullptr, kVAfc, kHidden);
         vcopy(p.apj ? p.bpj + dir * p.bpj_stride : nullptr, kVBpj, kHidden);
@@ -406,14 +422,14 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
     }
 
     // ---- epilogue: y = out + sign (hid . b_proj) a_proj [, mixing], RMSNorm, next dots, stores
-    const float corr = p.apj ? sgn * token_sum(pd) : 0.f;
-    float rl = 0.f, ml = 0.f;
-    if constexpr (MIX) {
-        rl = *p.lam_r;
-        ml = *p.lam_x;
-        if (p.eps_r) rl += sgn * p.eps_r[dir * p.eps_stride];
-        if (p.eps_x) ml += sgn * p.eps_x[dir * p.eps_stride];
+    // QKV: the next block's per-token scalars (rotary rows, value-table row) in flight under the epilogue
+    QkvLane L;
+    if constexpr (QKV != 0) {
+        L.m = m; L.t0 = t0; L.tok = tok; L.wave = wave; L.lane = lane; L.tid = tid; L.dir = dir; L.row = row;
+        L.sgn = sgn;
+        qkv_token_scalars<QKV == 2>(p.q, L);
     }
+    const float corr = p.apj ? sgn * token_sum(pd) : 0.f;
     float ssq = 0.f;
     {
         const float *apj = reinterpret_cast<const float *>(lds + kVApj) + 4 * g;
@@ -500,10 +516,7 @@ __global__ __launch_bounds__(kBlkThreads, 1) void block_kernel(BlockArgs p) {
         __syncthreads();  // every wave has read back its staged rows: the stage buffers are free
 #pragma unroll
         for (int k = 0; k < 3; ++k) qkv_issue(p.q, lbase, wave, lane, k);
-        QkvLane L;
-        L.m = m; L.t0 = t0; L.tok = tok; L.wave = wave; L.lane = lane; L.tid = tid; L.dir = dir; L.row = row;
-        L.sgn = sgn; L.dq0 = dq[0]; L.dq1 = dq[1]; L.dq2 = dq[2];
-        qkv_token_scalars<QKV == 2>(p.q, L);
+        L.dq0 = dq[0]; L.dq1 = dq[1]; L.dq2 = dq[2];
         vm_wait<0>();  // the three stages and the scalars landed
         __syncthreads();
         qkv_phase<QKV == 2, true>(p.q, lds, xf, L);

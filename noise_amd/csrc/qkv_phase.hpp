@@ -130,20 +130,24 @@ __device__ __forceinline__ void gather_h32(const bf16x8 &x0, int tl, float (&xg)
         }
 }
 
-// gate of value head hd: 2 sigmoid(h[:32] . gate_w[hd] + sign (h[:32] . gate_b[dir]) gate_a[dir][hd]), summed over
-// features 0 .. 31 in order, as noise_pop_gate sums them (eggroll.py:88, utils/model.py:89)
-__device__ __forceinline__ float local_gate(const QkvRowsArgs &p, const float (&xg)[32], float sgn, int dir, int hd) {
+// the gates of the 8 value heads: 2 sigmoid(h[:32] . gate_w[hd] + sign (h[:32] . gate_b[dir]) gate_a[dir][hd]), each
+// summed over features 0 .. 31 in order, as noise_pop_gate sums them (eggroll.py:88, utils/model.py:89)
+__device__ __forceinline__ void local_gates(const QkvRowsArgs &p, const float (&xg)[32], float sgn, int dir,
+                                            float (&gates)[8]) {
     float dg = 0.f;
     if (p.gate_a) {
 #pragma unroll
         for (int c = 0; c < 32; ++c) dg += xg[c] * p.gate_b[dir * p.gate_b_stride + c];
         dg *= sgn;
     }
-    float z = 0.f;
 #pragma unroll
-    for (int c = 0; c < 32; ++c) z += xg[c] * p.gate_w[hd * 32 + c];
-    if (p.gate_a) z += dg * p.gate_a[dir * p.gate_a_stride + hd];
-    return 2.0f / (1.0f + __expf(-z));
+    for (int hd = 0; hd < 8; ++hd) {
+        float z = 0.f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) z += xg[c] * p.gate_w[hd * 32 + c];
+        if (p.gate_a) z += dg * p.gate_a[dir * p.gate_a_stride + hd];
+        gates[hd] = 2.0f / (1.0f + __expf(-z));
+    }
 }
 
 // stage k of the phase: rows 64 (s % 8) + 32 (k % 2) .. + 32 of matrix s / 8 (s = k / 2) as [8 k tiles][32
@@ -208,6 +212,15 @@ __device__ __forceinline__ void qkv_phase(const QkvRowsArgs &p, char *lds, const
         }
     };
 
+    // GATE_LOCAL: the token's 8 value-head gates, once for the phase (NaN for a token id outside the table)
+    float gates[8];
+    if constexpr (VE && GATE_LOCAL) {
+        float xg[32];
+        gather_h32(xf[0], tl, xg);
+        local_gates(p, xg, L.sgn, dir, gates);
+#pragma unroll
+        for (int hd = 0; hd < 8; ++hd) gates[hd] = bad ? __builtin_nanf("") : gates[hd];
+    }
     f32x4 acc[4];
     float4 av[4], ev[4], bv[4];  // the head's epilogue inputs (rank-1 a; value rows and value-table b)
     float gate = 0.f;
@@ -226,8 +239,9 @@ __device__ __forceinline__ void qkv_phase(const QkvRowsArgs &p, char *lds, const
                 flush_vt(vt_pending);
                 vt_pending = -1;
             }
-            if (h == 1) {
-                // the epilogue's inputs, under this stage's products
+            if (h == 0) {
+                // the head's epilogue inputs, issued a stage before the epilogue: waiting for them then also waits
+                // only for copies that had a stage to land (the vector memory counter retires in issue order)
                 if (p.a[mat]) {
                     const float *ar = p.a[mat] + dir * p.a_stride[mat] + 64 * hd + 4 * g;
 #pragma unroll
@@ -236,9 +250,9 @@ __device__ __forceinline__ void qkv_phase(const QkvRowsArgs &p, char *lds, const
                 if constexpr (VE) {
                     if (mat == 2) {
                         if constexpr (GATE_LOCAL) {
-                            float xg[32];
-                            gather_h32(xf[0], tl, xg);
-                            gate = bad ? __builtin_nanf("") : local_gate(p, xg, L.sgn, dir, hd);
+                            gate = gates[0];
+#pragma unroll
+                            for (int i = 1; i < 8; ++i) gate = hd == i ? gates[i] : gate;
                         } else {
                             gate = bad ? __builtin_nanf("") : p.gates[row * 8 + hd];
                         }
