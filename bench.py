@@ -65,8 +65,8 @@ PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'profiles', '
 # entry point (bench label) -> the kernel name in the committed trace of the default workload (the block
 # kernels that form the next block's q/k/v: 4 of their 7 launches carry value embeddings)
 ROCPROF_NAME = {'noise_pop_qkv': 'qkv16_kernel<false>', 'noise_pop_head_ce': 'head_x_kernel<false, false>',
-                'noise_pop_block_qkv[block]': 'block_kernel<true, 3, false, 2>',
-                'noise_pop_block[block]': 'block_kernel<false, 0, false, 0>'}
+                'noise_pop_block_qkv[block]': 'block_kernel<true, 3, false, 2, 0>',
+                'noise_pop_block[block]': 'block_kernel<false, 0, false, 0, 0>'}
 
 
 def profiled_traffic(kernel):
