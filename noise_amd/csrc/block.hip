@@ -109,10 +109,7 @@ struct BlockArgs {
 };
 
 // sum over the four lanes holding one token's features (l % 16 + 16 g)
-__device__ __forceinline__ float token_sum(float v) {
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
-}
+__device__ __forceinline__ float token_sum(float v) { return sum_lanes_16_32(v); }
 
 // QKV: 0, or the next block's q/k/v after the tail (1; 2 with its value embeddings) in place of the hout and
 // next_dots stores

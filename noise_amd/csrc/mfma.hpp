@@ -112,6 +112,22 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 // Value of lane (l ^ 32): the other half of a 32x32 MFMA column.
 __device__ __forceinline__ float swap_halves(float x) { return __shfl_xor(x, 32, 64); }
 
+// The sum over the four lanes l % 16 + 16 g, in the order two xor shuffles give it:
+// (v[l] + v[l ^ 16]) + (v[l ^ 32] + v[l ^ 48]). It uses gfx950's lane swaps (VALU) instead of two LDS permutes.
+// A swap exchanges half of one register with half of another. Given two copies of a value, every lane ends up
+// with its own value in one register and its partner's in the other. fp32 addition commutes, so each lane's sum
+// is bitwise the shuffles' sum. The swaps are inline asm because the compiler's builtin loses its second result.
+// A VALU write read by a lane swap needs two wait states: hence the s_nop.
+__device__ __forceinline__ float sum_lanes_16_32(float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    v = a + b;
+    a = v;
+    b = v;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    return a + b;
+}
+
 // orders this wave's LDS writes before its lanes read what other lanes of the wave wrote (the compiler
 // otherwise reasons per lane and may move such a read ahead of the writes)
 __device__ __forceinline__ void wave_lds_sync() {

@@ -89,10 +89,7 @@ inline QkvRowsArgs qkv_rows_args(const noise_population_t *pop, noise_view_t x, 
     return a;
 }
 
-__device__ __forceinline__ float token_sum4(float v) {
-    v += __shfl_xor(v, 16, 64);
-    return v + __shfl_xor(v, 32, 64);
-}
+__device__ __forceinline__ float token_sum4(float v) { return sum_lanes_16_32(v); }
 
 // the per-token scalars of the phase's epilogues: rotary rows, value-table row and its noise scale
 template <bool VE>
