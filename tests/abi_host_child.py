@@ -64,6 +64,28 @@ assert need > cap
 w7 = (ctypes.c_void_p * 7)(*([16] * 7))
 assert lib.noise_dust_block_static(16, 16, 64, 2048, w7, 16, 16, 16, 1024, None, None, None, None, None) == -1
 assert 'static array holds' in message()
+# the grouped noise gather: the descriptor's group count, widths and packing, the rows per call and the row stride
+sg = abi.SliceGroups()
+gather = lambda nrows, ld: lib.noise_gather_slice_groups(16, nrows, ld, ctypes.byref(sg), None, 1 << 20, 0, 0, 1 << 19,
+                                                         None)
+for count in (0, abi.SLICE_GROUPS_MAX + 1):
+    sg.count = count
+    assert gather(4, 1 << 16) == -1 and f'got {count}' in message()
+sg.count = 2
+sg.offsets[0] = sg.offsets[1] = 16
+sg.width[0], sg.width[1], sg.col[0], sg.col[1] = 256, 300, 0, 256
+assert gather(4, 1 << 16) == -1 and 'group 1' in message()      # width not a multiple of 256
+sg.width[1], sg.col[1] = 256, 200
+assert gather(4, 1 << 16) == -1 and 'column 256' in message()   # not packed in order
+sg.col[1] = 256
+assert gather(4, 300) == -1 and 'row stride 300' in message()   # below the total width of 512
+assert gather(70000, 1 << 16) == -1 and 'rows per call' in message()
+# direct_errors' mask-and-scale pass and the rerun's row kernels
+assert lib.noise_mask_scale(16, None, 2, 12, 0.1, 16, None) == -1 and 'multiple of 8' in message()
+assert lib.noise_mask_scale(8, None, 2, 16, 0.1, 16, None) == -1 and '16 B aligned' in message()
+assert lib.noise_block_entry(16, 4, 8, 4, 16, 16, None) == -1 and 'add must be 16 B aligned' in message()
+assert lib.noise_add_bf16(16, 16, 12, None) == -1 and 'multiple of 8' in message()
+assert lib.noise_rerun_mix_norm(16, 4, 16, 4, None, None, 4, 16, 16, None) == -1 and 'lambdas' in message()
 print('targeted invalid arguments: rejected', flush=True)
 
 # concurrent calls: each thread's message is its own call's
