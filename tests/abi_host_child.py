@@ -86,6 +86,15 @@ assert lib.noise_mask_scale(8, None, 2, 16, 0.1, 16, None) == -1 and '16 B align
 assert lib.noise_block_entry(16, 4, 8, 4, 16, 16, None) == -1 and 'add must be 16 B aligned' in message()
 assert lib.noise_add_bf16(16, 16, 12, None) == -1 and 'multiple of 8' in message()
 assert lib.noise_rerun_mix_norm(16, 4, 16, 4, None, None, 4, 16, 16, None) == -1 and 'lambdas' in message()
+# the jittered block kernel: no jitter, misaligned jitter rows, no zero row for a block without mlp.c_proj jitter
+pop_j = abi.Population(2, 256, None, 1, 0)
+y_j = abi.View(256, 256 * 512, 512)
+for (fc, mlp, zero), text in (((None, None, None), 'NULL or empty'), ((8, None, 256), '16 B aligned'),
+                              ((256, None, None), 'zero row')):
+    jit = abi.BlockJitter(fc, mlp, zero)
+    assert lib.noise_pop_block_jit(ctypes.byref(pop_j), y_j, 256, y_j, 256, 256, 0, None, None, abi.View(None, 0, 0),
+                                   256, 1, ctypes.byref(jit), None) == -1
+    assert text in message(), message()
 print('targeted invalid arguments: rejected', flush=True)
 
 # concurrent calls: each thread's message is its own call's
