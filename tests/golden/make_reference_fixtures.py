@@ -1,6 +1,6 @@
 """Writes tests/golden/reference_fixtures.npz from the reference's own code, imported from
-/root/reference on the CPU of the build container (the reference never travels to the GPU box; only these
-vectors do). It pins what no closed form or library routine pins:
+/root/reference on the CPU (the tests that run on the GPU never need the reference itself, only these vectors).
+It pins what no closed form or library routine pins:
 
   init_*    sha256 of every tensor of the reference's seed-0 model (train/val/eggroll.py:38-53
             make_model('cpu', 0), fp32 bytes in state_dict order)
