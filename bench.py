@@ -72,7 +72,7 @@ ROCPROF_NAME = {'noise_pop_qkv': 'qkv16_kernel<false>', 'noise_pop_head_ce': 'he
 def profiled_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 summary (FETCH_SIZE + WRITE_SIZE, scaled
     by the 1 GiB copy calibration), or None."""
-    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel<true>' if kernel.startswith('noise_attention') else None)
+    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel<true, false>' if kernel.startswith('noise_attention') else None)
     if not name or not os.path.exists(PROFILE):
         return None
     for line in open(PROFILE):
@@ -88,7 +88,7 @@ def profiled_traffic(kernel):
 def profiled_mfma_busy(kernel):
     """The kernel's MFMA-busy fraction from the committed counter table (SQ_VALU_MFMA_BUSY_CYCLES over the
     cycles it ran, on its own clock), or None."""
-    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel<true>' if kernel.startswith('noise_attention') else None)
+    name = ROCPROF_NAME.get(kernel) or ('attention_vt_kernel<true, false>' if kernel.startswith('noise_attention') else None)
     if not name or not os.path.exists(PROFILE):
         return None
     col = None

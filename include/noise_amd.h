@@ -104,6 +104,7 @@ int noise_orthogonal_draws(void *out, int out_bf16, int64_t n, int64_t bt, int64
  * q, k, o: element (b, t, h, d) at b*s_b + h*s_h + t*s_t + d (the reference's [B, T, H, D] and its
  * transposes are all expressible). v: the same with vs_x = token stride, or, with flag
  * NOISE_ATTN_V_TRANSPOSED, element (b, t, h, d) at b*vs_b + h*vs_h + d*vs_x + t. head_dim must be 64.
+ * A seq in whole 256-query tiles runs the ring kernel with either V layout, other lengths the general one.
  * NOISE_ATTN_QK_NORMED: the caller guarantees every q and k row has RMS <= 1, as RMSNorm outputs do (the
  * reference normalises both, utils/model.py:94); scores are then bounded and the softmax runs with a
  * fixed shift instead of a running maximum (same result; rows that break the promise by less than a
@@ -115,9 +116,9 @@ int noise_orthogonal_draws(void *out, int out_bf16, int64_t n, int64_t bt, int64
 #define NOISE_ATTN_QK_NORMED 2
 
 /* V element (b, t, h, d) at b*vs_b + h*vs_h + t*vs_t + d -> vt [batch][heads][64][seq] contiguous, the
- * NOISE_ATTN_V_TRANSPOSED layout (no counterpart in the reference: the attention(q, k, v, window) drop-in,
- * utils/model.py:24-31, transposes V with it so that noise_attention_fwd runs its transposed-V kernel).
- * seq a multiple of 64, head_dim 64. */
+ * NOISE_ATTN_V_TRANSPOSED layout that the population path writes (no counterpart in the reference; a layout
+ * utility: noise_attention_fwd takes V in either layout, so the attention(q, k, v, window) drop-in,
+ * utils/model.py:24-31, passes V as it is). seq a multiple of 64, head_dim 64. */
 int noise_v_transpose(const void *v, int64_t batch, int64_t heads, int64_t seq, int64_t head_dim, int64_t vs_b,
                       int64_t vs_h, int64_t vs_t, void *vt, noise_stream_t stream);
 int noise_attention_fwd(const void *q, const void *k, const void *v, void *o, int64_t batch, int64_t heads,

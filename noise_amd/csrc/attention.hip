@@ -12,10 +12,10 @@
 // O^T = V^T P^T with the key index permuted identically on both sides, so P never touches LDS.
 //  - attention_fwd_kernel (any layout and length): 4 waves of 64 queries, K / V tiles register-staged
 //    into double-buffered LDS (rows padded to 144 B), running-max softmax.
-//  - attention_vt_kernel (transposed V, length a multiple of 256; the population path): 8 waves of 32
-//    queries (four waves per SIMD) in two groups half a tile apart, K / V^T copied global -> LDS into a
-//    four-stage swizzled ring, and an optional fixed-shift softmax for RMS-normed q, k (described at the
-//    kernel).
+//  - attention_vt_kernel (length a multiple of 256; V transposed, the population path, or natural, the
+//    drop-in's): 8 waves of 32 queries (four waves per SIMD) in two groups half a tile apart, K and V (or V^T)
+//    copied global -> LDS into a four-stage swizzled ring, and an optional fixed-shift softmax for RMS-normed
+//    q, k (described at the kernel).
 // Key tiles outside a wave's band are skipped; masking runs only on band-edge tiles. All query tiles of
 // one head run on one XCD (workgroups are dispatched round-robin over the 8 XCDs), heaviest tile first,
 // so that head's K/V stay in that XCD's L2.
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
 
 
 // ------------------------------------------------------------------------------------------------
-// Transposed-V kernel (the population layout; seq a multiple of 256). K and V^T tiles are copied
+// Ring kernel (seq a multiple of 256; shown for V^T, the population layout). K and V^T tiles are copied
 // global -> LDS directly (global_load_lds_dwordx4) into a ring of four stages, rows of 128 B with the
 // 16 B chunks XOR-swizzled by row pair (conflict-free fragment reads). The K rows of each 32-key block
 // are read in the order sigma (bits 2 and 3 of the key index swapped), which makes register r of a
@@ -296,7 +296,9 @@ __device__ __forceinline__ int key_sigma(int i) { return (i & ~12) | ((i & 4) <<
 // Both groups pass the same barriers (one per tile), placed at different points of their loops. A alone
 // copies the K / V^T tiles (4 copies per wave per tile) into a 4-slot ring; after barrier t + 1 it refills
 // the slot of tile t - 1, which B finished reading before that barrier.
-template <bool BOUNDED>
+// VNAT: V in its natural layout [.., token, dim] (the drop-in's), copied as K is, with the 16 B chunks of row R
+// swizzled by 2 (R % 4) instead, and each V^T fragment put together from two transposing LDS reads.
+template <bool BOUNDED, bool VNAT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void attention_vt_kernel(AttnArgs a) {
     constexpr int QT = kVtQT, NS = 4;
     constexpr int QB = 1, NW = QT / 32, QW = 32, CPW = 4;  // waves, queries per wave, copies per A wave
@@ -350,9 +352,13 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     // or V^T. Row R's slot P holds chunk P ^ ((R >> 1) & 7); for this lane R = 8 c' + lane / 8, so the chunk
     // it fetches is (lane % 8) ^ (4 (c' & 1) + lane / 16), the same for all of a wave's copies (c' & 1 = w & 1).
     const int chunk = (lane & 7) ^ (4 * (wave & 1) + (lane >> 4));
+    // VNAT: row R = 8 c' + lane / 8 of a V tile keeps chunk C at slot C ^ 2 (R % 4), R % 4 = (lane / 8) % 4. The
+    // four rows that one transposing read takes from each group of 16 lanes then lie in four different 32 B
+    // of a 128 B row (the row-pair swizzle of K would put all four on the same banks)
+    const int vchunk = VNAT ? (lane & 7) ^ (2 * ((lane >> 3) & 3)) : chunk;
     const bool group_a = wave < 4;
     const unsigned koff = (unsigned)((lane >> 3) * a.ks_t * 2 + chunk * 16);
-    const unsigned voff = (unsigned)((lane >> 3) * a.vs_x * 2 + chunk * 16);
+    const unsigned voff = (unsigned)((lane >> 3) * a.vs_x * 2 + vchunk * 16);
     const unsigned lb = lds_addr(lds);
     auto issue = [&](int k0, unsigned st) {  // st: LDS byte address of the stage
 #pragma unroll
@@ -360,6 +366,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
             const int c = 4 * i + wave;  // A waves only: copy c's row parity is the wave's
             if (c < 8)
                 lds_dma16_at(Kb + (int64_t)(k0 + 8 * c) * a.ks_t, koff, st + c * 1024);
+            else if constexpr (VNAT)
+                lds_dma16_at(Vb + (int64_t)(k0 + 8 * (c - 8)) * a.vs_x, voff, st + c * 1024);
             else
                 lds_dma16_at(Vb + (int64_t)(8 * (c - 8)) * a.vs_x + k0, voff, st + c * 1024);
         }
@@ -372,6 +380,12 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         kfo[s] = sj * 128 + (((2 * s + hf) ^ ((sj >> 1) & 7)) << 4);
         vfo[s] = 64 * 128 + j * 128 + (((2 * s + hf) ^ ((j >> 1) & 7)) << 4);
     }
+    // VNAT: the fragment of lane j + 32 hf (dims j (+ 32 db), keys 16 s + 8 hf .. + 8) from two transposing reads
+    // (keys + 0 .. 3, + 4 .. 7): as a source, lane 16 g + i addresses key 8 (g / 2) + i / 4 (+ 16 s, + 4), dims
+    // 16 (g % 2) + 4 (i % 4) .. + 4 (+ 32 db, which flips bit 2 of the chunk: byte offset ^ 64)
+    const int vnr = 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int vnb = 64 * 128 + vnr * 128 +
+                    (((2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) ^ (2 * (vnr & 3))) << 4) + 8 * (lane & 1);
 
     float m[QB], l[QB];
     f32x16 o[2][QB];
@@ -495,7 +509,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
             for (int db = 0; db < 2; ++db) {
-                const bf16x8 va = *reinterpret_cast<const bf16x8 *>(st + vfo[s] + db * 32 * 128);
+                bf16x8 va;
+                if constexpr (VNAT) {
+                    const char *p = st + (vnb ^ (64 * db)) + 2048 * s;
+                    const bf16x4 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 512);
+                    va = bf16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                } else {
+                    va = *reinterpret_cast<const bf16x8 *>(st + vfo[s] + db * 32 * 128);
+                }
 #pragma unroll
                 for (int qb = 0; qb < QB; ++qb) o[db][qb] = mfma32x32x16(va, pf[qb][s], o[db][qb]);
             }
@@ -590,6 +611,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 
 
 
+
 // V [b, t, h, d] (d contiguous) -> V^T [b][h][d][t]: one workgroup per (b*h, 64-token tile); each thread
 // reads two 16 B pieces of token rows and writes two 16 B pieces of dim rows through a padded LDS tile.
 __global__ __launch_bounds__(256) void v_transpose_kernel(const __bf16 *v, int64_t vs_b, int64_t vs_h, int64_t vs_t,
@@ -668,7 +690,8 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     NOISE_CHECK_ARG(dot_out == nullptr || (dot_vec != nullptr && dot_div >= 1),
                     "noise_attention_fwd: dot_out needs dot_vec and dot_div >= 1");
     int64_t bh = batch * heads;
-    const bool vt_path = v_transposed && seq % kVtQT == 0;
+    // lengths in whole 256-query tiles run the ring kernel, with V in either layout
+    const bool vt_path = seq % kVtQT == 0;
     const int64_t qtile = vt_path ? kVtQT : kBQ;
     int64_t qtiles = (seq + qtile - 1) / qtile;
     NOISE_CHECK_ARG(bh * qtiles < (1ll << 31), "noise_attention_fwd: too many workgroups");
@@ -691,10 +714,10 @@ extern "C" int noise_attention_fwd(const void *q, const void *k, const void *v, 
     a.shift = kD * fabsf(scale) * kLog2e * 1.0079f;
     dim3 grid((unsigned)(bh * qtiles));
     if (vt_path) {
-        if (flags & NOISE_ATTN_QK_NORMED)
-            hipLaunchKernelGGL(attention_vt_kernel<true>, grid, dim3(512), 0, (hipStream_t)stream, a);
-        else
-            hipLaunchKernelGGL(attention_vt_kernel<false>, grid, dim3(512), 0, (hipStream_t)stream, a);
+        const bool bounded = flags & NOISE_ATTN_QK_NORMED;
+        auto kernel = v_transposed ? (bounded ? attention_vt_kernel<true, false> : attention_vt_kernel<false, false>)
+                                   : (bounded ? attention_vt_kernel<true, true> : attention_vt_kernel<false, true>);
+        hipLaunchKernelGGL(kernel, grid, dim3(512), 0, (hipStream_t)stream, a);
     } else if (v_transposed)
         hipLaunchKernelGGL(attention_fwd_kernel<true>, grid, dim3(256), 0, (hipStream_t)stream, a);
     else

@@ -128,6 +128,18 @@ __device__ __forceinline__ float sum_lanes_16_32(float v) {
     return a + b;
 }
 
+// gfx950's transposing LDS read (ds_read_b64_tr_b16). Every lane gives the address of 8 B (four 16-bit
+// elements). Within each group of 16 lanes, lane i receives as its element e (e = 0 .. 3) element i % 4 of
+// the 8 B that lane i / 4 + 4 e of its group addressed. So if lane s of a group points at row r0 + s / 4,
+// columns c0 + 4 (s % 4) .. + 4 of a row-major matrix, lane i receives column c0 + i of rows r0 .. r0 + 3.
+__device__ __forceinline__ bf16x4 lds_read_tr16(const void *p) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4 *)p);
+    bf16x4 r;
+    __builtin_memcpy(&r, &v, 8);
+    return r;
+}
+
 // orders this wave's LDS writes before its lanes read what other lanes of the wave wrote (the compiler
 // otherwise reasons per lane and may move such a read ahead of the writes)
 __device__ __forceinline__ void wave_lds_sync() {

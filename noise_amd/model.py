@@ -166,22 +166,12 @@ def attention(q, k, v, window):
     B, T, H, D = q.shape
     qb, kb, vb = _operand(q), _operand(k), _operand(v)
     out = torch.empty(B, T, H, D, dtype=BF16, device=q.device)
-    stream = _lib.stream_ptr(q.device)
-    if T % 256 == 0 and D == 64 and B * H > 0 and vb.stride(0) % 8 == 0 and vb.stride(2) % 8 == 0 and \
-            vb.stride(1) % 8 == 0 and vb.data_ptr() % 16 == 0:
-        # lengths in whole 256-query tiles run the transposed-V kernel: V^T [B, H, D, T] first
-        vt = torch.empty(B, H, D, T, dtype=BF16, device=q.device)
-        _lib.call('noise_v_transpose', vb.data_ptr(), B, H, T, D, vb.stride(0), vb.stride(2), vb.stride(1),
-                  vt.data_ptr(), stream)
-        _lib.call('noise_attention_fwd', qb.data_ptr(), kb.data_ptr(), vt.data_ptr(), out.data_ptr(), B, H, T, D,
-                  qb.stride(0), qb.stride(2), qb.stride(1), kb.stride(0), kb.stride(2), kb.stride(1),
-                  vt.stride(0), vt.stride(1), vt.stride(2), _lib.ATTN_V_TRANSPOSED, out.stride(0), out.stride(2),
-                  out.stride(1), int(window), 1.0 / math.sqrt(D), None, 0, 1, None, stream)
-    else:
-        _lib.call('noise_attention_fwd', qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), out.data_ptr(), B, H, T, D,
-                  qb.stride(0), qb.stride(2), qb.stride(1), kb.stride(0), kb.stride(2), kb.stride(1),
-                  vb.stride(0), vb.stride(2), vb.stride(1), 0, out.stride(0), out.stride(2), out.stride(1),
-                  int(window), 1.0 / math.sqrt(D), None, 0, 1, None, stream)
+    # V in its own layout: lengths in whole 256-query tiles run the ring kernel, which reads V^T fragments
+    # from natural V tiles with transposing LDS reads; other lengths run the general kernel
+    _lib.call('noise_attention_fwd', qb.data_ptr(), kb.data_ptr(), vb.data_ptr(), out.data_ptr(), B, H, T, D,
+              qb.stride(0), qb.stride(2), qb.stride(1), kb.stride(0), kb.stride(2), kb.stride(1),
+              vb.stride(0), vb.stride(2), vb.stride(1), 0, out.stride(0), out.stride(2), out.stride(1),
+              int(window), 1.0 / math.sqrt(D), None, 0, 1, None, _lib.stream_ptr(q.device))
     return out if q.dtype == BF16 else out.to(q.dtype)
 
 

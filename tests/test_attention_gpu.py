@@ -119,6 +119,30 @@ def test_transposed_v_population_shape(window):
     assert (outs[0] - outs[1]).abs().max().item() <= 2e-2 * ref.abs().max().item()
 
 
+@pytest.mark.parametrize('qk_normed,window', [(False, 2048), (False, 300), (True, 1024), (True, 0)])
+def test_natural_v_ring_kernel_equals_transposed(qk_normed, window):
+    """The ring kernel on V in its natural layout (V^T fragments put together by transposing LDS reads) against
+    the same kernel on V^T: the same bf16 operands in the same products, so the outputs are bit-identical. V
+    is a [B, T, H, D] view of [B, H, T, D] storage (token stride 64, not heads * 64); 1024 tokens, 3 heads."""
+    from noise_amd.model import attention_raw
+    g = torch.Generator().manual_seed(8)
+    B, H, T = 2, 3, 1024
+    q, k = (torch.randn(B, T, H, 64, generator=g) for _ in range(2))
+    q, k = (_rms_normed(t) if qk_normed else t.bfloat16() for t in (q, k))
+    q, k = q.to(DEV), k.to(DEV)
+    vh = torch.randn(B, H, T, 64, generator=g).bfloat16().to(DEV)
+    v, vt = vh.transpose(1, 2), vh.transpose(2, 3).contiguous()
+    outs = []
+    for layout, vv in (('natural', v), ('transposed', vt)):
+        out = torch.full((B, T, H, 64), float('nan'), dtype=torch.bfloat16, device=DEV)
+        attention_raw(q, k, vv, out, window, v_transposed=layout == 'transposed', qk_normed=qk_normed)
+        outs.append(out)
+    assert torch.equal(outs[0], outs[1]), 'natural-V and V^T ring kernels differ'
+    rel_ok(outs[0], fp32_reference_gpu(q, k, v, window))
+    if window == 0:
+        assert torch.equal(outs[0], v), 'window 0: each query returns its own value row'
+
+
 def test_transposed_v_normed_promise_broken_stays_finite():
     """q, k of RMS 2.5 (scores up to ~6x the normed bound) under the fixed shift: still finite and right."""
     from noise_amd.model import attention_raw
@@ -160,8 +184,8 @@ def test_invalid_head_dim_raises():
 
 
 def test_v_transpose_layout_exact():
-    """noise_v_transpose: V [B, T, H, D] (a strided view) -> [B, H, D, T], bit for bit; the drop-in's
-    transposed-V route (T a multiple of 256) equals the general kernel's result within bf16 rounding."""
+    """noise_v_transpose: V [B, T, H, D] (a strided view) -> [B, H, D, T], bit for bit; the drop-in on the
+    same strided V (T a multiple of 256: the ring kernel on natural V) against the fp32 reference."""
     from noise_amd import _lib
     from noise_amd.model import attention
     g = torch.Generator().manual_seed(3)
