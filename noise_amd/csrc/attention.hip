@@ -611,7 +611,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 
 
 
-
 // V [b, t, h, d] (d contiguous) -> V^T [b][h][d][t]: one workgroup per (b*h, 64-token tile); each thread
 // reads two 16 B pieces of token rows and writes two 16 B pieces of dim rows through a padded LDS tile.
 __global__ __launch_bounds__(256) void v_transpose_kernel(const __bf16 *v, int64_t vs_b, int64_t vs_h, int64_t vs_t,
