@@ -477,7 +477,9 @@ typedef struct {
     int64_t rows, cols;
 } noise_update_param_t;
 
-/* Bytes of workspace noise_update_gradients needs for these parameters at this chunk of directions. */
+/* Bytes of workspace noise_update_gradients needs for these parameters at this chunk of directions: the split-bf16
+ * tables, then room for the GEMM's partial tiles on a 256-CU device (a workspace that holds only the tables is
+ * accepted: the GEMM then runs whole tiles only, with the same results up to summation order). */
 int64_t noise_update_workspace_bytes(const noise_update_param_t *params, int nparams, int64_t pairs,
                                      int64_t chunk);
 

@@ -12,11 +12,12 @@
 // A 2-D parameter's gradient G = scale * sum_d w_d a_d b_d^T is a GEMM [rows x pairs] x [pairs x cols]. The
 // reference runs it in fp32 (TF32 under set_float32_matmul_precision('high'), run.py:676 / eggroll.py main);
 // gfx950 has no xf32 MFMA, so each chunk of directions is regenerated into a bf16 table holding the hi and lo
-// halves of every value (v = hi + lo to 2^-16), laid out so that one bf16 product over K = 3 np sums
-// hi_a hi_b + hi_a lo_b + lo_a hi_b (split-bf16x3, fp32 accumulation): per row of a (weights folded in)
-// [hi | hi | lo], per row of b [hi | lo | hi]. The GEMM is the shared Mma K loop; chunks accumulate into G
-// in order (deterministic). Parameters whose sides are not multiples of 256 (ve_gate [8, 32], the 1-D
-// mixing scalars) are small: one workgroup per gradient entry sums over all directions.
+// halves of every value (v = hi + lo to 2^-16; the weights folded into a's rows), in blocks of 32 directions
+// per 128 B line: [hi x 32 | lo x 32]. The GEMM reads a line of every row per stage and issues the three bf16
+// products hi_a hi_b, hi_a lo_b, lo_a hi_b of each 16 directions from one read of each fragment
+// (split-bf16x3, fp32 accumulation). Chunks accumulate into G in order (deterministic). Parameters whose
+// sides are not multiples of 256 (ve_gate [8, 32], the 1-D mixing scalars) are small: one workgroup per
+// gradient entry sums over all directions.
 #include "common.hpp"
 #include "philox.hpp"
 #include "tile.hpp"
@@ -31,7 +32,7 @@ constexpr int kTile = 256;
 struct UpdateSet {
     int n;
     const int64_t *offsets[kMaxParams];
-    __bf16 *table[kMaxParams];        // [rows + cols][3 np]: a rows, then b rows
+    __bf16 *table[kMaxParams];        // [rows + cols][2 np]: a rows, then b rows, [hi 32 | lo 32] blocks
     float *grad[kMaxParams];          // [rows][cols]
     int rows[kMaxParams], cols[kMaxParams];
     int row_start[kMaxParams + 1];    // prefix sums of rows + cols
@@ -84,6 +85,9 @@ __global__ __launch_bounds__(1024) void update_weights_kernel(const float *__res
     }
 }
 
+// position of direction k's hi half in a table row ([hi x 32 | lo x 32] per 32 directions; lo 32 after it)
+__device__ __forceinline__ int64_t tab_pos(int64_t k) { return (k >> 5) * 64 + (k & 31); }
+
 // One table row per workgroup, 256 directions per thread block column: row r of parameter p holds, for
 // direction d0 + k, the element off_d + r of the draw (a for r < rows, scaled by weight * scale; b after).
 // Directions k >= n (padding up to np) are zero.
@@ -95,7 +99,7 @@ __global__ __launch_bounds__(256) void update_tables_kernel(UpdateSet s, int64_t
     while (p + 1 < s.n && s.row_start[p + 1] <= r) ++p;
     const int rl = r - s.row_start[p];
     const bool is_a = rl < s.rows[p];
-    __bf16 *row = s.table[p] + (int64_t)rl * 3 * np;
+    __bf16 *row = s.table[p] + (int64_t)rl * 2 * np;
     const int64_t k = (int64_t)blockIdx.y * 256 + threadIdx.x;
     float v = 0.0f;
     if (k < n) {
@@ -104,17 +108,16 @@ __global__ __launch_bounds__(256) void update_tables_kernel(UpdateSet s, int64_t
         if (is_a) v *= weight[d] * scale;
     }
     const __bf16 hi = (__bf16)v;
-    const __bf16 lo = (__bf16)(v - (float)hi);
-    row[k] = hi;
-    row[np + k] = is_a ? hi : lo;
-    row[2 * np + k] = is_a ? lo : hi;
+    row[tab_pos(k)] = hi;
+    row[tab_pos(k) + 32] = (__bf16)(v - (float)hi);
 }
 
 // As update_tables_kernel, reading the draw from a materialised buffer (fp32 [numel]) instead of the Philox
-// counter: a workgroup reads 64 directions x 256 consecutive elements (1 KiB per direction, coalesced) into
-// LDS, then writes the 256 table rows' 64 columns of each third (8 lanes x 16 B per row: whole 128 B lines).
-// grid = (rows_total / 256, np / 64).
-constexpr int kTabK = 64, kTabPad = 257;
+// counter: a workgroup reads 32 directions x 256 consecutive elements (1 KiB per direction, coalesced) into
+// LDS, all 32 loads of a thread in flight together, then writes the 256 table rows' block of 32 directions
+// (4 lanes x 2 x 16 B per row: one whole 128 B line). The 33 KB tile lets four workgroups share a CU, which
+// keeps enough bytes in flight for the HBM's latency. grid = (rows_total / 256, np / 32).
+constexpr int kTabK = 32, kTabPad = 257;
 __global__ __launch_bounds__(256) void update_tables_from_buffer_kernel(UpdateSet s, int64_t d0, int64_t n,
                                                                         int64_t np, const float *__restrict__ weight,
                                                                         float scale, const float *__restrict__ buf,
@@ -127,27 +130,27 @@ __global__ __launch_bounds__(256) void update_tables_from_buffer_kernel(UpdateSe
     const int64_t k0 = (int64_t)blockIdx.y * kTabK;
     const int kv = n - k0 < kTabK ? (int)(n - k0) : kTabK;  // valid directions of this block (>= 1)
     const int64_t *off = s.offsets[p] + d0 + k0;
-    // 16 loads in flight per thread: addresses clamped into the buffer, out-of-range elements set after
-    for (int kb = 0; kb < kTabK; kb += 16) {
-        float v[16];
-        bool ok[16];
+    // the tile's loads in flight together: addresses clamped into the buffer, out-of-range elements set after
+    for (int kb = 0; kb < kTabK; kb += 32) {
+        float v[32];
+        bool ok[32];
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
+        for (int e = 0; e < 32; ++e) {
             const int64_t L = (kb + e < kv ? off[kb + e] : 0) + rl0 + tid;
             ok[e] = L >= 0 && L < numel;
             v[e] = buf[L < 0 ? 0 : (L < numel ? L : numel - 1)];
         }
 #pragma unroll
-        for (int e = 0; e < 16; ++e)
+        for (int e = 0; e < 32; ++e)
             sm[(kb + e) * kTabPad + tid] = kb + e < kv ? (ok[e] ? v[e] : __builtin_nanf("")) : 0.0f;
     }
     __syncthreads();
-    const int c = tid & 7;  // columns 8c .. 8c + 7 of the block's 64
+    const int c = tid & 3;  // directions 8c .. 8c + 7 of the block's 32
     float wk[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) wk[e] = k0 + 8 * c + e < n ? weight[d0 + k0 + 8 * c + e] * scale : 0.0f;
-    for (int pass = 0; pass < 8; ++pass) {
-        const int rr = pass * 32 + (tid >> 3), rl = rl0 + rr;
+    for (int pass = 0; pass < 4; ++pass) {
+        const int rr = pass * 64 + (tid >> 2), rl = rl0 + rr;
         const bool is_a = rl < s.rows[p];
         bf16x8 hi, lo;
 #pragma unroll
@@ -157,31 +160,127 @@ __global__ __launch_bounds__(256) void update_tables_from_buffer_kernel(UpdateSe
             hi[e] = (__bf16)v;
             lo[e] = (__bf16)(v - (float)hi[e]);
         }
-        __bf16 *row = s.table[p] + (int64_t)rl * 3 * np + k0 + 8 * c;
+        __bf16 *row = s.table[p] + (int64_t)rl * 2 * np + tab_pos(k0 + 8 * c);
         *reinterpret_cast<bf16x8 *>(row) = hi;
-        *reinterpret_cast<bf16x8 *>(row + np) = is_a ? hi : lo;
-        *reinterpret_cast<bf16x8 *>(row + 2 * np) = is_a ? lo : hi;
+        *reinterpret_cast<bf16x8 *>(row + 32) = lo;
     }
 }
 
-// G[o][i] (+)= sum_k table_a[o][k] table_b[i][k]: one 256 x 256 tile of one parameter per workgroup.
-__global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int K, int accumulate) {
-    using M = Mma<8, kTile, kTile, 64, 2>;
-    __shared__ __attribute__((aligned(16))) __bf16 lds[M::LDS_BYTES / 2];
-    const int wg = blockIdx.x;
+// G[o][i] (+)= sum_d A[o][d] B[i][d] over the chunk's np directions, A = hi_a + lo_a and B = hi_b + lo_b read
+// from the tables, as hi_a hi_b + hi_a lo_b + lo_a hi_b: one 256 x 256 tile of one parameter per workgroup.
+// 8 waves of 128 (A rows) x 64 (B rows), four 32 x 32 accumulator blocks by two. Workgroups past the first
+// `full` take part q of `split` equal ranges of the chunk's directions for tile full + (wg - full) / split
+// and write that partial tile to part (summed in order by update_reduce_kernel): the last, partial round of
+// workgroups then runs `split` times shorter. Per stage, 32 directions:
+// one 128 B line of each of the tile's 512 rows ([hi | lo] of 32 directions) copied global -> LDS directly,
+// chunks XOR-swizzled by row pair; two stages in flight. Per 16 directions a wave reads its hi and lo
+// fragments once (12 reads) for 24 products.
+constexpr int kUgStage = 512 * 128;  // bytes per stage: 256 A rows, then 256 B rows
+__global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, int accumulate, int full, int split,
+                                                          float *__restrict__ part) {
+    __shared__ __attribute__((aligned(16))) char lds[2 * kUgStage];
+    // workgroups are dispatched round-robin over the 8 XCDs: each XCD takes a contiguous range of the full
+    // tiles (and of the partial items), so the tiles that share a table panel run under one L2
+    int wg = blockIdx.x;
+    if (wg < full) {
+        if ((full & 7) == 0) wg = (wg & 7) * (full >> 3) + (wg >> 3);
+    } else {
+        const int items = (int)gridDim.x - full, i = wg - full;
+        if ((items & 7) == 0) wg = full + (i & 7) * (items >> 3) + (i >> 3);
+    }
+    const bool partial = wg >= full;
+    const int item = wg - full;  // partial workgroups: item = split * (tile - full) + q
+    const int tile = partial ? full + item / split : wg;
     int p = 0;
-    while (p + 1 < s.n && s.tile_start[p + 1] <= wg) ++p;
-    const int t = wg - s.tile_start[p];
+    while (p + 1 < s.n && s.tile_start[p + 1] <= tile) ++p;
+    const int t = tile - s.tile_start[p];
     const int rows = s.rows[p], cols = s.cols[p];
     const int ot = t / (cols / kTile), ct = t % (cols / kTile);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, j = lane & 31, hf = lane >> 5;
-    const int wn0 = M::wn0(wave), wm0 = M::wm0(wave);
-    const __bf16 *tab = s.table[p];
+    const int tid = threadIdx.x, lane = tid & 63, j = lane & 31, hf = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wn0 = 128 * (wave & 1), wm0 = 64 * (wave >> 1);
+    const int64_t ld = 2 * (int64_t)np;  // table row length (elements)
+    const __bf16 *A = s.table[p] + (int64_t)ot * kTile * ld, *B = s.table[p] + (int64_t)(rows + ct * kTile) * ld;
+    const unsigned lbase = lds_addr(lds);
+    // copy i (0 .. 7) of a stage: tile rows 64 i + 8 wave .. + 8 (A for i < 4, B after); lane: row lane / 8 of
+    // the copy, LDS slot lane % 8 holds the line's chunk (lane % 8) ^ ((row >> 1) & 7), the same for every copy
+    const int rl = 8 * wave + (lane >> 3);
+    const int cl = (lane & 7) ^ ((rl >> 1) & 7);
+    const unsigned off = (unsigned)(rl * ld * 2 + cl * 16);
+    // stages k0 .. k0 + nk - 1 of the chunk's np / 32 (np is a multiple of 256: np / 32 divides by split)
+    const int nk = partial ? np / 32 / split : np / 32;
+    const int k0 = partial ? (item % split) * nk : 0;
+    auto issue = [&](int ks) {  // stage k0 + ks into buffer ks % 2
+        const unsigned st = lbase + (ks & 1) * kUgStage + wave * 1024;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const __bf16 *src = (i < 4 ? A + (int64_t)(64 * i) * ld : B + (int64_t)(64 * (i - 4)) * ld) + 64 * (k0 + ks);
+            lds_dma16_at(src, off, st + i * 8192);
+        }
+    };
+    // fragment rows wn0 + 32 fb + j (A) and 256 + wm0 + 32 tb + j (B) share the swizzle of row j; chunk
+    // 2 s + hf is the hi half of directions 16 s + 8 hf .. + 8, chunk 4 + 2 s + hf its lo half
+    int fo[2][2];
+#pragma unroll
+    for (int sk = 0; sk < 2; ++sk)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) fo[sk][h] = j * 128 + (((4 * h + 2 * sk + hf) ^ ((j >> 1) & 7)) << 4);
     f32x16 acc[4][2];
-    M::run(tab + (int64_t)ot * kTile * K, K, tab + (int64_t)(rows + ct * kTile) * K, K, K, lds, acc, tid, wn0, wm0);
+#pragma unroll
+    for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) acc[fb][tb] = f32x16{};
+    // fragments of 16 directions, double buffered: those of the next step are read while this step's run
+    bf16x8 ah[2][4], al[2][4], bh[2][2], bl[2][2];
+    auto fetch = [&](int buf, const char *st, int sk) {
+#pragma unroll
+        for (int fb = 0; fb < 4; ++fb) {
+            ah[buf][fb] = *reinterpret_cast<const bf16x8 *>(st + (wn0 + 32 * fb) * 128 + fo[sk][0]);
+            al[buf][fb] = *reinterpret_cast<const bf16x8 *>(st + (wn0 + 32 * fb) * 128 + fo[sk][1]);
+        }
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb) {
+            bh[buf][tb] = *reinterpret_cast<const bf16x8 *>(st + (256 + wm0 + 32 * tb) * 128 + fo[sk][0]);
+            bl[buf][tb] = *reinterpret_cast<const bf16x8 *>(st + (256 + wm0 + 32 * tb) * 128 + fo[sk][1]);
+        }
+    };
+    // the three products as three passes over the 8 accumulators: dependent products 8 apart
+    auto products = [&](int buf) {
+#pragma unroll
+        for (int pr = 0; pr < 3; ++pr)
+#pragma unroll
+            for (int fb = 0; fb < 4; ++fb)
+#pragma unroll
+                for (int tb = 0; tb < 2; ++tb)
+                    acc[fb][tb] = mfma32x32x16(pr == 2 ? al[buf][fb] : ah[buf][fb], pr == 1 ? bl[buf][tb] : bh[buf][tb],
+                                               acc[fb][tb]);
+    };
+    issue(0);
+    if (nk > 1) issue(1);
+    vm_wait_groups<8, 1>(nk > 1 ? 1 : 0);
+    __syncthreads();
+    fetch(0, lds, 0);
+#pragma unroll 1
+    for (int ks = 0; ks < nk; ++ks) {
+        const char *st = lds + (ks & 1) * kUgStage;
+        fetch(1, st, 1);
+        products(0);
+        if (ks + 1 < nk) {
+            // stage ks + 1 landed for every wave (nothing was issued after it); every wave has read its
+            // fragments of stage ks, whose buffer takes stage ks + 2
+            vm_wait<0>();
+            __syncthreads();
+            if (ks + 2 < nk) issue(ks + 2);
+            fetch(0, lds + ((ks + 1) & 1) * kUgStage, 0);
+        }
+        products(1);
+    }
     // lane (j, hf), register 4 g + e of block (fb, tb): row o = wn0 + 32 fb + 8 g + 4 hf + e, column
-    // i = wm0 + 32 tb + j; the 32 lanes of a half-wave write 128 contiguous bytes of one row
-    float *g = s.grad[p] + (int64_t)ot * kTile * cols + ct * kTile;
+    // i = wm0 + 32 tb + j; the 32 lanes of a half-wave write 128 contiguous bytes of one row (a partial tile:
+    // [256][256] of its own)
+    float *g = partial ? part + (int64_t)item * kTile * kTile : s.grad[p] + (int64_t)ot * kTile * cols + ct * kTile;
+    const int64_t ldg = partial ? kTile : cols;
+    const bool add = accumulate && !partial;
 #pragma unroll
     for (int fb = 0; fb < 4; ++fb)
 #pragma unroll
@@ -189,10 +288,33 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int K, in
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int o = wn0 + 32 * fb + 8 * (q >> 2) + 4 * hf + (q & 3);
-                float *dst = g + (int64_t)o * cols + wm0 + 32 * tb + j;
+                float *dst = g + (int64_t)o * ldg + wm0 + 32 * tb + j;
                 const float v = acc[fb][tb][q];
-                *dst = accumulate ? *dst + v : v;
+                *dst = add ? *dst + v : v;
             }
+}
+
+// The partial tiles of update_gemm_kernel summed in order (part 0 first) into G (+=): 1024 entries per
+// workgroup, 64 workgroups per tile. grid = (tiles - full) * 64.
+__global__ __launch_bounds__(256) void update_reduce_kernel(UpdateSet s, int full, int split,
+                                                            const float *__restrict__ part, int accumulate) {
+    const int tile = full + blockIdx.x / 64, e = (blockIdx.x % 64) * 1024 + 4 * threadIdx.x;
+    int p = 0;
+    while (p + 1 < s.n && s.tile_start[p + 1] <= tile) ++p;
+    const int t = tile - s.tile_start[p], cols = s.cols[p];
+    const int ot = t / (cols / kTile), ct = t % (cols / kTile);
+    const float *src = part + (int64_t)(tile - full) * split * kTile * kTile + e;
+    float4 v = ld4(src);
+    for (int q = 1; q < split; ++q) {
+        const float4 w = ld4(src + (int64_t)q * kTile * kTile);
+        v.x += w.x; v.y += w.y; v.z += w.z; v.w += w.w;
+    }
+    float *dst = s.grad[p] + (int64_t)(ot * kTile + e / kTile) * cols + ct * kTile + e % kTile;
+    if (accumulate) {
+        const float4 g = ld4(dst);
+        v.x += g.x; v.y += g.y; v.z += g.z; v.w += g.w;
+    }
+    st4(dst, v);
 }
 
 // One gradient entry per workgroup: scale * sum_d weight[d] a_d[o] (b_d[i] or 1), 256 threads striding
@@ -231,6 +353,32 @@ int64_t padded_chunk(int64_t chunk, int64_t pairs) {
     return (c + 255) / 256 * 256;
 }
 
+// The GEMM's last, partial round of workgroups (one per CU) over `cus` compute units: tiles full .. tiles - 1
+// run as `split` shorter partial workgroups each, so that round fills the device; split 1: no partials.
+void gemm_split(int64_t tiles, int64_t cus, int64_t &full, int &split) {
+    const int64_t r = cus > 0 ? tiles % cus : 0;
+    const int64_t sp = r ? cus / r : 1;
+    split = sp >= 4 ? 4 : sp >= 2 ? 2 : 1;
+    full = split > 1 ? tiles - r : tiles;
+}
+
+int64_t partial_bytes(int64_t tiles, int64_t full, int split) {
+    return split > 1 ? (tiles - full) * split * kTile * kTile * (int64_t)sizeof(float) : 0;
+}
+
+// compute units of the current device (gfx950 parts have 256), cached per device
+int64_t device_cus() {
+    static int cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cached[dev]) {
+        int n = 0;
+        cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
+                          ? n : 256;
+    }
+    return cached[dev];
+}
+
 }  // namespace
 }  // namespace noise
 
@@ -253,10 +401,17 @@ extern "C" int64_t noise_update_workspace_bytes(const noise_update_param_t *para
                                                 int64_t chunk) {
     if (params == nullptr || nparams < 0 || pairs < 1 || chunk < 1) return -1;
     const int64_t np = padded_chunk(chunk, pairs);
-    int64_t bytes = 0;
+    int64_t bytes = 0, tiles = 0;
     for (int i = 0; i < nparams; ++i)
-        if (is_big(params[i])) bytes += (params[i].rows + params[i].cols) * 3 * np * 2;
-    return bytes;
+        if (is_big(params[i])) {
+            bytes += (params[i].rows + params[i].cols) * 2 * np * 2;
+            tiles += (params[i].rows / kTile) * (params[i].cols / kTile);
+        }
+    // the tables, then the GEMM's partial tiles for a device of 256 compute units
+    int64_t full;
+    int split;
+    gemm_split(tiles, 256, full, split);
+    return bytes + partial_bytes(tiles, full, split);
 }
 
 extern "C" int noise_update_gradients(const noise_update_param_t *params, int nparams, int64_t pairs,
@@ -274,7 +429,8 @@ extern "C" int noise_update_gradients(const noise_update_param_t *params, int np
     NOISE_CHECK_ARG(numel > 0, "noise_update_gradients: numel must be positive");
     NOISE_CHECK_ARG(buffer == nullptr || aligned(buffer, 4), "noise_update_gradients: buffer must be 4-byte aligned");
     const int64_t np = padded_chunk(chunk, pairs);
-    NOISE_CHECK_ARG(3 * np < (1ll << 31) && np / 256 <= 65535, "noise_update_gradients: chunk too large");
+    // (the GEMM's 32-bit copy offsets span 64 table rows of 2 np elements)
+    NOISE_CHECK_ARG(np <= (1 << 22), "noise_update_gradients: chunk too large (at most 4194304 directions)");
     UpdateSet big{};
     UpdateSmall small{};
     int64_t rows_total = 0, tiles_total = 0, entries_total = 0, need = 0;
@@ -298,7 +454,7 @@ extern "C" int noise_update_gradients(const noise_update_param_t *params, int np
             big.table[b] = reinterpret_cast<__bf16 *>(ws + need);
             rows_total += q.rows + q.cols;
             tiles_total += (q.rows / kTile) * (q.cols / kTile);
-            need += (q.rows + q.cols) * 3 * np * 2;
+            need += (q.rows + q.cols) * 2 * np * 2;
         } else {
             const int64_t entries = q.rows * (q.cols ? q.cols : 1);
             NOISE_CHECK_ARG(entries <= 65536,
@@ -323,6 +479,15 @@ extern "C" int noise_update_gradients(const noise_update_param_t *params, int np
                     "see noise_update_workspace_bytes", (long long)need, (long long)workspace_bytes);
     DrawLayout dl{seed, offset, (uint64_t)threads};
     hipStream_t s = (hipStream_t)stream;
+    // the GEMM's partial tiles after the tables, when the workspace holds them (else whole tiles only)
+    int64_t full;
+    int split;
+    gemm_split(tiles_total, device_cus(), full, split);
+    while (split > 1 && (workspace == nullptr || workspace_bytes - need < partial_bytes(tiles_total, full, split))) {
+        split /= 2;
+        if (split == 1) full = tiles_total;
+    }
+    float *part = split > 1 ? reinterpret_cast<float *>(ws + need) : nullptr;
     if (small.n) {
         hipLaunchKernelGGL(update_small_kernel, dim3((unsigned)entries_total), dim3(256), 0, s, small, pairs, weight,
                            scale, dl, numel);
@@ -341,10 +506,17 @@ extern "C" int noise_update_gradients(const noise_update_param_t *params, int np
                                    0, s, big, d0, n, np, weight, scale, dl, numel);
             int st = launch_status("noise_update_gradients (tables)");
             if (st) return st;
-            hipLaunchKernelGGL(update_gemm_kernel, dim3((unsigned)tiles_total), dim3(512), 0, s, big, (int)(3 * np),
-                               d0 > 0 ? 1 : 0);
+            const int64_t wgs = full + (tiles_total - full) * split;
+            hipLaunchKernelGGL(update_gemm_kernel, dim3((unsigned)wgs), dim3(512), 0, s, big, (int)np, d0 > 0 ? 1 : 0,
+                               (int)full, split, part);
             st = launch_status("noise_update_gradients (gemm)");
             if (st) return st;
+            if (split > 1) {
+                hipLaunchKernelGGL(update_reduce_kernel, dim3((unsigned)((tiles_total - full) * 64)), dim3(256), 0, s,
+                                   big, (int)full, split, part, d0 > 0 ? 1 : 0);
+                st = launch_status("noise_update_gradients (partial tiles)");
+                if (st) return st;
+            }
         }
     }
     return NOISE_OK;

@@ -88,9 +88,11 @@ def _params(lib, shapes):
 
 def test_update_workspace_bytes(lib):
     arr = _params(lib, [(512, 512), (2048, 512), (8, 32), (8, 0)])
-    # big parameters only: (rows + cols) * 3 * chunk (rounded up to 256) bf16
-    assert lib.lib().noise_update_workspace_bytes(arr, 4, 1000, 300) == (1024 + 2560) * 3 * 512 * 2
-    assert lib.lib().noise_update_workspace_bytes(arr, 4, 64, 4096) == (1024 + 2560) * 3 * 256 * 2
+    # big parameters only: (rows + cols) * 2 (the hi and lo halves) * chunk (rounded up to 256) bf16, then the
+    # GEMM's partial tiles: 4 + 16 tiles of 256 x 256 fill a 256-CU device split in 4 (fp32)
+    partials = (4 + 16) * 4 * 256 * 256 * 4
+    assert lib.lib().noise_update_workspace_bytes(arr, 4, 1000, 300) == (1024 + 2560) * 2 * 512 * 2 + partials
+    assert lib.lib().noise_update_workspace_bytes(arr, 4, 64, 4096) == (1024 + 2560) * 2 * 256 * 2 + partials
     assert lib.lib().noise_update_workspace_bytes(arr, 4, 0, 256) == -1
 
 

@@ -162,3 +162,33 @@ def test_materialised_buffer_gives_the_same_gradients():
     for n in g_regen:
         print(n, float((g_regen[n] - g_buf[n]).abs().max()), flush=True)
         assert torch.equal(g_regen[n], g_buf[n]), n
+
+
+def test_workspace_without_partial_tiles_gives_the_same_gradients(monkeypatch):
+    # a workspace that holds only the tables: the GEMM then runs whole tiles over every direction instead of
+    # splitting the last round's tiles into partial tiles summed in order. The same products, summed in another
+    # order: equal to fp32 rounding of the sums, and both within the oracle's bar
+    from noise_amd import _lib
+    from noise_amd.eggroll import Eggroll
+    es = Eggroll(_Params().cuda(), 600)
+    offsets = es.offsets(7)
+    losses = _losses(1200, seed=4)
+    lib = _lib.lib()
+    full_bytes = lib.noise_update_workspace_bytes
+
+    def tables_only(table, n, pairs, chunk):
+        np_ = (min(chunk, pairs) + 255) // 256 * 256
+        big = [table[i] for i in range(n) if table[i].cols > 0 and table[i].rows % 256 == 0 and table[i].cols % 256 == 0]
+        need = sum((t.rows + t.cols) * 2 * np_ * 2 for t in big)
+        assert full_bytes(table, n, pairs, chunk) > need  # the default leaves room for partial tiles
+        return need
+
+    split = es.update(losses, offsets, chunk=256)
+    monkeypatch.setattr(lib, 'noise_update_workspace_bytes', tables_only)
+    whole = es.update(losses, offsets, chunk=256)
+    ref = _oracle(es, losses, offsets)
+    for n in es.params:
+        a, b = split[n].cpu().numpy(), whole[n].cpu().numpy()
+        print(n, _rel(a, b), flush=True)
+        assert _rel(a, b) <= 1e-6, n
+        assert _rel(b, ref[n]) <= TOL, n
