@@ -11,7 +11,8 @@
 // query and row reductions need one exchange with lane ^ 32; P is fed from registers as the B operand of
 // O^T = V^T P^T with the key index permuted identically on both sides, so P never touches LDS.
 //  - attention_fwd_kernel (any layout and length): 4 waves of 64 queries, K / V tiles register-staged
-//    into double-buffered LDS (rows padded to 144 B), running-max softmax.
+//    into double-buffered LDS (rows padded to 144 B), running-max softmax (rescaled only when the maximum
+//    grows by more than 2^8).
 //  - attention_vt_kernel (length a multiple of 256; V transposed, the population path, or natural, the
 //    drop-in's): 8 waves of 32 queries (four waves per SIMD) in two groups half a tile apart, K and V (or V^T)
 //    copied global -> LDS into a four-stage swizzled ring, and an optional fixed-shift softmax for RMS-normed
@@ -197,21 +198,28 @@ __global__ __launch_bounds__(256, 2) void attention_fwd_kernel(AttnArgs a) {
 #pragma unroll
                     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, st[kb][qb][r]);
                 mx = fmaxf(mx, swap_halves(mx));
-                const float m_new = fmaxf(m[qb], mx * a.scale_log2);
-                const float alpha = exp2_fast(m[qb] - m_new);
-                m[qb] = m_new;
+                // lazy rescale, as in the ring kernel: m moves only when a row's maximum passes it by more than
+                // 8 (log2 units); the weights then stay below 2^8 and o and l share the stale m
+                const float mc = mx * a.scale_log2;
+                if (__builtin_amdgcn_ballot_w64(mc > m[qb] + 8.0f)) {
+                    const float m_new = fmaxf(m[qb], mc);
+                    const float alpha = exp2_fast(m[qb] - m_new);
+                    m[qb] = m_new;
+                    l[qb] *= alpha;
+#pragma unroll
+                    for (int db = 0; db < 2; ++db) o[db][qb] *= alpha;
+                }
+                const float mb = m[qb];
                 float rs = 0.f;
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
                     for (int r = 0; r < 16; ++r) {
-                        float p = exp2_fast(__builtin_fmaf(st[kb][qb][r], a.scale_log2, -m_new));
+                        float p = exp2_fast(__builtin_fmaf(st[kb][qb][r], a.scale_log2, -mb));
                         st[kb][qb][r] = p;
                         rs += p;
                     }
-                l[qb] = l[qb] * alpha + rs;
-#pragma unroll
-                for (int db = 0; db < 2; ++db) o[db][qb] *= alpha;
+                l[qb] += rs;
 #pragma unroll
                 for (int s = 0; s < 4; ++s) {
                     bf16x8 v;
@@ -468,13 +476,20 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
 #pragma unroll
                     for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kb][qb][r]);
                 mx = fmaxf(mx, swap_halves(mx));
-                const float m_new = fmaxf(m[qb], mx * c2);
-                const float alpha = exp2_fast(m[qb] - m_new);
-                m[qb] = m_new;
-                l[qb] *= alpha;
+                // the reference maximum m moves only in tiles where some row's maximum passes it by more than 8
+                // (log2 units): the weights exp2(s c2 - m) then stay below 2^8, and the output and the row sum
+                // share the stale m, so the softmax is unchanged. The rescale of o and l (a wave-uniform branch)
+                // runs in the few tiles that raise m instead of in every tile
+                const float mc = mx * c2;
+                if (__builtin_amdgcn_ballot_w64(mc > m[qb] + 8.0f)) {
+                    const float m_new = fmaxf(m[qb], mc);
+                    const float alpha = exp2_fast(m[qb] - m_new);
+                    m[qb] = m_new;
+                    l[qb] *= alpha;
 #pragma unroll
-                for (int db = 0; db < 2; ++db) o[db][qb] *= alpha;
-                mb = m_new;
+                    for (int db = 0; db < 2; ++db) o[db][qb] *= alpha;
+                }
+                mb = m[qb];
             }
             float rs = 0.f;
 #pragma unroll
