@@ -18,6 +18,8 @@
 // (split-bf16x3, fp32 accumulation). Chunks accumulate into G in order (deterministic). Parameters whose
 // sides are not multiples of 256 (ve_gate [8, 32], the 1-D mixing scalars) are small: one workgroup per
 // gradient entry sums over all directions.
+#include <atomic>
+
 #include "common.hpp"
 #include "philox.hpp"
 #include "tile.hpp"
@@ -366,17 +368,18 @@ int64_t partial_bytes(int64_t tiles, int64_t full, int split) {
     return split > 1 ? (tiles - full) * split * kTile * kTile * (int64_t)sizeof(float) : 0;
 }
 
-// compute units of the current device (gfx950 parts have 256), cached per device
+// compute units of the current device (gfx950 parts have 256), cached per device (any host thread may ask)
 int64_t device_cus() {
-    static int cached[64];
+    static std::atomic<int> cached[64];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-    if (!cached[dev]) {
+    int c = cached[dev].load(std::memory_order_relaxed);
+    if (!c) {
         int n = 0;
-        cached[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0
-                          ? n : 256;
+        c = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+        cached[dev].store(c, std::memory_order_relaxed);
     }
-    return cached[dev];
+    return c;
 }
 
 }  // namespace
