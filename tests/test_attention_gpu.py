@@ -201,3 +201,24 @@ def test_v_transpose_layout_exact():
     fast = attention(q, k, v, 200)
     ref = fp32_reference_gpu(q, k, v, 200)
     rel_ok(fast, ref)
+
+
+@pytest.mark.parametrize('T', [1024, 600])
+def test_running_max_rescales_as_scores_grow(T):
+    """Scores that grow along the keys (k rows scaled by 1 .. 150 with the key position, q along the same
+    direction): a query's maximum climbs to ~80 in log2 units, passing the stale reference maximum by more than 8
+    again and again, so the lazy rescale runs in many tiles, of the ring kernel (T = 1024) and of the general
+    kernel (T = 600). Against the fp32 reference."""
+    from noise_amd.model import attention
+    g = torch.Generator().manual_seed(9)
+    B, H = 2, 3
+    u = torch.randn(64, generator=g)
+    u = u / u.norm()
+    ramp = torch.linspace(1.0, 150.0, T).view(1, T, 1, 1)
+    q = (3.0 * u + 0.3 * torch.randn(B, T, H, 64, generator=g)).bfloat16()
+    k = (ramp * (u + 0.3 * torch.randn(B, T, H, 64, generator=g))).bfloat16()
+    v = torch.randn(B, T, H, 64, generator=g).bfloat16()
+    q, k, v = q.to(DEV), k.to(DEV), v.to(DEV)
+    out = attention(q, k, v, T)
+    assert torch.isfinite(out.float()).all()
+    rel_ok(out, fp32_reference_gpu(q, k, v, T))
