@@ -419,7 +419,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     auto active = [&](int t) { return tile_k0(t) <= wq_hi && tile_k0(t) + kBKV - 1 >= wq_lo - W; };
     // S = K Q^T of tile t (slot t % NS); BOUNDED: K (c2 Q)^T - shift, the exponents
     auto qk = [&](int t) {
-        const char *st = lds + (t % NS) * kStage;
+        const char *st = lds + (t & (NS - 1)) * kStage;
         f32x16 init = f32x16{};
         if constexpr (BOUNDED) {
 #pragma unroll
@@ -519,7 +519,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
     };
     // O += V^T P^T of tile t
     auto pv = [&](int t) {
-        const char *st = lds + (t % NS) * kStage;
+        const char *st = lds + (t & (NS - 1)) * kStage;
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
 #pragma unroll
@@ -546,31 +546,45 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) voi
         vm_wait_groups<CPW, 2>(nt - 1 < 2 ? nt - 1 : 2);
     }
     __syncthreads();  // barrier 0: tile 0 landed
+    // the tile loops step by the ring's depth (NS = 4), so that each unrolled tile's slot t & 3 is a constant
+    // (the compiler does not unroll loops with barriers at run-time trip counts); the guards are uniform
     if (group_a) {
 #pragma unroll 1
-        for (int t = 0; t < nt; ++t) {
-            if (active(t)) {
-                qk(t);
-                softmax(t);
-                pv(t);
-            }
-            if (t + 1 < nt) {
-                // tile t + 1 landed: tiles after it issued so far: min(t + 2, nt - 1) - (t + 1)
-                vm_wait_groups<CPW, 1>(nt - 2 - t < 1 ? nt - 2 - t : 1);
-                __syncthreads();  // barrier t + 1
-                if (t + 3 < nt) issue(tile_k0(t + 3), lb + ((t + 3) % NS) * kStage);
+        for (int t0 = 0; t0 < nt; t0 += NS) {
+#pragma unroll
+            for (int u = 0; u < NS; ++u) {
+                const int t = t0 + u;
+                if (t < nt) {
+                    if (active(t)) {
+                        qk(t);
+                        softmax(t);
+                        pv(t);
+                    }
+                    if (t + 1 < nt) {
+                        // tile t + 1 landed: tiles after it issued so far: min(t + 2, nt - 1) - (t + 1)
+                        vm_wait_groups<CPW, 1>(nt - 2 - t < 1 ? nt - 2 - t : 1);
+                        __syncthreads();  // barrier t + 1
+                        if (t + 3 < nt) issue(tile_k0(t + 3), lb + ((t + 3) & (NS - 1)) * kStage);
+                    }
+                }
             }
         }
     } else {
         if (active(0)) qk(0);
 #pragma unroll 1
-        for (int t = 1; t < nt; ++t) {
-            __syncthreads();  // barrier t: tile t landed
-            if (active(t - 1)) {
-                softmax(t - 1);
-                pv(t - 1);
+        for (int t0 = 0; t0 < nt; t0 += NS) {
+#pragma unroll
+            for (int u = 0; u < NS; ++u) {
+                const int t = t0 + u;
+                if (t >= 1 && t < nt) {
+                    __syncthreads();  // barrier t: tile t landed
+                    if (active(t - 1)) {
+                        softmax(t - 1);
+                        pv(t - 1);
+                    }
+                    if (active(t)) qk(t);
+                }
             }
-            if (active(t)) qk(t);
         }
         if (active(nt - 1)) {
             softmax(nt - 1);
