@@ -167,6 +167,16 @@ def test_fp32_head_split_bf16x3(params):
     assert err <= 1e-4
 
 
+def test_fp32_head_population_at_the_bar(params):
+    """The fp32 head in the population path at the scale the other composites use (x30, sigma 0.02, two seeds):
+    every member within the 1e-3 bar of the fp32 oracle."""
+    P = scaled_head(params, 30.0)
+    for seed in (6, 7):
+        got, ref = run_both(P, BLOCK_MATRICES, 4, 512, 0.02, seed=seed, fp32_head=True)
+        check(got, ref)
+        assert (ref[1::2] - ref[0::2]).abs().max() > 5 * TOL, 'perturbations must be visible'
+
+
 def test_repeatable(params):
     from noise_amd.eggroll import Weights, population_forward
     P = scaled_head(params, 30.0)
