@@ -78,6 +78,21 @@ __device__ __forceinline__ void lds_dma16(const void *base, unsigned off, const 
     lds_dma16_at(base, off, lds_addr(l));
 }
 
+// As lds_dma16_at with 4 B per lane: lane l's dword lands at LDS byte la + 4 l (256 B per wave-wide copy); the
+// global address needs only 4 B alignment.
+__device__ __forceinline__ void lds_dma4_at(const void *base, unsigned off, unsigned la) {
+    const uint64_t b = (uint64_t)base;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32));
+    const uint64_t ub = ((uint64_t)hi << 32) | (uint64_t)lo;
+    const unsigned l = (unsigned)__builtin_amdgcn_readfirstlane((int)la);
+    unsigned save;
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %3\n\tglobal_load_lds_dword %1, %2\n\ts_mov_b32 m0, %0"
+                 : "=&s"(save)
+                 : "v"(off), "s"(ub), "s"(l)
+                 : "memory");
+}
+
 // s_waitcnt vmcnt(N) (expcnt and lgkmcnt left alone)
 template <int N>
 __device__ __forceinline__ void vm_wait() {

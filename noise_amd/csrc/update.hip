@@ -109,9 +109,13 @@ __global__ __launch_bounds__(256) void update_tables_kernel(UpdateSet s, int64_t
         v = noise_at(dl, s.offsets[p][d] + rl, numel);
         if (is_a) v *= weight[d] * scale;
     }
-    const __bf16 hi = (__bf16)v;
-    row[tab_pos(k)] = hi;
-    row[tab_pos(k) + 32] = (__bf16)(v - (float)hi);
+    {
+        // v rounded to fp32 first, then lo = v - hi exactly (no fused multiply-subtract)
+#pragma clang fp contract(off)
+        const __bf16 hi = (__bf16)v;
+        row[tab_pos(k)] = hi;
+        row[tab_pos(k) + 32] = (__bf16)(v - (float)hi);
+    }
 }
 
 // As update_tables_kernel, reading the draw from a materialised buffer (fp32 [numel]) instead of the Philox
@@ -157,6 +161,8 @@ __global__ __launch_bounds__(256) void update_tables_from_buffer_kernel(UpdateSe
         bf16x8 hi, lo;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
+            // v rounded to fp32 first, then lo = v - hi exactly (no fused multiply-subtract)
+#pragma clang fp contract(off)
             float v = sm[(8 * c + e) * kTabPad + rr];
             if (is_a) v *= wk[e];
             hi[e] = (__bf16)v;
@@ -168,19 +174,41 @@ __global__ __launch_bounds__(256) void update_tables_from_buffer_kernel(UpdateSe
     }
 }
 
-// G[o][i] (+)= sum_d A[o][d] B[i][d] over the chunk's np directions, A = hi_a + lo_a and B = hi_b + lo_b read
-// from the tables, as hi_a hi_b + hi_a lo_b + lo_a hi_b: one 256 x 256 tile of one parameter per workgroup.
-// 8 waves of 128 (A rows) x 64 (B rows), four 32 x 32 accumulator blocks by two. Workgroups past the first
-// `full` take part q of `split` equal ranges of the chunk's directions for tile full + (wg - full) / split
-// and write that partial tile to part (summed in order by update_reduce_kernel): the last, partial round of
-// workgroups then runs `split` times shorter. Per stage, 32 directions:
-// one 128 B line of each of the tile's 512 rows ([hi | lo] of 32 directions) copied global -> LDS directly,
-// chunks XOR-swizzled by row pair; two stages in flight. Per 16 directions a wave reads its hi and lo
-// fragments once (12 reads) for 24 products.
-constexpr int kUgStage = 512 * 128;  // bytes per stage: 256 A rows, then 256 B rows
+// G[o][i] (+)= sum_d A[o][d] B[i][d] over the chunk's np directions, A = hi_a + lo_a and B = hi_b + lo_b, as
+// hi_a hi_b + hi_a lo_b + lo_a hi_b: one 256 x 256 tile of one parameter per workgroup. 8 waves of 128 (A rows)
+// x 64 (B rows), four 32 x 32 accumulator blocks by two. Workgroups past the first `full` take part q of `split`
+// equal ranges of the chunk's directions for tile full + (wg - full) / split and write that partial tile to part
+// (summed in order by update_reduce_kernel): the last, partial round of workgroups then runs `split` times
+// shorter. Per stage, 32 directions of the tile's 512 rows (64 KiB), two stages in flight; per 16 directions a
+// wave reads its hi and lo fragments once for 24 products.
+//
+// Tables (RAW false): a stage is one 128 B line of each row ([hi | lo] of 32 directions) copied global -> LDS,
+// chunks XOR-swizzled by row pair, read as 16 B fragments.
+//
+// Buffer (RAW true): no tables. A stage is the 32 directions' fp32 slices themselves, [direction][A rows | B
+// rows] at a stride of 2176 B (2 KiB + 128), copied straight from the buffer (16 B per lane; slices start at any
+// element). Each wave copies 4 directions and, once its copies have landed, splits them in place: the 32 B
+// holding rows 8 c .. 8 c + 7 of a direction become [hi x 8 | lo x 8] (lo first where bit 1 of the direction is
+// set), so nothing crosses lanes or waves before the stage's barrier. Fragments are then read with gfx950's
+// transposing LDS read (ds_read_b64_tr_b16: in each 16 lanes, lane i takes element i % 4 of the 8 B that lane
+// i / 4 + 4 e addresses), which gathers a row's 4 consecutive directions from 4 direction rows. The odd stride
+// (128 B apart mod 256) and the hi / lo swap put a read's 4 directions on 4 disjoint sets of banks. The values,
+// hence the products and G, are those of the tables.
+struct UpdateRaw {
+    int64_t d0, n;             // the chunk's first direction and its valid directions (the rest up to np is zero)
+    const float *weight;
+    float scale;
+    const float *buf;          // fp32 [numel], numel <= 2^30 (lane offsets are 32-bit byte offsets)
+    int64_t numel;
+};
+constexpr int kUgStage = 512 * 128;  // tables: bytes per stage, 256 A rows, then 256 B rows
+constexpr int kUgDir = 2176;         // buffer: bytes per direction of a stage (2 KiB of rows, 128 B apart)
+constexpr int kUgRawStage = 32 * kUgDir;
+template <bool RAW>
 __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, int accumulate, int full, int split,
-                                                          float *__restrict__ part) {
-    __shared__ __attribute__((aligned(16))) char lds[2 * kUgStage];
+                                                          float *__restrict__ part, UpdateRaw raw) {
+    constexpr int kSt = RAW ? kUgRawStage : kUgStage;
+    __shared__ __attribute__((aligned(16))) char lds[2 * kSt];
     // workgroups are dispatched round-robin over the 8 XCDs: each XCD takes a contiguous range of the full
     // tiles (and of the partial items), so the tiles that share a table panel run under one L2
     int wg = blockIdx.x;
@@ -204,14 +232,15 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
     const int64_t ld = 2 * (int64_t)np;  // table row length (elements)
     const __bf16 *A = s.table[p] + (int64_t)ot * kTile * ld, *B = s.table[p] + (int64_t)(rows + ct * kTile) * ld;
     const unsigned lbase = lds_addr(lds);
-    // copy i (0 .. 7) of a stage: tile rows 64 i + 8 wave .. + 8 (A for i < 4, B after); lane: row lane / 8 of
-    // the copy, LDS slot lane % 8 holds the line's chunk (lane % 8) ^ ((row >> 1) & 7), the same for every copy
-    const int rl = 8 * wave + (lane >> 3);
-    const int cl = (lane & 7) ^ ((rl >> 1) & 7);
-    const unsigned off = (unsigned)(rl * ld * 2 + cl * 16);
     // stages k0 .. k0 + nk - 1 of the chunk's np / 32 (np is a multiple of 256: np / 32 divides by split)
     const int nk = partial ? np / 32 / split : np / 32;
     const int k0 = partial ? (item % split) * nk : 0;
+
+    // tables: copy i (0 .. 7) of a stage: tile rows 64 i + 8 wave .. + 8 (A for i < 4, B after); lane: row
+    // lane / 8 of the copy, LDS slot lane % 8 holds the line's chunk (lane % 8) ^ ((row >> 1) & 7)
+    const int rl = 8 * wave + (lane >> 3);
+    const int cl = (lane & 7) ^ ((rl >> 1) & 7);
+    const unsigned off = (unsigned)(rl * ld * 2 + cl * 16);
     auto issue = [&](int ks) {  // stage k0 + ks into buffer ks % 2
         const unsigned st = lbase + (ks & 1) * kUgStage + wave * 1024;
 #pragma unroll
@@ -220,13 +249,119 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
             lds_dma16_at(src, off, st + i * 8192);
         }
     };
-    // fragment rows wn0 + 32 fb + j (A) and 256 + wm0 + 32 tb + j (B) share the swizzle of row j; chunk
+
+    // buffer: wave w copies and splits directions 4 w + i (i = 0 .. 3) of each stage. The offsets and weights
+    // are read through the scalar cache (address space 4: this kernel writes neither).
+    typedef const __attribute__((address_space(4))) int64_t *c_i64p;
+    typedef const __attribute__((address_space(4))) float *c_f32p;
+    const c_i64p offs = (c_i64p)s.offsets[p];
+    const c_f32p wts = (c_f32p)raw.weight;
+    const int64_t side0 = (int64_t)ot * kTile, side1 = (int64_t)rows + ct * kTile;  // first slice element per side
+    // a side of a direction (256 rows, 1 KiB) in one copy of 16 B per lane (lane l: rows 4 l .. + 4)
+    auto issue_raw = [&](int ks) {
+        const unsigned st = lbase + (ks & 1) * kUgRawStage;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int dl = 4 * wave + i;
+            const int64_t k = (int64_t)(k0 + ks) * 32 + dl;
+            const bool valid = k < raw.n;
+            const int64_t o = valid ? offs[raw.d0 + k] : 0;
+            // fast: the tile's rows of this slice lie in the buffer. Otherwise (a slice that leaves the buffer, whose
+            // elements become NaN when split, or a padding direction) 4 B copies with every lane's element clamped
+            // into the buffer
+            if (valid && o + side0 >= 0 && o + side1 + kTile <= raw.numel) {
+                lds_dma16_at(raw.buf + o + side0, (unsigned)(16 * lane), st + dl * kUgDir);
+                lds_dma16_at(raw.buf + o + side1, (unsigned)(16 * lane), st + dl * kUgDir + 1024);
+            } else {
+#pragma unroll
+                for (int side = 0; side < 2; ++side)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        int64_t L = valid ? o + (side ? side1 : side0) + 64 * q + lane : 0;
+                        L = L < 0 ? 0 : (L < raw.numel ? L : raw.numel - 1);
+                        lds_dma4_at(raw.buf, (unsigned)(4 * L), st + dl * kUgDir + side * 1024 + 256 * q);
+                    }
+            }
+        }
+    };
+    // split stage ks (buffer ks % 2) in place: lane l takes side l / 32, rows 64 q + 8 c .. + 8 (q = (l / 8) % 4,
+    // c = l % 8) of each of the wave's 4 directions
+    auto split_raw = [&](int ks) {
+        char *st = lds + (ks & 1) * kUgRawStage;
+        const int side = lane >> 5, q = (lane >> 3) & 3, cp = lane & 7;
+        // the two 16 B halves (rows + 0 .. 3, + 4 .. 7) in the order h, 1 - h with h = bit 3 of the lane: each
+        // 16-lane pass then covers every bank once
+        const int h0 = (lane >> 3) & 1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int dl = 4 * wave + i, sb = (i >> 1) & 1;
+            const int64_t k = (int64_t)(k0 + ks) * 32 + dl;
+            const bool valid = k < raw.n;
+            char *c = st + dl * kUgDir + side * 1024 + 256 * q + 32 * cp;
+            float4 v4[2] = {*reinterpret_cast<const float4 *>(c + 16 * h0),
+                            *reinterpret_cast<const float4 *>(c + 16 * (1 - h0))};
+            float w = 0.0f;
+            if (valid) {
+                const int64_t o = offs[raw.d0 + k];
+                w = side ? 1.0f : wts[raw.d0 + k] * raw.scale;  // a rows: weight * scale; b rows: 1
+                if (!(o + side0 >= 0 && o + side1 + kTile <= raw.numel)) {
+                    // (wave-uniform, rare) the slice leaves the buffer: its elements outside read as NaN
+                    const int64_t L = o + (side ? side1 : side0) + 64 * q + 8 * cp;  // the first of the 8 rows
+#pragma unroll
+                    for (int t = 0; t < 2; ++t) {
+                        const int64_t Lh = L + 4 * (t ? 1 - h0 : h0);
+                        float *f = reinterpret_cast<float *>(&v4[t]);
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) f[e] = (Lh + e >= 0 && Lh + e < raw.numel) ? f[e] : __builtin_nanf("");
+                    }
+                }
+            } else {
+                // (wave-uniform) a padding direction: zero
+                v4[0] = v4[1] = float4{0.f, 0.f, 0.f, 0.f};
+                w = 1.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                // v rounded to fp32 first, then lo = v - hi exactly (no fused multiply-subtract), as the tables
+#pragma clang fp contract(off)
+                const int hh = t ? 1 - h0 : h0;
+                const float v[4] = {v4[t].x * w, v4[t].y * w, v4[t].z * w, v4[t].w * w};
+                bf16x4 hi, lo;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    hi[e] = (__bf16)v[e];
+                    lo[e] = (__bf16)(v[e] - (float)hi[e]);
+                }
+                *reinterpret_cast<bf16x4 *>(c + 16 * sb + 8 * hh) = hi;
+                *reinterpret_cast<bf16x4 *>(c + 16 * (1 - sb) + 8 * hh) = lo;
+            }
+        }
+    };
+
+    // tables: fragment rows wn0 + 32 fb + j (A) and 256 + wm0 + 32 tb + j (B) share the swizzle of row j; chunk
     // 2 s + hf is the hi half of directions 16 s + 8 hf .. + 8, chunk 4 + 2 s + hf its lo half
     int fo[2][2];
 #pragma unroll
     for (int sk = 0; sk < 2; ++sk)
 #pragma unroll
         for (int h = 0; h < 2; ++h) fo[sk][h] = j * 128 + (((4 * h + 2 * sk + hf) ^ ((j >> 1) & 7)) << 4);
+    // buffer: lane 16 G + i addresses direction 8 (G / 2) + i / 4 (+ 16 sk + 4 e) and rows 16 (G % 2) + 4 (i % 4)
+    // .. + 4 of a 32-row block; bit 1 of that direction (bit 3 of i) swaps hi and lo. tro[lo]
+    int tro[2];
+    {
+        const int G = lane >> 4, i = lane & 15;
+        const int grp = 2 * (G & 1) + ((i & 3) >> 1);  // row group within the block (0 .. 3)
+#pragma unroll
+        for (int lo = 0; lo < 2; ++lo)
+            tro[lo] = (8 * (G >> 1) + (i >> 2)) * kUgDir + 32 * grp + 16 * (((i >> 3) & 1) ^ lo) + 8 * (i & 1);
+    }
+    // 32 rows from row R (a multiple of 32 within the side), directions 16 sk + 8 hf + 0 .. 7
+    auto tr_frag = [&](const char *st, int side, int R, int sk, int lo) {
+        const char *b = st + tro[lo] + side * 1024 + 4 * R + 16 * sk * kUgDir;
+        const bf16x4 x = lds_read_tr16(b), y = lds_read_tr16(b + 4 * kUgDir);
+        return __builtin_shufflevector(x, y, 0, 1, 2, 3, 4, 5, 6, 7);
+    };
+
     f32x16 acc[4][2];
 #pragma unroll
     for (int fb = 0; fb < 4; ++fb)
@@ -235,15 +370,28 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
     // fragments of 16 directions, double buffered: those of the next step are read while this step's run
     bf16x8 ah[2][4], al[2][4], bh[2][2], bl[2][2];
     auto fetch = [&](int buf, const char *st, int sk) {
+        if constexpr (RAW) {
 #pragma unroll
-        for (int fb = 0; fb < 4; ++fb) {
-            ah[buf][fb] = *reinterpret_cast<const bf16x8 *>(st + (wn0 + 32 * fb) * 128 + fo[sk][0]);
-            al[buf][fb] = *reinterpret_cast<const bf16x8 *>(st + (wn0 + 32 * fb) * 128 + fo[sk][1]);
-        }
+            for (int fb = 0; fb < 4; ++fb) {
+                ah[buf][fb] = tr_frag(st, 0, wn0 + 32 * fb, sk, 0);
+                al[buf][fb] = tr_frag(st, 0, wn0 + 32 * fb, sk, 1);
+            }
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            bh[buf][tb] = *reinterpret_cast<const bf16x8 *>(st + (256 + wm0 + 32 * tb) * 128 + fo[sk][0]);
-            bl[buf][tb] = *reinterpret_cast<const bf16x8 *>(st + (256 + wm0 + 32 * tb) * 128 + fo[sk][1]);
+            for (int tb = 0; tb < 2; ++tb) {
+                bh[buf][tb] = tr_frag(st, 1, wm0 + 32 * tb, sk, 0);
+                bl[buf][tb] = tr_frag(st, 1, wm0 + 32 * tb, sk, 1);
+            }
+        } else {
+#pragma unroll
+            for (int fb = 0; fb < 4; ++fb) {
+                ah[buf][fb] = *reinterpret_cast<const bf16x8 *>(st + (wn0 + 32 * fb) * 128 + fo[sk][0]);
+                al[buf][fb] = *reinterpret_cast<const bf16x8 *>(st + (wn0 + 32 * fb) * 128 + fo[sk][1]);
+            }
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb) {
+                bh[buf][tb] = *reinterpret_cast<const bf16x8 *>(st + (256 + wm0 + 32 * tb) * 128 + fo[sk][0]);
+                bl[buf][tb] = *reinterpret_cast<const bf16x8 *>(st + (256 + wm0 + 32 * tb) * 128 + fo[sk][1]);
+            }
         }
     };
     // the three products as three passes over the 8 accumulators: dependent products 8 apart
@@ -257,25 +405,50 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
                     acc[fb][tb] = mfma32x32x16(pr == 2 ? al[buf][fb] : ah[buf][fb], pr == 1 ? bl[buf][tb] : bh[buf][tb],
                                                acc[fb][tb]);
     };
-    issue(0);
-    if (nk > 1) issue(1);
-    vm_wait_groups<8, 1>(nk > 1 ? 1 : 0);
-    __syncthreads();
+    if constexpr (RAW) {
+        // (a direction's copies number 2 or 8, so stage 0 lands and is split before stage 1 is issued: every
+        // later wait is for all copies in flight)
+        issue_raw(0);
+        vm_wait<0>();
+        asm volatile("" ::: "memory");
+        split_raw(0);
+        __syncthreads();
+        if (nk > 1) issue_raw(1);
+    } else {
+        issue(0);
+        if (nk > 1) issue(1);
+        vm_wait_groups<8, 1>(nk > 1 ? 1 : 0);
+        __syncthreads();
+    }
     fetch(0, lds, 0);
 #pragma unroll 1
     for (int ks = 0; ks < nk; ++ks) {
-        const char *st = lds + (ks & 1) * kUgStage;
+        const char *st = lds + (ks & 1) * kSt;
         fetch(1, st, 1);
         products(0);
-        if (ks + 1 < nk) {
-            // stage ks + 1 landed for every wave (nothing was issued after it); every wave has read its
-            // fragments of stage ks, whose buffer takes stage ks + 2
-            vm_wait<0>();
-            __syncthreads();
-            if (ks + 2 < nk) issue(ks + 2);
-            fetch(0, lds + ((ks + 1) & 1) * kUgStage, 0);
+        if constexpr (RAW) {
+            // buffer: this wave splits its part of stage ks + 1 once its copies landed (nothing was issued after
+            // them), under the tail of this stage's products and with no fragments held
+            products(1);
+            if (ks + 1 < nk) {
+                vm_wait<0>();
+                asm volatile("" ::: "memory");
+                split_raw(ks + 1);
+                __syncthreads();  // stage ks + 1 split; every wave has read its fragments of stage ks
+                if (ks + 2 < nk) issue_raw(ks + 2);
+                fetch(0, lds + ((ks + 1) & 1) * kSt, 0);
+            }
+        } else {
+            if (ks + 1 < nk) {
+                // stage ks + 1 landed (nothing was issued after it); every wave has read its fragments of stage
+                // ks, whose buffer takes stage ks + 2
+                vm_wait<0>();
+                __syncthreads();
+                if (ks + 2 < nk) issue(ks + 2);
+                fetch(0, lds + ((ks + 1) & 1) * kUgStage, 0);
+            }
+            products(1);
         }
-        products(1);
     }
     // lane (j, hf), register 4 g + e of block (fb, tb): row o = wn0 + 32 fb + 8 g + 4 hf + e, column
     // i = wm0 + 32 tb + j; the 32 lanes of a half-wave write 128 contiguous bytes of one row (a partial tile:
@@ -498,20 +671,29 @@ extern "C" int noise_update_gradients(const noise_update_param_t *params, int np
         if (st) return st;
     }
     if (big.n) {
+        // with a buffer of at most 2^30 elements the GEMM reads the slices itself; otherwise tables first
+        const bool direct = buffer != nullptr && numel <= (1ll << 30);
         for (int64_t d0 = 0; d0 < pairs; d0 += np) {
             const int64_t n = pairs - d0 < np ? pairs - d0 : np;
-            if (buffer)
-                hipLaunchKernelGGL(update_tables_from_buffer_kernel, dim3((unsigned)(rows_total / 256),
-                                   (unsigned)(np / kTabK)), dim3(256), 0, s, big, d0, n, np, weight, scale, buffer,
-                                   numel);
-            else
-                hipLaunchKernelGGL(update_tables_kernel, dim3((unsigned)rows_total, (unsigned)(np / 256)), dim3(256),
-                                   0, s, big, d0, n, np, weight, scale, dl, numel);
-            int st = launch_status("noise_update_gradients (tables)");
-            if (st) return st;
             const int64_t wgs = full + (tiles_total - full) * split;
-            hipLaunchKernelGGL(update_gemm_kernel, dim3((unsigned)wgs), dim3(512), 0, s, big, (int)np, d0 > 0 ? 1 : 0,
-                               (int)full, split, part);
+            int st;
+            if (direct) {
+                const UpdateRaw raw{d0, n, weight, scale, buffer, numel};
+                hipLaunchKernelGGL(update_gemm_kernel<true>, dim3((unsigned)wgs), dim3(512), 0, s, big, (int)np,
+                                   d0 > 0 ? 1 : 0, (int)full, split, part, raw);
+            } else {
+                if (buffer)
+                    hipLaunchKernelGGL(update_tables_from_buffer_kernel, dim3((unsigned)(rows_total / 256),
+                                       (unsigned)(np / kTabK)), dim3(256), 0, s, big, d0, n, np, weight, scale, buffer,
+                                       numel);
+                else
+                    hipLaunchKernelGGL(update_tables_kernel, dim3((unsigned)rows_total, (unsigned)(np / 256)),
+                                       dim3(256), 0, s, big, d0, n, np, weight, scale, dl, numel);
+                st = launch_status("noise_update_gradients (tables)");
+                if (st) return st;
+                hipLaunchKernelGGL(update_gemm_kernel<false>, dim3((unsigned)wgs), dim3(512), 0, s, big, (int)np,
+                                   d0 > 0 ? 1 : 0, (int)full, split, part, UpdateRaw{});
+            }
             st = launch_status("noise_update_gradients (gemm)");
             if (st) return st;
             if (split > 1) {

@@ -164,6 +164,31 @@ def test_materialised_buffer_gives_the_same_gradients():
         assert torch.equal(g_regen[n], g_buf[n]), n
 
 
+def test_slices_leaving_the_draw_give_nan_rows_and_columns():
+    # an element of a slice outside the draw reads as NaN: a slice starting before it makes the first rows of
+    # that matrix's gradient NaN, one running past its end the last columns. The GEMM reading the materialised
+    # draw and the regenerating path mark the same entries and agree bitwise on the others (the second slice
+    # lies in the second chunk of directions; the third chunk is padded)
+    from noise_amd.eggroll import Eggroll
+    es = Eggroll(_Params().cuda(), 600, noise_numel=1 << 22)
+    offsets = {n: o.clone() for n, o in es.offsets(9).items()}
+    numel = es.noise_numel
+    offsets['q'][0] = -100                   # a[0 .. 99] before the draw
+    offsets['fc'][300] = numel - 2048 - 200  # a inside, b[200 ..] past the end
+    losses = _losses(1200, seed=5)
+    g_regen = es.update(losses, offsets, chunk=256, materialise=False)
+    g_buf = es.update(losses, offsets, chunk=256, materialise=True)
+    for n in g_regen:
+        a, b = g_regen[n], g_buf[n]
+        assert torch.equal(torch.isnan(a), torch.isnan(b)), n
+        assert torch.equal(torch.nan_to_num(a, nan=0.0), torch.nan_to_num(b, nan=0.0)), n
+    q, fc = g_buf['q'], g_buf['fc']
+    assert torch.isnan(q[:100]).all() and torch.isfinite(q[100:]).all()
+    assert torch.isnan(fc[:, 200:]).all() and torch.isfinite(fc[:, :200]).all()
+    for n in ('proj', 'gate', 'lam'):
+        assert torch.isfinite(g_buf[n]).all(), n
+
+
 def test_workspace_without_partial_tiles_gives_the_same_gradients(monkeypatch):
     # a workspace that holds only the tables: the GEMM then runs whole tiles over every direction instead of
     # splitting the last round's tiles into partial tiles summed in order. The same products, summed in another
