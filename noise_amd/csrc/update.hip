@@ -257,27 +257,40 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
     const c_i64p offs = (c_i64p)s.offsets[p];
     const c_f32p wts = (c_f32p)raw.weight;
     const int64_t side0 = (int64_t)ot * kTile, side1 = (int64_t)rows + ct * kTile;  // first slice element per side
-    // a side of a direction (256 rows, 1 KiB) in one copy of 16 B per lane (lane l: rows 4 l .. + 4)
+    // a side of a direction (256 rows, 1 KiB) in one copy of 16 B per lane (lane l: rows 4 l .. + 4). The split
+    // of a stage follows its copies' issue with no other issue between (issue 0, split 0, issue 1, ...; split
+    // ks + 1 then issue ks + 2), so each direction's offset, scaled weight and kind pass from one to the other
+    // in wave-uniform registers. kind: 0 padding, 1 inside the buffer, 2 leaving it (elements outside: NaN)
+    int64_t d_off[4];
+    float d_w[4];
+    int d_kind[4];
     auto issue_raw = [&](int ks) {
         const unsigned st = lbase + (ks & 1) * kUgRawStage;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int dl = 4 * wave + i;
             const int64_t k = (int64_t)(k0 + ks) * 32 + dl;
-            const bool valid = k < raw.n;
-            const int64_t o = valid ? offs[raw.d0 + k] : 0;
-            // fast: the tile's rows of this slice lie in the buffer. Otherwise (a slice that leaves the buffer, whose
-            // elements become NaN when split, or a padding direction) 4 B copies with every lane's element clamped
-            // into the buffer
-            if (valid && o + side0 >= 0 && o + side1 + kTile <= raw.numel) {
+            int64_t o = 0;
+            int kind = 0;
+            float w = 0.0f;
+            if (k < raw.n) {
+                o = offs[raw.d0 + k];
+                w = wts[raw.d0 + k] * raw.scale;
+                kind = o + side0 >= 0 && o + side1 + kTile <= raw.numel ? 1 : 2;
+            }
+            d_off[i] = o;
+            d_w[i] = w;
+            d_kind[i] = kind;
+            if (kind == 1) {
                 lds_dma16_at(raw.buf + o + side0, (unsigned)(16 * lane), st + dl * kUgDir);
                 lds_dma16_at(raw.buf + o + side1, (unsigned)(16 * lane), st + dl * kUgDir + 1024);
             } else {
+                // 4 B copies with every lane's element clamped into the buffer (a padding direction reads row 0)
 #pragma unroll
                 for (int side = 0; side < 2; ++side)
 #pragma unroll
                     for (int q = 0; q < 4; ++q) {
-                        int64_t L = valid ? o + (side ? side1 : side0) + 64 * q + lane : 0;
+                        int64_t L = kind ? o + (side ? side1 : side0) + 64 * q + lane : 0;
                         L = L < 0 ? 0 : (L < raw.numel ? L : raw.numel - 1);
                         lds_dma4_at(raw.buf, (unsigned)(4 * L), st + dl * kUgDir + side * 1024 + 256 * q);
                     }
@@ -295,30 +308,22 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int dl = 4 * wave + i, sb = (i >> 1) & 1;
-            const int64_t k = (int64_t)(k0 + ks) * 32 + dl;
-            const bool valid = k < raw.n;
             char *c = st + dl * kUgDir + side * 1024 + 256 * q + 32 * cp;
             float4 v4[2] = {*reinterpret_cast<const float4 *>(c + 16 * h0),
                             *reinterpret_cast<const float4 *>(c + 16 * (1 - h0))};
-            float w = 0.0f;
-            if (valid) {
-                const int64_t o = offs[raw.d0 + k];
-                w = side ? 1.0f : wts[raw.d0 + k] * raw.scale;  // a rows: weight * scale; b rows: 1
-                if (!(o + side0 >= 0 && o + side1 + kTile <= raw.numel)) {
-                    // (wave-uniform, rare) the slice leaves the buffer: its elements outside read as NaN
-                    const int64_t L = o + (side ? side1 : side0) + 64 * q + 8 * cp;  // the first of the 8 rows
-#pragma unroll
-                    for (int t = 0; t < 2; ++t) {
-                        const int64_t Lh = L + 4 * (t ? 1 - h0 : h0);
-                        float *f = reinterpret_cast<float *>(&v4[t]);
-#pragma unroll
-                        for (int e = 0; e < 4; ++e) f[e] = (Lh + e >= 0 && Lh + e < raw.numel) ? f[e] : __builtin_nanf("");
-                    }
-                }
-            } else {
-                // (wave-uniform) a padding direction: zero
+            // a rows: weight * scale; b rows: 1 (a padding direction: zeros times 1)
+            const float w = side && d_kind[i] ? 1.0f : d_w[i];
+            if (d_kind[i] == 0) {
                 v4[0] = v4[1] = float4{0.f, 0.f, 0.f, 0.f};
-                w = 1.0f;
+            } else if (d_kind[i] == 2) {
+                const int64_t L = d_off[i] + (side ? side1 : side0) + 64 * q + 8 * cp;  // the first of the 8 rows
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    const int64_t Lh = L + 4 * (t ? 1 - h0 : h0);
+                    float *f = reinterpret_cast<float *>(&v4[t]);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) f[e] = (Lh + e >= 0 && Lh + e < raw.numel) ? f[e] : __builtin_nanf("");
+                }
             }
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
