@@ -489,9 +489,12 @@ int64_t noise_update_workspace_bytes(const noise_update_param_t *params, int npa
  * grad = scale * sum_d weight[d] a_d for 1-D parameters. The reference's p.grad is scale = -1/len(fitness).
  * Parameters with both sides multiples of 256 run as split-bf16x3 MFMA GEMMs over chunks of `chunk`
  * directions (rounded up to 256), accumulated in order; others (<= 65536 entries) are summed directly.
- * The matrices' slices are regenerated from the Philox counter in-kernel, or, when `buffer` is non-NULL,
- * read from that materialised draw (fp32 [numel], noise_normal_fill of the same draw): cheaper once
- * pairs * sum(rows + cols) exceeds numel, since every buffer element then serves several directions. */
+ * The matrices' slices are regenerated from the Philox counter in-kernel (through the split tables), or, when
+ * `buffer` is non-NULL, read from that materialised draw (fp32 [numel], noise_normal_fill of the same draw):
+ * cheaper once pairs * sum(rows + cols) exceeds numel, since every buffer element then serves several
+ * directions. With a buffer of at most 2^30 elements the GEMM copies the slices straight from it and splits
+ * them itself (the workspace's table area is then unused; the results are the same bits). An element of a
+ * slice outside [0, numel) reads as NaN. */
 int noise_update_gradients(const noise_update_param_t *params, int nparams, int64_t pairs, const float *weight,
                            float scale, int64_t chunk, int64_t numel, uint64_t seed, uint64_t offset,
                            int64_t threads, const float *buffer, void *workspace, int64_t workspace_bytes,

@@ -309,36 +309,46 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
         for (int i = 0; i < 4; ++i) {
             const int dl = 4 * wave + i, sb = (i >> 1) & 1;
             char *c = st + dl * kUgDir + side * 1024 + 256 * q + 32 * cp;
-            float4 v4[2] = {*reinterpret_cast<const float4 *>(c + 16 * h0),
-                            *reinterpret_cast<const float4 *>(c + 16 * (1 - h0))};
-            // a rows: weight * scale; b rows: 1 (a padding direction: zeros times 1)
-            const float w = side && d_kind[i] ? 1.0f : d_w[i];
-            if (d_kind[i] == 0) {
-                v4[0] = v4[1] = float4{0.f, 0.f, 0.f, 0.f};
-            } else if (d_kind[i] == 2) {
+            const float4 v4[2] = {*reinterpret_cast<const float4 *>(c + 16 * h0),
+                                  *reinterpret_cast<const float4 *>(c + 16 * (1 - h0))};
+            // a rows: weight * scale; b rows: 1. Each case converts on its own, so that the common one (kind 1)
+            // keeps its loaded registers (a merge after the rare cases' rewrites would copy them)
+            const float w = side ? 1.0f : d_w[i];
+            auto convert = [&](const float4 (&x)[2], float wx) {
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    // v rounded to fp32 first, then lo = v - hi exactly (no fused multiply-subtract), as the tables
+#pragma clang fp contract(off)
+                    const int hh = t ? 1 - h0 : h0;
+                    const float v[4] = {x[t].x * wx, x[t].y * wx, x[t].z * wx, x[t].w * wx};
+                    bf16x4 hi, lo;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        hi[e] = (__bf16)v[e];
+                        lo[e] = (__bf16)(v[e] - (float)hi[e]);
+                    }
+                    *reinterpret_cast<bf16x4 *>(c + 16 * sb + 8 * hh) = hi;
+                    *reinterpret_cast<bf16x4 *>(c + 16 * (1 - sb) + 8 * hh) = lo;
+                }
+            };
+            if (d_kind[i] == 1) {
+                convert(v4, w);
+            } else if (d_kind[i] == 0) {
+                // a padding direction: zeros
+                const float4 z[2] = {float4{0.f, 0.f, 0.f, 0.f}, float4{0.f, 0.f, 0.f, 0.f}};
+                convert(z, 1.0f);
+            } else {
+                // the slice leaves the buffer: its elements outside read as NaN
                 const int64_t L = d_off[i] + (side ? side1 : side0) + 64 * q + 8 * cp;  // the first of the 8 rows
+                float4 y[2] = {v4[0], v4[1]};
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     const int64_t Lh = L + 4 * (t ? 1 - h0 : h0);
-                    float *f = reinterpret_cast<float *>(&v4[t]);
+                    float *f = reinterpret_cast<float *>(&y[t]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) f[e] = (Lh + e >= 0 && Lh + e < raw.numel) ? f[e] : __builtin_nanf("");
                 }
-            }
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                // v rounded to fp32 first, then lo = v - hi exactly (no fused multiply-subtract), as the tables
-#pragma clang fp contract(off)
-                const int hh = t ? 1 - h0 : h0;
-                const float v[4] = {v4[t].x * w, v4[t].y * w, v4[t].z * w, v4[t].w * w};
-                bf16x4 hi, lo;
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    hi[e] = (__bf16)v[e];
-                    lo[e] = (__bf16)(v[e] - (float)hi[e]);
-                }
-                *reinterpret_cast<bf16x4 *>(c + 16 * sb + 8 * hh) = hi;
-                *reinterpret_cast<bf16x4 *>(c + 16 * (1 - sb) + 8 * hh) = lo;
+                convert(y, w);
             }
         }
     };
