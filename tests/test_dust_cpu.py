@@ -292,3 +292,31 @@ def test_rerun_bf16_flow_reduces_to_the_fp32_rerun(monkeypatch):
     out = odust.block_forward_bf16_flow(cache['blocks'][6].bfloat16().float(), odust.block_weights(P, 6), None, cos,
                                         sin, window_sizes()[6])
     assert torch.equal(out, out.bfloat16().float())
+
+
+def test_rerun_batch_rows_are_cached_per_capture():
+    # the tensors rerun derives from the captured batch (ids and targets repeated per draw, rotary tables, x0
+    # repeated per draw) are built once per capture and n, and rebuilt when a source tensor is replaced or
+    # changed in place, or n changes
+    import torch
+    from types import SimpleNamespace
+    from noise_amd import dust as ndust
+    T, b = 16, 2
+    g = torch.Generator().manual_seed(0)
+    model = SimpleNamespace(cos=torch.randn(1, 64, 1, 32, generator=g), sin=torch.randn(1, 64, 1, 32, generator=g))
+    state = SimpleNamespace(model=model, length=T, x=torch.randint(0, 99, (b, T), generator=g),
+                            y=torch.randint(0, 99, (b, T), generator=g), x0=torch.randn(b, T, 512, generator=g))
+    r1 = ndust._batch_rows(state, 3, True)
+    assert torch.equal(r1['idx'], state.x.repeat(3, 1)) and torch.equal(r1['targets'], state.y.repeat(3, 1))
+    assert torch.equal(r1['x0'], state.x0.repeat(3, 1, 1))
+    assert r1['rope'][0].shape == (T, 32) and r1['rope'][0].dtype == torch.bfloat16
+    assert ndust._batch_rows(state, 3, True) is r1
+    state.x0.mul_(2)  # in place: the version moves
+    r2 = ndust._batch_rows(state, 3, True)
+    assert r2 is not r1 and torch.equal(r2['x0'], state.x0.repeat(3, 1, 1))
+    state.y = state.y.clone()  # another tensor with the same values
+    r3 = ndust._batch_rows(state, 3, True)
+    assert r3 is not r2
+    r4 = ndust._batch_rows(state, 4, True)
+    assert r4 is not r3 and r4['idx'].shape == (4 * b, T)
+    assert ndust._batch_rows(state, 4, False)['x0'] is None
