@@ -257,7 +257,8 @@ __global__ __launch_bounds__(512) void update_gemm_kernel(UpdateSet s, int np, i
     const c_i64p offs = (c_i64p)s.offsets[p];
     const c_f32p wts = (c_f32p)raw.weight;
     const int64_t side0 = (int64_t)ot * kTile, side1 = (int64_t)rows + ct * kTile;  // first slice element per side
-    // a side of a direction (256 rows, 1 KiB) in one copy of 16 B per lane (lane l: rows 4 l .. + 4). The split
+    // a side of a direction (256 rows, 1 KiB) in one copy of 16 B per lane (lane l: rows 4 l .. + 4; a slice may
+    // start at any element, so a lane's 16 B are 4 B aligned, which multi-dword global loads accept). The split
     // of a stage follows its copies' issue with no other issue between (issue 0, split 0, issue 1, ...; split
     // ks + 1 then issue ks + 2), so each direction's offset, scaled weight and kind pass from one to the other
     // in wave-uniform registers. kind: 0 padding, 1 inside the buffer, 2 leaving it (elements outside: NaN)
